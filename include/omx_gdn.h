@@ -1,0 +1,146 @@
+/*
+ * omx_gdn.h -- C ABI of the MI355X (gfx950) GatedDeltaNet library (libomx_gdn.so).
+ *
+ * Drop-in boundary for omegalax's Qwen3.5 gated-delta-rule path
+ * (omegalax/models/qwen3_5/deltanet.py).  Every entry point takes raw device
+ * pointers, sizes and a HIP stream (hipStream_t passed as void*; NULL = the
+ * null stream), enqueues its kernels on that stream and returns without
+ * synchronising.  The library never allocates device memory in these calls:
+ * callers pass any scratch as `workspace` (size from the *_workspace_size
+ * query).  Buffers are dense, row-major, in the layouts given per argument.
+ *
+ * Return value: OMX_GDN_OK (0) or a negative code; omx_gdn_last_error() then
+ * returns a message for the calling thread.  Arguments are validated on the
+ * host before any HIP call, so a bad call returns OMX_GDN_EINVAL without
+ * touching the GPU.
+ *
+ * dtype codes: OMX_GDN_F32 (float32) or OMX_GDN_BF16 (bfloat16 as uint16 bits).
+ * Shapes: B batch, T tokens, Hk key heads, Hv value heads (Hv % Hk == 0; value
+ * head h reads key head h / (Hv/Hk), the repeat-interleave of
+ * deltanet.py:272-280), dk/dv head dims, K conv taps, conv_dim = 2*Hk*dk + Hv*dv.
+ */
+#ifndef OMX_GDN_H
+#define OMX_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OMX_GDN_OK 0
+#define OMX_GDN_EINVAL (-1)      /* bad shape, dtype, pointer or attribute */
+#define OMX_GDN_EUNSUPPORTED (-2) /* valid request outside the compiled shapes */
+#define OMX_GDN_ELAUNCH (-3)      /* a HIP launch failed */
+
+#define OMX_GDN_F32 0
+#define OMX_GDN_BF16 1
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* omx_gdn_last_error(void);
+
+/* Library ABI version (major * 100 + minor). */
+int omx_gdn_abi_version(void);
+
+/*
+ * Chunked gated delta rule, the core of the prefill.
+ * Replaces chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH,
+ * chunk_size=64) -> o_BTHU (deltanet.py:53-153), whose only caller is
+ * _full_deltanet (deltanet.py:281).  Adds the semantics of transformers'
+ * torch_chunk_gated_delta_rule: initial_state, final state and packed sequences.
+ *
+ *   q, k         [B, T, Hk, dk]  in_dtype (bf16 or f32); L2-normalised in the kernel
+ *                                when qk_l2norm != 0 (deltanet.py:65-66), at the input
+ *                                precision, then scaled by `scale` (deltanet.py:84-85)
+ *   v            [B, T, Hv, dv]  in_dtype
+ *   g            [B, T, Hv] f32  log decay (<= 0)
+ *   beta         [B, T, Hv] f32
+ *   initial_state [N, Hv, dk, dv] f32 or NULL (zeros, deltanet.py:118)
+ *   cu_seqlens   int32 [N+1] device array or NULL.  When given, B must be 1 and
+ *                sequence n spans tokens [cu[n], cu[n+1]); each sequence starts from
+ *                its own initial state and chunks restart at its first token.
+ *                Without it N = B.
+ *   o            [B, T, Hv, dv] f32 (the reference returns fp32, deltanet.py:153)
+ *   final_state  [N, Hv, dk, dv] f32 or NULL (the reference discards it, :146)
+ *   chunk_size   must be 64.
+ */
+int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
+                      const float* g, const float* beta, const float* initial_state,
+                      const int32_t* cu_seqlens, int64_t N, float* o, float* final_state,
+                      int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                      int64_t chunk_size, float scale, int qk_l2norm, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                                        int64_t dk, int64_t dv, int64_t N);
+
+/*
+ * GatedDeltaNet prefill from the projection outputs to the gated-norm output.
+ * Replaces the middle of GatedDeltaNet.__call__ (deltanet.py:243-293): causal
+ * depthwise conv1d + SiLU (:243), gates beta = sigmoid(b), g = -exp(A_log) *
+ * softplus(a + dt_bias) (:248-250), the split/GQA/L2-norm/chunked rule of
+ * _full_deltanet (:261-281) and the inline gated RMSNorm (:282-293).  The
+ * projections (:234-241) and out_proj (:305) stay with the caller.
+ *
+ *   mixed_qkv     [B, T, conv_dim] bf16  (in_proj_qkv output, token-major)
+ *   z             [B, T, Hv, dv] bf16
+ *   a, b          [B, T, Hv] bf16
+ *   conv_w        [conv_dim, K] f32 (cast to bf16 as at deltanet.py:243)
+ *   A_log, dt_bias [Hv] f32;  norm_w [dv] f32;  eps (rms_norm_eps)
+ *   cu_seqlens    as for omx_gdn_chunk_fwd (conv history also restarts per sequence)
+ *   initial_state / final_state  [N, Hv, dk, dv] f32 or NULL
+ *   conv_state_in  [N, conv_dim, K-1] bf16 or NULL: raw inputs preceding each
+ *                  sequence (oldest first); NULL = zeros (deltanet.py:46)
+ *   conv_state_out [N, conv_dim, K-1] bf16 or NULL: the last K-1 raw inputs of each
+ *                  sequence (the decode cache after this prefill)
+ *   out           [B, T, Hv*dv] bf16
+ */
+int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                    const float* conv_w, const float* A_log, const float* dt_bias,
+                    const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                    const float* initial_state, float* final_state, const void* conv_state_in,
+                    void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                    int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                      int64_t dv, int64_t N);
+
+/*
+ * One cached decode step for one token per sequence: conv-cache update + SiLU,
+ * gates, q/k L2-norm, recurrent rule, gated RMSNorm.  No reference counterpart:
+ * omegalax drops the cache for Qwen3.5 (model.py:324-326) and its decode API
+ * raises (text/api.py:128-131).  Semantics follow transformers'
+ * causal_conv1d_update and torch_recurrent_gated_delta_rule, with the
+ * reference's fp32 gated norm (deltanet.py:282-293).
+ *
+ *   mixed_qkv  [B, conv_dim] bf16;  z [B, Hv, dv] bf16;  a, b [B, Hv] bf16
+ *   conv_state [B, conv_dim, K-1] bf16, updated in place (oldest tap first)
+ *   state      [B, Hv, dk, dv] f32, updated in place
+ *   out        [B, Hv*dv] bf16
+ */
+int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                        const float* conv_w, const float* A_log, const float* dt_bias,
+                        const float* norm_w, float eps, void* conv_state, float* state,
+                        void* out, int64_t B, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                        int64_t K, void* stream);
+
+/*
+ * One token of the recurrent rule on post-conv inputs (core level).  Semantics of
+ * transformers' torch_recurrent_gated_delta_rule with use_qk_l2norm_in_kernel=True
+ * and T=1; equals omx_gdn_chunk_fwd on a one-token sequence.
+ *
+ *   q, k [B, Hk, dk], v [B, Hv, dv] in_dtype;  g, beta [B, Hv] f32
+ *   state [B, Hv, dk, dv] f32 in place;  o [B, Hv, dv] f32
+ */
+int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_dtype,
+                           const float* g, const float* beta, float* state, float* o, int64_t B,
+                           int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, float scale,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OMX_GDN_H */

@@ -1,0 +1,151 @@
+// C ABI of libomx_gdn.so: argument validation, workspace planning and launch.
+//
+// Every entry point validates its arguments on the host before the first HIP
+// call, so an invalid request returns OMX_GDN_EINVAL (with a message from
+// omx_gdn_last_error) on any machine, GPU or not.  No C++ exception crosses
+// the ABI and nothing here synchronises the stream.
+#include "../../include/omx_gdn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "gdn_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return OMX_GDN_OK;
+}
+
+int launch_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(OMX_GDN_ELAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+#define REQUIRE(cond, ...) \
+  do {                     \
+    if (!(cond)) return fail(OMX_GDN_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+int check_heads(const char* fn, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv) {
+  REQUIRE(Hk >= 1 && Hv >= 1, "%s: head counts must be positive (Hk=%lld, Hv=%lld)", fn,
+          (long long)Hk, (long long)Hv);
+  REQUIRE(Hv % Hk == 0, "%s: value heads (%lld) must be a multiple of key heads (%lld)", fn,
+          (long long)Hv, (long long)Hk);
+  REQUIRE(Hv <= 4096, "%s: too many value heads (%lld)", fn, (long long)Hv);
+  REQUIRE(dk >= 1 && dv >= 1, "%s: head dims must be positive (dk=%lld, dv=%lld)", fn,
+          (long long)dk, (long long)dv);
+  return OMX_GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* omx_gdn_last_error(void) { return g_last_error.c_str(); }
+
+int omx_gdn_abi_version(void) { return 100; }
+
+int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                        const float* conv_w, const float* A_log, const float* dt_bias,
+                        const float* norm_w, float eps, void* conv_state, float* state,
+                        void* out, int64_t B, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                        int64_t K, void* stream) {
+  const char* fn = "omx_gdn_decode_step";
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(B >= 0 && B <= 65535, "%s: batch %lld out of range [0, 65535]", fn, (long long)B);
+  REQUIRE(K >= 2 && K <= 8, "%s: conv kernel size %lld not in [2, 8]", fn, (long long)K);
+  REQUIRE(eps >= 0.f && eps < 1.f, "%s: eps %g out of range", fn, (double)eps);
+  if (!omx::decode_dims_supported((int)dk, (int)dv))
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled (16/32/64/128)",
+                fn, (long long)dk, (long long)dv);
+  if (Hv / Hk > omx::decode_max_gqa())
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: gqa factor %lld above %d", fn, (long long)(Hv / Hk),
+                omx::decode_max_gqa());
+  if (B == 0) return ok();
+  REQUIRE(mixed_qkv && z && a && b && conv_w && A_log && dt_bias && norm_w && conv_state &&
+              state && out,
+          "%s: a required pointer is NULL", fn);
+  REQUIRE(aligned(state, 16), "%s: state must be 16-byte aligned", fn);
+  omx::DecodeParams p{};
+  p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b; p.conv_w = conv_w; p.A_log = A_log;
+  p.dt_bias = dt_bias; p.norm_w = norm_w; p.conv_state = conv_state; p.out = out;
+  p.state = state;
+  p.B = (int)B; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.dv = (int)dv;
+  p.conv_k = (int)K; p.scale = 1.0f / sqrtf((float)dk); p.eps = eps;
+  return launch_status(omx::launch_decode(p, true, true, (hipStream_t)stream), fn);
+}
+
+int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_dtype,
+                           const float* g, const float* beta, float* state, float* o, int64_t B,
+                           int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, float scale,
+                           void* stream) {
+  const char* fn = "omx_gdn_recurrent_step";
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
+          in_dtype);
+  REQUIRE(B >= 0 && B <= 65535, "%s: batch %lld out of range [0, 65535]", fn, (long long)B);
+  if (!omx::decode_dims_supported((int)dk, (int)dv))
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled (16/32/64/128)",
+                fn, (long long)dk, (long long)dv);
+  if (B == 0) return ok();
+  REQUIRE(q && k && v && g && beta && state && o, "%s: a required pointer is NULL", fn);
+  REQUIRE(aligned(state, 16), "%s: state must be 16-byte aligned", fn);
+  omx::DecodeParams p{};
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.o = o; p.state = state;
+  p.B = (int)B; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.dv = (int)dv;
+  p.scale = scale; p.eps = 0.f;
+  return launch_status(
+      omx::launch_decode(p, false, in_dtype == OMX_GDN_BF16, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- prefill (pending)
+extern "C" {
+
+size_t omx_gdn_chunk_fwd_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                        int64_t) {
+  return 0;
+}
+
+int omx_gdn_chunk_fwd(const void*, const void*, const void*, int, const float*, const float*,
+                      const float*, const int32_t*, int64_t, float*, float*, int64_t, int64_t,
+                      int64_t, int64_t, int64_t, int64_t, int64_t, float, int, void*, size_t,
+                      void*) {
+  return fail(OMX_GDN_EUNSUPPORTED, "omx_gdn_chunk_fwd: not built yet");
+}
+
+size_t omx_gdn_prefill_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                      int64_t) {
+  return 0;
+}
+
+int omx_gdn_prefill(const void*, const void*, const void*, const void*, const float*,
+                    const float*, const float*, const float*, float, const int32_t*, int64_t,
+                    const float*, float*, const void*, void*, void*, int64_t, int64_t, int64_t,
+                    int64_t, int64_t, int64_t, int64_t, int64_t, void*, size_t, void*) {
+  return fail(OMX_GDN_EUNSUPPORTED, "omx_gdn_prefill: not built yet");
+}
+
+}  // extern "C"

@@ -1,0 +1,277 @@
+// Single-token cached decode step of the gated delta rule (gfx950).
+//
+// The reference has no Qwen3.5 decode (omegalax/models/qwen3_5/model.py:324-326,
+// text/api.py:128-131).  Semantics follow transformers' causal_conv1d_update and
+// torch_recurrent_gated_delta_rule; the gated norm follows deltanet.py:282-293.
+//
+// Work mapping: one workgroup of 256 threads per (sequence, key head).  The
+// workgroup owns every channel of that key head's q/k and of its gqa value heads,
+// so it can update the conv-state cache in place without racing another
+// workgroup, and it loops over its value heads.  For one value head the fp32
+// state S[dk][dv] (row-major, dv contiguous) is streamed once in and once out:
+// thread t owns 4 consecutive columns (one float4 per row) of the rows
+// rg, rg+RG, ... so one wavefront load covers whole contiguous rows.
+// With the recurrence written as
+//     kv = a S^T k,  delta = beta (v - kv),  o = a S^T q + (q.k) delta,
+//     S' = a S + k delta^T
+// both reductions over dk come from the same register-resident pass over S;
+// S' is written back from the same registers.  Per sequence and step the kernel
+// moves Hv*dk*dv*8 bytes of state plus the token's activations.
+#include "gdn_common.h"
+#include "gdn_kernels.h"
+
+namespace omx {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxConvK = 8;
+
+template <int DK, int DV, bool LAYER, typename InT>
+__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
+  constexpr int CG = DV / 4;            // column groups of 4
+  constexpr int RG = kThreads / CG;     // row groups
+  constexpr int R = (DK + RG - 1) / RG; // rows per thread
+  static_assert(DV % 4 == 0 && CG <= kThreads, "dv layout");
+
+  const int hk = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int gqa = p.Hv / p.Hk;
+
+  __shared__ __align__(16) float s_q[DK];
+  __shared__ __align__(16) float s_k[DK];
+  __shared__ __align__(16) float s_v[DV];
+  __shared__ __align__(16) float s_red_kv[RG][DV + 1];
+  __shared__ __align__(16) float s_red_qs[RG][DV + 1];
+  __shared__ __align__(16) float s_delta[DV];
+  __shared__ __align__(16) float s_o[DV];
+  __shared__ float s_scal[8];
+
+  // ---------------------------------------------------------------- q, k (and conv)
+  if (LAYER) {
+    const int conv_dim = 2 * p.Hk * DK + p.Hv * DV;
+    const int nch = 2 * DK + gqa * DV;
+    const int K = p.conv_k;
+    for (int i = tid; i < nch; i += kThreads) {
+      int c;
+      if (i < DK) c = hk * DK + i;
+      else if (i < 2 * DK) c = p.Hk * DK + hk * DK + (i - DK);
+      else c = 2 * p.Hk * DK + hk * gqa * DV + (i - 2 * DK);
+      const bf16_t* xin = (const bf16_t*)p.mixed_qkv + (size_t)b * conv_dim;
+      bf16_t* cs = (bf16_t*)p.conv_state + ((size_t)b * conv_dim + c) * (K - 1);
+      float hist[kMaxConvK];
+#pragma unroll
+      for (int j = 0; j < kMaxConvK - 1; ++j) hist[j] = (j < K - 1) ? bf2f(cs[j]) : 0.f;
+      const bf16_t xr = xin[c];
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxConvK; ++j) {
+        if (j < K - 1) acc += round_bf(p.conv_w[(size_t)c * K + j]) * hist[j];
+      }
+      acc += round_bf(p.conv_w[(size_t)c * K + K - 1]) * bf2f(xr);
+      const float y = round_bf(siluf_(round_bf(acc)));
+      // shift the cache: drop the oldest input, append this token's raw input
+#pragma unroll
+      for (int j = 0; j < kMaxConvK - 2; ++j) {
+        if (j < K - 2) cs[j] = f2bf(hist[j + 1]);
+      }
+      cs[K - 2] = xr;
+      if (i < DK) s_q[i] = y;
+      else if (i < 2 * DK) s_k[i - DK] = y;
+      else {
+        // value channels of head hh = (i - 2DK) / DV are parked in the reduction
+        // buffer until their head's turn
+        const int vi = i - 2 * DK;
+        s_red_kv[vi / DV][vi % DV] = y;  // gqa * DV <= RG * (DV + 1) checked on the host
+      }
+    }
+  } else {
+    const InT* qp = (const InT*)p.q + ((size_t)b * p.Hk + hk) * DK;
+    const InT* kp = (const InT*)p.k + ((size_t)b * p.Hk + hk) * DK;
+    for (int i = tid; i < DK; i += kThreads) {
+      if constexpr (sizeof(InT) == 2) {
+        s_q[i] = bf2f(qp[i]);
+        s_k[i] = bf2f(kp[i]);
+      } else {
+        s_q[i] = qp[i];
+        s_k[i] = kp[i];
+      }
+    }
+  }
+  __syncthreads();
+
+  // L2 norm of q and k at the input precision (deltanet.py:30-32, 65-66)
+  const int wave = tid >> 6, lane = tid & 63;
+  if (wave < 2) {
+    const float* src = wave == 0 ? s_q : s_k;
+    float ss = 0.f;
+    for (int i = lane; i < DK; i += 64) ss += src[i] * src[i];
+    ss = wave_sum(ss);
+    if (lane == 0) s_scal[wave] = rsqrtf(ss + 1e-6f);
+  }
+  __syncthreads();
+  const bool round_act = LAYER || sizeof(InT) == 2;
+  const float scale = p.scale;
+  for (int i = tid; i < DK; i += kThreads) {
+    float qn = s_q[i] * s_scal[0];
+    float kn = s_k[i] * s_scal[1];
+    if (round_act) { qn = round_bf(qn); kn = round_bf(kn); }
+    s_q[i] = qn * scale;
+    s_k[i] = kn;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float d = 0.f;
+    for (int i = lane; i < DK; i += 64) d += s_q[i] * s_k[i];
+    d = wave_sum(d);
+    if (lane == 0) s_scal[2] = d;
+  }
+  // value channels out of the parking buffer
+  float vpark[(DV * 8 + kThreads - 1) / kThreads];  // gqa <= 8
+  if (LAYER) {
+#pragma unroll
+    for (int j = 0; j < (DV * 8 + kThreads - 1) / kThreads; ++j) {
+      const int vi = tid + j * kThreads;
+      vpark[j] = (vi < gqa * DV) ? s_red_kv[vi / DV][vi % DV] : 0.f;
+    }
+  }
+  __syncthreads();
+  const float qk = s_scal[2];
+
+  const int cg = tid % CG, rg = tid / CG;
+  for (int hh = 0; hh < gqa; ++hh) {
+    const int h = hk * gqa + hh;
+    float alpha, beta;
+    if (LAYER) {
+      const float av = bf2f(((const bf16_t*)p.a)[(size_t)b * p.Hv + h]);
+      const float bv = bf2f(((const bf16_t*)p.b)[(size_t)b * p.Hv + h]);
+      const float g = -expf(p.A_log[h]) * softplusf_(av + p.dt_bias[h]);
+      alpha = expf(g);
+      beta = round_bf(sigmoidf_(bv));
+      // this head's values from the parked registers
+#pragma unroll
+      for (int j = 0; j < (DV * 8 + kThreads - 1) / kThreads; ++j) {
+        const int vi = tid + j * kThreads;
+        if (vi >= hh * DV && vi < (hh + 1) * DV) s_v[vi - hh * DV] = vpark[j];
+      }
+    } else {
+      alpha = expf(p.g[(size_t)b * p.Hv + h]);
+      beta = p.beta[(size_t)b * p.Hv + h];
+      const InT* vp = (const InT*)p.v + ((size_t)b * p.Hv + h) * DV;
+      for (int i = tid; i < DV; i += kThreads) {
+        if constexpr (sizeof(InT) == 2) s_v[i] = bf2f(vp[i]);
+        else s_v[i] = vp[i];
+      }
+    }
+
+    float* S = p.state + ((size_t)b * p.Hv + h) * DK * DV;
+    float4 st[R];
+    float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), qs = kv;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rg + r * RG;
+      if (row < DK) st[r] = *(const float4*)(S + (size_t)row * DV + 4 * cg);
+      else st[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rg + r * RG;
+      const float kr = row < DK ? s_k[row] : 0.f;
+      const float qr = row < DK ? s_q[row] : 0.f;
+      kv.x += kr * st[r].x; kv.y += kr * st[r].y; kv.z += kr * st[r].z; kv.w += kr * st[r].w;
+      qs.x += qr * st[r].x; qs.y += qr * st[r].y; qs.z += qr * st[r].z; qs.w += qr * st[r].w;
+    }
+    s_red_kv[rg][4 * cg + 0] = kv.x; s_red_kv[rg][4 * cg + 1] = kv.y;
+    s_red_kv[rg][4 * cg + 2] = kv.z; s_red_kv[rg][4 * cg + 3] = kv.w;
+    s_red_qs[rg][4 * cg + 0] = qs.x; s_red_qs[rg][4 * cg + 1] = qs.y;
+    s_red_qs[rg][4 * cg + 2] = qs.z; s_red_qs[rg][4 * cg + 3] = qs.w;
+    __syncthreads();
+    if (tid < DV) {
+      float skv = 0.f, sqs = 0.f;
+#pragma unroll
+      for (int r = 0; r < RG; ++r) { skv += s_red_kv[r][tid]; sqs += s_red_qs[r][tid]; }
+      const float delta = beta * (s_v[tid] - alpha * skv);
+      s_delta[tid] = delta;
+      s_o[tid] = alpha * sqs + qk * delta;
+    }
+    __syncthreads();
+    float4 dl = *(const float4*)(s_delta + 4 * cg);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rg + r * RG;
+      if (row < DK) {
+        const float kr = s_k[row];
+        float4 n;
+        n.x = alpha * st[r].x + kr * dl.x;
+        n.y = alpha * st[r].y + kr * dl.y;
+        n.z = alpha * st[r].z + kr * dl.z;
+        n.w = alpha * st[r].w + kr * dl.w;
+        *(float4*)(S + (size_t)row * DV + 4 * cg) = n;
+      }
+    }
+    if (LAYER) {
+      // gated RMSNorm on the fp32 core output (deltanet.py:282-293)
+      if (wave == 0) {
+        float ss = 0.f;
+        for (int i = lane; i < DV; i += 64) ss += s_o[i] * s_o[i];
+        ss = wave_sum(ss);
+        if (lane == 0) s_scal[3] = rsqrtf(ss / DV + p.eps);
+      }
+      __syncthreads();
+      const float rn = s_scal[3];
+      bf16_t* out = (bf16_t*)p.out + ((size_t)b * p.Hv + h) * DV;
+      const bf16_t* z = (const bf16_t*)p.z + ((size_t)b * p.Hv + h) * DV;
+      for (int i = tid; i < DV; i += kThreads) {
+        const float n = p.norm_w[i] * (s_o[i] * rn);
+        out[i] = f2bf(n * siluf_(bf2f(z[i])));
+      }
+    } else {
+      float* o = p.o + ((size_t)b * p.Hv + h) * DV;
+      for (int i = tid; i < DV; i += kThreads) o[i] = s_o[i];
+    }
+    __syncthreads();
+  }
+}
+
+template <int DK, int DV>
+hipError_t launch_dims(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
+  dim3 grid(p.Hk, p.B);
+  if (layer) {
+    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t>), grid, dim3(kThreads), 0, stream, p);
+  } else if (in_bf16) {
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, bf16_t>), grid, dim3(kThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, float>), grid, dim3(kThreads), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool decode_dims_supported(int dk, int dv) {
+  auto ok = [](int d) { return d == 16 || d == 32 || d == 64 || d == 128; };
+  return ok(dk) && ok(dv);
+}
+
+int decode_max_gqa() { return 8; }
+
+hipError_t launch_decode(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
+#define OMX_DK_CASE(DKV)                                                        \
+  if (p.dk == DKV) {                                                            \
+    switch (p.dv) {                                                             \
+      case 16: return launch_dims<DKV, 16>(p, layer, in_bf16, stream);         \
+      case 32: return launch_dims<DKV, 32>(p, layer, in_bf16, stream);         \
+      case 64: return launch_dims<DKV, 64>(p, layer, in_bf16, stream);         \
+      case 128: return launch_dims<DKV, 128>(p, layer, in_bf16, stream);       \
+    }                                                                           \
+  }
+  OMX_DK_CASE(16)
+  OMX_DK_CASE(32)
+  OMX_DK_CASE(64)
+  OMX_DK_CASE(128)
+#undef OMX_DK_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace omx

@@ -1,0 +1,208 @@
+"""GatedDeltaNet on MI355X: Python mirror of omegalax's interface over libomx_gdn.
+
+Reference interface (omegalax/models/qwen3_5/deltanet.py):
+  * ``chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=64)``
+    (:53-153) -- same positional signature and defaults, fp32 output; keyword-only
+    extensions ``initial_state``, ``output_final_state``, ``cu_seqlens``.
+  * ``GatedDeltaNet.__call__(hidden_BTD, attention_mask_BT=None)`` (:226-306) -- see
+    ``omegalax_amd.layer``.
+Tensors are torch tensors on the GPU (torch supplies device memory and the
+current stream); every computation runs in libomx_gdn's HIP kernels.  There is
+no fallback: a missing library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "chunk_gated_delta_rule", "recurrent_gated_delta_rule_step", "gdn_prefill",
+    "gdn_decode_step", "GDNError",
+]
+
+GDNError = _lib.GDNError
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dev(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("omegalax_amd kernels need GPU tensors (got a CPU tensor)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+        if not t.is_contiguous():
+            raise ValueError("omegalax_amd kernels need contiguous tensors")
+    return dev
+
+
+def _dtype_code(t):
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    if t.dtype == torch.float32:
+        return _lib.F32
+    raise ValueError(f"unsupported dtype {t.dtype} (bf16 or fp32)")
+
+
+def _f32(t):
+    return None if t is None else t.to(torch.float32).contiguous()
+
+
+def _workspace(nbytes, device):
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=64, *,
+                           initial_state=None, output_final_state=False, cu_seqlens=None,
+                           scale=None, use_qk_l2norm=True):
+    """Chunked gated delta rule (deltanet.py:53-153) on libomx_gdn.
+
+    q/k [B,T,Hk,A] and v [B,T,H,U] (bf16 or fp32, same dtype); Hk may divide H
+    (GQA, repeat-interleave semantics of deltanet.py:272-280) or equal it.
+    g/beta [B,T,H].  Returns o [B,T,H,U] fp32, or (o, final_state) when
+    ``output_final_state``.  ``cu_seqlens`` (int32 [N+1], B == 1) packs N
+    sequences; ``initial_state`` is [N or B, H, A, U] fp32.
+    """
+    q, k, v = q_BTHA.contiguous(), k_BTHA.contiguous(), v_BTHU.contiguous()
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    g, beta = _f32(g_BTH), _f32(beta_BTH)
+    dev = _dev(q, k, v, g, beta, initial_state, cu_seqlens)
+    B, T, Hk, A = q.shape
+    H, U = v.shape[2], v.shape[3]
+    if k.shape != q.shape or v.shape[:2] != (B, T) or g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
+                         f"g{tuple(g.shape)} beta{tuple(beta.shape)}")
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32:
+            raise ValueError("cu_seqlens must be int32")
+        N = cu_seqlens.numel() - 1
+    else:
+        N = B
+    if initial_state is not None:
+        initial_state = _f32(initial_state)
+        if tuple(initial_state.shape) != (N, H, A, U):
+            raise ValueError(f"initial_state must be {(N, H, A, U)}, got {tuple(initial_state.shape)}")
+    o = torch.empty((B, T, H, U), dtype=torch.float32, device=dev)
+    fs = torch.empty((N, H, A, U), dtype=torch.float32, device=dev) if output_final_state else None
+    sc = float(A ** -0.5) if scale is None else float(scale)
+    L = _lib.lib()
+    ws_bytes = L.omx_gdn_chunk_fwd_workspace_size(B, T, Hk, H, A, U, N)
+    ws = _workspace(ws_bytes, dev)
+    _lib.call("omx_gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), _dtype_code(q), _ptr(g), _ptr(beta),
+              _ptr(initial_state), _ptr(cu_seqlens), N, _ptr(o), _ptr(fs), B, T, Hk, H, A, U,
+              int(chunk_size), sc, int(bool(use_qk_l2norm)), _ptr(ws), ws_bytes, _stream(dev))
+    return (o, fs) if output_final_state else o
+
+
+def recurrent_gated_delta_rule_step(q, k, v, g, beta, state, *, scale=None):
+    """One token of the recurrent rule, in place on ``state`` [B,H,A,U] fp32.
+
+    q/k [B,Hk,A], v [B,H,U] (bf16 or fp32), g/beta [B,H].  Returns o [B,H,U] fp32.
+    Semantics of transformers' torch_recurrent_gated_delta_rule (qk L2-norm in kernel).
+    """
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g, beta = _f32(g), _f32(beta)
+    dev = _dev(q, k, v, g, beta, state)
+    if state.dtype != torch.float32:
+        raise ValueError("state must be fp32")
+    B, Hk, A = q.shape
+    H, U = v.shape[1], v.shape[2]
+    if tuple(state.shape) != (B, H, A, U):
+        raise ValueError(f"state must be {(B, H, A, U)}, got {tuple(state.shape)}")
+    o = torch.empty((B, H, U), dtype=torch.float32, device=dev)
+    sc = float(A ** -0.5) if scale is None else float(scale)
+    _lib.call("omx_gdn_recurrent_step", _ptr(q), _ptr(k), _ptr(v), _dtype_code(q), _ptr(g),
+              _ptr(beta), _ptr(state), _ptr(o), B, Hk, H, A, U, sc, _stream(dev))
+    return o
+
+
+def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_heads, head_k_dim,
+                num_v_heads, head_v_dim, eps=1e-6, chunk_size=64, cu_seqlens=None,
+                initial_state=None, conv_state=None, output_final_state=False):
+    """Prefill from projection outputs to the gated-norm output (deltanet.py:243-293).
+
+    mixed_qkv [B,T,conv_dim] bf16, z [B,T,Hv,dv] bf16 (or [B,T,Hv*dv]), a/b [B,T,Hv] bf16,
+    conv_w [conv_dim,K], A_log/dt_bias [Hv], norm_w [dv].  Returns out [B,T,Hv*dv] bf16,
+    or (out, final_state, conv_state_out) when ``output_final_state``.
+    """
+    Hk, dk, Hv, dv = num_k_heads, head_k_dim, num_v_heads, head_v_dim
+    x = mixed_qkv.contiguous()
+    z = z.contiguous()
+    a, b = a.contiguous(), b.contiguous()
+    conv_w, A_log, dt_bias, norm_w = (_f32(t) for t in (conv_w, A_log, dt_bias, norm_w))
+    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, cu_seqlens, initial_state, conv_state)
+    for name, t in (("mixed_qkv", x), ("z", z), ("a", a), ("b", b)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16")
+    B, T, Cd = x.shape
+    K = conv_w.shape[1]
+    if Cd != 2 * Hk * dk + Hv * dv or conv_w.shape[0] != Cd:
+        raise ValueError("mixed_qkv / conv_w channel count does not match the head layout")
+    if z.numel() != B * T * Hv * dv or a.shape != (B, T, Hv) or b.shape != (B, T, Hv):
+        raise ValueError("z/a/b shape does not match the head layout")
+    N = B if cu_seqlens is None else cu_seqlens.numel() - 1
+    if initial_state is not None:
+        initial_state = _f32(initial_state)
+        if tuple(initial_state.shape) != (N, Hv, dk, dv):
+            raise ValueError(f"initial_state must be {(N, Hv, dk, dv)}")
+    if conv_state is not None:
+        if conv_state.dtype != torch.bfloat16 or tuple(conv_state.shape) != (N, Cd, K - 1):
+            raise ValueError(f"conv_state must be bf16 {(N, Cd, K - 1)}")
+    out = torch.empty((B, T, Hv * dv), dtype=torch.bfloat16, device=dev)
+    fs = cs = None
+    if output_final_state:
+        fs = torch.empty((N, Hv, dk, dv), dtype=torch.float32, device=dev)
+        cs = torch.empty((N, Cd, K - 1), dtype=torch.bfloat16, device=dev)
+    L = _lib.lib()
+    ws_bytes = L.omx_gdn_prefill_workspace_size(B, T, Hk, Hv, dk, dv, N)
+    ws = _workspace(ws_bytes, dev)
+    _lib.call("omx_gdn_prefill", _ptr(x), _ptr(z), _ptr(a), _ptr(b), _ptr(conv_w), _ptr(A_log),
+              _ptr(dt_bias), _ptr(norm_w), float(eps), _ptr(cu_seqlens), N, _ptr(initial_state),
+              _ptr(fs), _ptr(conv_state), _ptr(cs), _ptr(out), B, T, Hk, Hv, dk, dv, K,
+              int(chunk_size), _ptr(ws), ws_bytes, _stream(dev))
+    return (out, fs, cs) if output_final_state else out
+
+
+def gdn_decode_step(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, conv_state, state, *,
+                    num_k_heads, head_k_dim, num_v_heads, head_v_dim, eps=1e-6):
+    """One cached decode step; updates ``conv_state`` and ``state`` in place.
+
+    mixed_qkv [B,conv_dim] bf16, z [B,Hv,dv] bf16, a/b [B,Hv] bf16,
+    conv_state [B,conv_dim,K-1] bf16, state [B,Hv,dk,dv] fp32.  Returns out [B,Hv*dv] bf16.
+    """
+    Hk, dk, Hv, dv = num_k_heads, head_k_dim, num_v_heads, head_v_dim
+    x = mixed_qkv.contiguous()
+    z, a, b = z.contiguous(), a.contiguous(), b.contiguous()
+    conv_w, A_log, dt_bias, norm_w = (_f32(t) for t in (conv_w, A_log, dt_bias, norm_w))
+    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, conv_state, state)
+    B, Cd = x.shape
+    K = conv_w.shape[1]
+    if Cd != 2 * Hk * dk + Hv * dv:
+        raise ValueError("mixed_qkv channel count does not match the head layout")
+    if tuple(conv_state.shape) != (B, Cd, K - 1) or conv_state.dtype != torch.bfloat16:
+        raise ValueError(f"conv_state must be bf16 {(B, Cd, K - 1)}")
+    if tuple(state.shape) != (B, Hv, dk, dv) or state.dtype != torch.float32:
+        raise ValueError(f"state must be fp32 {(B, Hv, dk, dv)}")
+    for name, t in (("mixed_qkv", x), ("z", z), ("a", a), ("b", b)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16")
+    out = torch.empty((B, Hv * dv), dtype=torch.bfloat16, device=dev)
+    _lib.call("omx_gdn_decode_step", _ptr(x), _ptr(z), _ptr(a), _ptr(b), _ptr(conv_w),
+              _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), float(eps), _ptr(conv_state),
+              _ptr(state), _ptr(out), B, Hk, Hv, dk, dv, K, _stream(dev))
+    return out

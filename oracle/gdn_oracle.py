@@ -291,7 +291,7 @@ def split_mixed_qkv(x_BTC, Hk, dk, Hv, dv):
 
 def _conv_silu(x_BTC, conv_w, history, act_round):
     w = act_round(np.asarray(conv_w, dtype=np.float32))        # cast to act dtype (deltanet.py:243)
-    y = causal_depthwise_conv1d(x_BTC, w, history)
+    y = act_round(causal_depthwise_conv1d(x_BTC, w, history))  # conv output in act dtype
     return act_round(silu(y))                                  # SiLU in act dtype (:243)
 
 

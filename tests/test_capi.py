@@ -1,0 +1,91 @@
+"""C-ABI tests that need no GPU: the library loads, exports every declared entry
+point, and rejects invalid requests on the host before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from omegalax_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "omx_gdn.h")
+
+pytestmark = pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH),
+                                reason="libomx_gdn.so not built (python -m omegalax_amd.build)")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(omx_gdn_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+
+
+def test_abi_version():
+    assert _lib.lib().omx_gdn_abi_version() == 100
+
+
+def _decode(**over):
+    args = dict(mixed_qkv=1, z=1, a=1, b=1, conv_w=1, A_log=1, dt_bias=1, norm_w=1, eps=1e-6,
+                conv_state=1, state=16, out=1, B=2, Hk=2, Hv=4, dk=128, dv=128, K=4, stream=None)
+    args.update(over)
+    L = _lib.lib()
+    rc = L.omx_gdn_decode_step(*args.values())
+    return rc, L.omx_gdn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(Hv=5), _lib.EINVAL, "multiple of key heads"),
+    (dict(Hk=0), _lib.EINVAL, "positive"),
+    (dict(K=1), _lib.EINVAL, "conv kernel size"),
+    (dict(K=9), _lib.EINVAL, "conv kernel size"),
+    (dict(B=-1), _lib.EINVAL, "batch"),
+    (dict(B=70000), _lib.EINVAL, "batch"),
+    (dict(eps=-1.0), _lib.EINVAL, "eps"),
+    (dict(dk=96), _lib.EUNSUPPORTED, "not compiled"),
+    (dict(Hk=1, Hv=16), _lib.EUNSUPPORTED, "gqa"),
+    (dict(state=None), _lib.EINVAL, "NULL"),
+    (dict(out=None), _lib.EINVAL, "NULL"),
+    (dict(state=8), _lib.EINVAL, "aligned"),
+])
+def test_decode_rejects_bad_arguments(over, code, msg):
+    rc, err = _decode(**over)
+    assert rc == code
+    assert msg in err
+
+
+def test_decode_zero_batch_is_a_noop():
+    rc, err = _decode(B=0, state=None, out=None)
+    assert rc == _lib.OK and err == ""
+
+
+def test_recurrent_step_rejects_bad_dtype_and_null():
+    L = _lib.lib()
+    rc = L.omx_gdn_recurrent_step(1, 1, 1, 7, 1, 1, 16, 1, 1, 1, 1, 64, 64, 0.125, None)
+    assert rc == _lib.EINVAL and "in_dtype" in L.omx_gdn_last_error().decode()
+    rc = L.omx_gdn_recurrent_step(1, 1, None, 0, 1, 1, 16, 1, 1, 1, 1, 64, 64, 0.125, None)
+    assert rc == _lib.EINVAL and "NULL" in L.omx_gdn_last_error().decode()
+
+
+def test_call_raises_gdnerror_with_message():
+    with pytest.raises(_lib.GDNError, match="multiple of key heads"):
+        _lib.call("omx_gdn_decode_step", 1, 1, 1, 1, 1, 1, 1, 1, 1e-6, 1, 16, 1,
+                  1, 3, 4, 128, 128, 4, None)
+
+
+def test_python_api_rejects_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from omegalax_amd import recurrent_gated_delta_rule_step
+    q = torch.zeros(1, 1, 16)
+    with pytest.raises(ValueError, match="GPU"):
+        recurrent_gated_delta_rule_step(q, q, torch.zeros(1, 1, 16), torch.zeros(1, 1),
+                                        torch.zeros(1, 1), torch.zeros(1, 1, 16, 16))
