@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X GatedDeltaNet path on one GPU; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|core]
+
+Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
+  prefill  config C1: GDN layer prefill from projection outputs (mixed_qkv, z, a, b)
+           to the gated-norm output, B=4 T=4096 Hk=16 Hv=32 d=128 (headline).
+           A "step" is one omx_gdn_prefill call over the whole batch.
+  decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
+  core     config C4-shaped chunked rule at the core-function boundary.
+The headline line reports prefill tokens/s with the chunked-scan kernel's MFMA
+roofline, and carries the decode step's HBM roofline as "decode".  Only one GPU
+is used: --gpus above 1 exits with a message.
+
+Kernel durations come from HIP events recorded on the stream the kernels run on
+(torch's current stream, which the library launches on).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+C = 64
+
+
+def prefill_flops_per_token_head(dk, dv, c=C):
+    """Matmuls of deltanet.py:107,115,116,130,133,136,137,142: 2C(3dk+2dv) + 6 dk dv."""
+    return 2 * c * (3 * dk + 2 * dv) + 6 * dk * dv
+
+
+def decode_bytes_per_seq(Hk, Hv, dk, dv, K=4):
+    conv_dim = 2 * Hk * dk + Hv * dv
+    return (Hv * dk * dv * 4 * 2 + 2 * conv_dim * (K - 1) * 2 + conv_dim * 2 + 2 * Hv * 2
+            + 2 * Hv * dv * 2)
+
+
+def _say(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_launches(fn, steps, warmup):
+    """Run fn warmup+steps times; return (wall seconds of the timed steps, mean event ms per call)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) for s, e in evs]
+    return wall, float(np.mean(per))
+
+
+def cpu_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+# ----------------------------------------------------------------------------- decode (C2)
+
+def bench_decode(B, steps, warmup, cpu_baseline):
+    import torch
+    from omegalax_amd import gdn_decode_step, workloads as W
+    Hk, Hv, d = 16, 32, 128
+    _say(f"decode: B={B} generating inputs")
+    arrs = W.decode_inputs(B)
+    t = W.to_device(arrs)
+    dims = dict(num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+
+    def step():
+        gdn_decode_step(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                        t["dt_bias"], t["norm_w"], t["conv_state"], t["state"], **dims)
+
+    _say(f"decode: B={B} timing {steps} steps")
+    wall, ms = time_launches(step, steps, warmup)
+    nbytes = decode_bytes_per_seq(Hk, Hv, d, d) * B
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    res = {
+        "batch": B, "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+        "tokens_per_s": B * steps / wall,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None,
+                     "algorithmic_bytes": nbytes},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_decode_baseline()
+    return res
+
+
+def cpu_decode_baseline(B=8, budget_s=10.0):
+    """Oracle decode step (numpy fp64, the 'port') on a bounded sample: B=8 sequences."""
+    from oracle import gdn_oracle as O
+    from omegalax_amd import workloads as W
+    d = W.decode_inputs(B)
+    S = d["state"].astype(np.float64)
+    conv = d["conv_state"]
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        _, conv, S = O.gdn_decode_step(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"],
+                                       d["A_log"], d["dt_bias"], d["norm_w"], conv, S,
+                                       Hk=16, dk=128, Hv=32, dv=128)
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": B * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
+            "sample": f"{n} decode steps of the numpy fp64 oracle at B={B}, C2 head layout"}
+
+
+# ----------------------------------------------------------------------------- prefill (C1)
+
+def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
+    import torch
+    from omegalax_amd import chunk_gated_delta_rule, gdn_prefill, workloads as W
+    Hk, Hv, d = 16, 32, 128
+    _say(f"prefill: B={B} T={T} generating inputs")
+    arrs = W.layer_inputs(B, T, Hk, Hv, d, d)
+    t = W.to_device(arrs)
+    dims = dict(num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+
+    def step():
+        gdn_prefill(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                    t["dt_bias"], t["norm_w"], **dims)
+
+    _say(f"prefill: timing {steps} layer steps")
+    wall, ms_step = time_launches(step, steps, warmup)
+    tokens = B * T
+    flops = prefill_flops_per_token_head(d, d) * tokens * Hv
+
+    # the dominant kernel, the chunked scan, at the core-function boundary on the same shapes
+    rng = np.random.default_rng(7)
+    q = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hk, d), dtype=np.float32))).cuda().bfloat16()
+    k = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hk, d), dtype=np.float32))).cuda().bfloat16()
+    v = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hv, d), dtype=np.float32))).cuda().bfloat16()
+    g32, beta32 = W.gates_f32(arrs["a"], arrs["b"], arrs["A_log"], arrs["dt_bias"])
+    g = torch.from_numpy(g32).cuda()
+    beta = torch.from_numpy(beta32).cuda()
+
+    def core():
+        chunk_gated_delta_rule(q, k, v, g, beta, 64)
+
+    _say(f"prefill: timing {steps} core-kernel launches")
+    _, ms_core = time_launches(core, steps, warmup)
+    tf = flops / (ms_core * 1e-3) / 1e12
+    res = {
+        "tokens_per_s": tokens * steps / wall, "ms_per_step": wall / steps * 1e3,
+        "step_event_ms": ms_step, "core_kernel_ms": ms_core,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
+                     "algorithmic_flops": flops},
+    }
+    if cpu_baseline:
+        res["cpu_baseline"] = cpu_prefill_baseline()
+    return res
+
+
+def cpu_prefill_baseline(budget_s=15.0):
+    """Oracle layer prefill (numpy, fp32 chunked core) on a bounded C1 sample: B=1, T=512."""
+    from oracle import gdn_oracle as O
+    from omegalax_amd import workloads as W
+    B, T = 1, 512
+    d = W.layer_inputs(B, T)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        O.gdn_prefill_layer(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"], d["A_log"],
+                            d["dt_bias"], d["norm_w"], Hk=16, dk=128, Hv=32, dv=128)
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": B * T * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
+            "sample": f"{n} runs of the numpy oracle layer prefill, B={B} T={T}, C1 head layout"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=["prefill", "decode"], default="prefill")
+    ap.add_argument("--decode-batch", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the GDN path shards by sequence and head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    cpu = not args.no_cpu_baseline
+    if args.workload == "decode":
+        dec = bench_decode(args.decode_batch, args.steps, args.warmup, cpu)
+        line = {
+            "metric": "decode-step HBM GB/s (GDN decode, config C2)",
+            "value": dec["roofline"]["achieved"], "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": dec["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (seeded N(0,1) activations, random-init params)",
+            "config": {"workload": f"C2 decode step B={args.decode_batch} Hk=16 Hv=32 d=128"},
+            "roofline": dec["roofline"], "decode": dec,
+        }
+        if cpu:
+            line["cpu_baseline"] = dec.pop("cpu_baseline")
+        print(json.dumps(line), flush=True)
+        return 0
+    pre = bench_prefill(args.steps, args.warmup, cpu)
+    dec = bench_decode(args.decode_batch, max(args.steps, 20), args.warmup, False)
+    line = {
+        "metric": "GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
+        "value": pre["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": pre["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, random-init params)",
+        "config": {"workload": "C1 GDN layer prefill (projection outputs -> gated-norm output)",
+                   "batch": 4, "seq_len": 4096, "k_heads": 16, "v_heads": 32, "head_dim": 128,
+                   "chunk": 64},
+        "roofline": pre["roofline"],
+        "decode": {"config": f"C2 B={args.decode_batch}", "roofline": dec["roofline"],
+                   "kernel_ms": dec["kernel_ms"], "tokens_per_s": dec["tokens_per_s"]},
+        "prefill_detail": {k_: pre[k_] for k_ in ("step_event_ms", "core_kernel_ms")},
+    }
+    if cpu:
+        line["cpu_baseline"] = pre["cpu_baseline"]
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
