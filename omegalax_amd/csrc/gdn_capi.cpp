@@ -8,6 +8,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -126,14 +128,52 @@ extern "C" {
 
 size_t omx_gdn_chunk_fwd_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                                         int64_t) {
-  return 0;
+  return 0;  // the chunked kernel keeps every intermediate in registers and LDS
 }
 
-int omx_gdn_chunk_fwd(const void*, const void*, const void*, int, const float*, const float*,
-                      const float*, const int32_t*, int64_t, float*, float*, int64_t, int64_t,
-                      int64_t, int64_t, int64_t, int64_t, int64_t, float, int, void*, size_t,
-                      void*) {
-  return fail(OMX_GDN_EUNSUPPORTED, "omx_gdn_chunk_fwd: not built yet");
+int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
+                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
+                      int64_t N, float* o, float* final_state, int64_t B, int64_t T, int64_t Hk,
+                      int64_t Hv, int64_t dk, int64_t dv, int64_t chunk_size, float scale,
+                      int qk_l2norm, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "omx_gdn_chunk_fwd";
+  (void)workspace;
+  (void)workspace_bytes;
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
+          in_dtype);
+  REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
+  REQUIRE(B >= 0 && T >= 0, "%s: negative shape (B=%lld, T=%lld)", fn, (long long)B, (long long)T);
+  REQUIRE(B * T <= (int64_t)1 << 31, "%s: too many tokens (%lld)", fn, (long long)(B * T));
+  REQUIRE(std::isfinite(scale), "%s: scale must be finite", fn);
+  if (cu_seqlens) {
+    REQUIRE(B == 1, "%s: cu_seqlens requires batch 1 (got %lld)", fn, (long long)B);
+    REQUIRE(N >= 1 && N <= (1 << 20), "%s: sequence count %lld out of range", fn, (long long)N);
+  } else {
+    REQUIRE(N == B, "%s: without cu_seqlens N must equal B (%lld vs %lld)", fn, (long long)N,
+            (long long)B);
+  }
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  if (!omx::chunk_dims_supported((int)dk, (int)dv, f32))
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled for %s inputs",
+                fn, (long long)dk, (long long)dv, f32 ? "fp32" : "bf16");
+  if (N == 0 || (B * T == 0 && !final_state)) return ok();
+  REQUIRE(o || B * T == 0, "%s: o is NULL", fn);
+  if (B * T > 0) REQUIRE(q && k && v && g && beta, "%s: a required pointer is NULL", fn);
+  const size_t al = f32 ? 16 : 16;
+  REQUIRE(!q || (aligned(q, al) && aligned(k, al) && aligned(v, al)),
+          "%s: q, k, v must be 16-byte aligned", fn);
+  omx::ChunkParams p{};
+  p.q = q; p.k = k; p.v = v;
+  p.q_ld = Hk * dk; p.k_ld = Hk * dk; p.v_ld = Hv * dv;
+  p.g = g; p.beta = beta; p.o = o;
+  p.initial_state = initial_state; p.final_state = final_state; p.cu_seqlens = cu_seqlens;
+  p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.DV = (int)dv;
+  p.nb = (int)(dv / omx::chunk_block_cols((int)dk, (int)dv, f32));
+  p.scale = scale; p.qk_l2norm = qk_l2norm ? 1 : 0;
+  REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
+  return launch_status(omx::launch_chunk(p, f32, (hipStream_t)stream), fn);
 }
 
 size_t omx_gdn_prefill_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,

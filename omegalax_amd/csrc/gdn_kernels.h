@@ -35,6 +35,41 @@ struct DecodeParams {
   float scale, eps;
 };
 
+// Chunked prefill (core function or fused layer).
+struct ChunkParams {
+  // core mode inputs: q/k [tokens, *, dk], v [tokens, *, DV] with row strides (elements)
+  const void* q;
+  const void* k;
+  const void* v;
+  long long q_ld, k_ld, v_ld;
+  const float* g;         // [tokens, Hv]
+  const float* beta;      // [tokens, Hv]
+  float* o;               // [tokens, Hv, DV] fp32
+  // layer mode inputs
+  const void* mixed_qkv;  // [tokens, conv_dim] bf16
+  const void* z;          // [tokens, Hv, DV] bf16
+  const void* a;          // [tokens, Hv] bf16
+  const void* b;          // [tokens, Hv] bf16
+  const float* conv_w;    // [conv_dim, K]
+  const float* A_log;
+  const float* dt_bias;
+  const float* norm_w;
+  const void* conv_state_in;   // [N, conv_dim, K-1] bf16 or null
+  void* conv_state_out;        // [N, conv_dim, K-1] bf16 or null
+  void* out;                   // [tokens, Hv*DV] bf16
+  // both
+  const float* initial_state;  // [N, Hv, dk, DV] or null
+  float* final_state;          // [N, Hv, dk, DV] or null
+  const int32_t* cu_seqlens;   // [N+1] or null (then sequence n = batch row n of length T)
+  int N, T, Hk, Hv, dk, DV, nb, conv_k, conv_dim;
+  float scale, eps;
+  int qk_l2norm;
+};
+
+bool chunk_dims_supported(int dk, int dv, bool f32_inputs);
+int chunk_block_cols(int dk, int dv, bool f32_inputs);
+hipError_t launch_chunk(const ChunkParams& p, bool f32_inputs, hipStream_t stream);
+
 bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();
 hipError_t launch_decode(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream);

@@ -60,6 +60,21 @@ def _f32(t):
     return None if t is None else t.to(torch.float32).contiguous()
 
 
+def _check_cu_seqlens(cu, B, T):
+    """Validate packed-sequence offsets (int32 [N+1], 0 = cu[0] <= ... <= cu[N] = T, B == 1).
+
+    One small device-to-host copy; the kernels also clamp offsets to [0, T].
+    """
+    if cu.dtype != torch.int32 or cu.dim() != 1 or cu.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D int32 tensor with at least 2 entries")
+    if B != 1:
+        raise ValueError(f"cu_seqlens requires batch size 1, got {B}")
+    h = cu.detach().to("cpu")
+    if int(h[0]) != 0 or int(h[-1]) != T or bool((h[1:] < h[:-1]).any()):
+        raise ValueError(f"cu_seqlens must rise monotonically from 0 to T={T}: {h.tolist()[:16]}")
+    return cu.numel() - 1
+
+
 def _workspace(nbytes, device):
     if nbytes == 0:
         return None
@@ -87,12 +102,7 @@ def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=6
     if k.shape != q.shape or v.shape[:2] != (B, T) or g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
                          f"g{tuple(g.shape)} beta{tuple(beta.shape)}")
-    if cu_seqlens is not None:
-        if cu_seqlens.dtype != torch.int32:
-            raise ValueError("cu_seqlens must be int32")
-        N = cu_seqlens.numel() - 1
-    else:
-        N = B
+    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
     if initial_state is not None:
         initial_state = _f32(initial_state)
         if tuple(initial_state.shape) != (N, H, A, U):
@@ -155,7 +165,7 @@ def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_hea
         raise ValueError("mixed_qkv / conv_w channel count does not match the head layout")
     if z.numel() != B * T * Hv * dv or a.shape != (B, T, Hv) or b.shape != (B, T, Hv):
         raise ValueError("z/a/b shape does not match the head layout")
-    N = B if cu_seqlens is None else cu_seqlens.numel() - 1
+    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
     if initial_state is not None:
         initial_state = _f32(initial_state)
         if tuple(initial_state.shape) != (N, Hv, dk, dv):
