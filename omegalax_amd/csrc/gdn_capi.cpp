@@ -42,6 +42,8 @@ int launch_status(hipError_t e, const char* what) {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
 #define REQUIRE(cond, ...) \
   do {                     \
     if (!(cond)) return fail(OMX_GDN_EINVAL, __VA_ARGS__); \
@@ -123,7 +125,7 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
 
 }  // extern "C"
 
-// ---------------------------------------------------------------------------- prefill (pending)
+// ---------------------------------------------------------------------------- prefill
 extern "C" {
 
 size_t omx_gdn_chunk_fwd_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
@@ -170,22 +172,85 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   p.g = g; p.beta = beta; p.o = o;
   p.initial_state = initial_state; p.final_state = final_state; p.cu_seqlens = cu_seqlens;
   p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.DV = (int)dv;
-  p.nb = (int)(dv / omx::chunk_block_cols((int)dk, (int)dv, f32));
+  p.nb = (int)(dv / omx::chunk_block_cols());
   p.scale = scale; p.qk_l2norm = qk_l2norm ? 1 : 0;
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
   return launch_status(omx::launch_chunk(p, f32, (hipStream_t)stream), fn);
 }
 
-size_t omx_gdn_prefill_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                      int64_t) {
-  return 0;
+size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                      int64_t dv, int64_t N) {
+  (void)Hk;
+  (void)dk;
+  (void)N;
+  // dv wider than one workgroup's column block: bf16 o and per-block sums of o^2
+  const int64_t cols = omx::chunk_block_cols();
+  if (dv <= cols || B <= 0 || T <= 0 || Hv <= 0) return 0;
+  const int64_t nb = (dv + cols - 1) / cols;
+  const int64_t rows = B * T * Hv;
+  const size_t o_bytes = align_up((size_t)(rows * dv * 2), 256);
+  return o_bytes + align_up((size_t)(rows * nb * 4), 256);
 }
 
-int omx_gdn_prefill(const void*, const void*, const void*, const void*, const float*,
-                    const float*, const float*, const float*, float, const int32_t*, int64_t,
-                    const float*, float*, const void*, void*, void*, int64_t, int64_t, int64_t,
-                    int64_t, int64_t, int64_t, int64_t, int64_t, void*, size_t, void*) {
-  return fail(OMX_GDN_EUNSUPPORTED, "omx_gdn_prefill: not built yet");
+int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                    const float* conv_w, const float* A_log, const float* dt_bias,
+                    const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                    const float* initial_state, float* final_state, const void* conv_state_in,
+                    void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                    int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "omx_gdn_prefill";
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
+  REQUIRE(K >= 2 && K <= 4, "%s: conv kernel size %lld not in [2, 4]", fn, (long long)K);
+  REQUIRE(B >= 0 && T >= 0, "%s: negative shape (B=%lld, T=%lld)", fn, (long long)B, (long long)T);
+  REQUIRE(B * T <= (int64_t)1 << 31, "%s: too many tokens (%lld)", fn, (long long)(B * T));
+  REQUIRE(eps >= 0.f && eps < 1.f, "%s: eps %g out of range", fn, (double)eps);
+  if (cu_seqlens) {
+    REQUIRE(B == 1, "%s: cu_seqlens requires batch 1 (got %lld)", fn, (long long)B);
+    REQUIRE(N >= 1 && N <= (1 << 20), "%s: sequence count %lld out of range", fn, (long long)N);
+  } else {
+    REQUIRE(N == B, "%s: without cu_seqlens N must equal B (%lld vs %lld)", fn, (long long)N,
+            (long long)B);
+  }
+  if (!omx::layer_dims_supported((int)dk, (int)dv))
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled", fn,
+                (long long)dk, (long long)dv);
+  const size_t need = omx_gdn_prefill_workspace_size(B, T, Hk, Hv, dk, dv, N);
+  REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes is smaller than the %zu needed", fn,
+          workspace_bytes, need);
+  if (N == 0) return ok();
+  const int64_t tokens = B * T;
+  if (tokens > 0)
+    REQUIRE(mixed_qkv && z && a && b && out, "%s: an activation pointer is NULL", fn);
+  REQUIRE(conv_w && A_log && dt_bias && norm_w, "%s: a parameter pointer is NULL", fn);
+  REQUIRE(need == 0 || workspace, "%s: workspace is NULL", fn);
+  REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 4) && aligned(out, 4)),
+          "%s: mixed_qkv must be 16-byte, z and out 4-byte aligned", fn);
+  REQUIRE(!workspace || aligned(workspace, 16), "%s: workspace must be 16-byte aligned", fn);
+  omx::ChunkParams p{};
+  p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b;
+  p.conv_w = conv_w; p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w;
+  p.conv_state_in = conv_state_in; p.conv_state_out = conv_state_out; p.out = out;
+  p.initial_state = initial_state; p.final_state = final_state; p.cu_seqlens = cu_seqlens;
+  p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.DV = (int)dv;
+  p.nb = (int)(dv / omx::chunk_block_cols());
+  p.conv_k = (int)K;
+  p.conv_dim = (int)(2 * Hk * dk + Hv * dv);
+  p.scale = 1.0f / sqrtf((float)dk);
+  p.eps = eps;
+  p.qk_l2norm = 1;
+  if (p.nb > 1) {
+    p.o_part = workspace;
+    p.ss_part = (float*)((char*)workspace + align_up((size_t)(tokens * Hv * dv * 2), 256));
+  }
+  REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
+  hipError_t e = omx::launch_layer(p, (hipStream_t)stream);
+  if (e == hipSuccess && p.nb > 1)
+    e = omx::launch_norm_epilogue(p.o_part, p.ss_part, z, norm_w, out, tokens * Hv, (int)dv, p.nb,
+                                  eps, (hipStream_t)stream);
+  return launch_status(e, fn);
 }
 
 }  // extern "C"

@@ -2,32 +2,39 @@
 //
 // Follows chunk_gated_delta_rule (omegalax/models/qwen3_5/deltanet.py:53-153),
 // restated for MFMA.  Per chunk of C = 64 tokens, with G the in-chunk cumsum of g
-// (:98), L = strict_lower(beta_i (k_i.k_j) e^{G_i-G_j}) (:100-108) and
-// T = (I + L)^-1 (the solve_triangular of :110-113):
-//     V_new = T diag(beta) V - T diag(beta e^G) (K S)        (:115-116, :133-134)
-//     O     = e^G (Q S) scale + P V_new,  P = lower(scale (q_i.k_j) e^{G_i-G_j})  (:130-137)
-//     S    <- e^{G_last} S + K^T diag(e^{G_last - G}) V_new   (:139-142)
-// (W S is evaluated as T diag(beta e^G) (K S), the same product reassociated.)
+// (:98) and L = strict_lower(beta_i (k_i.k_j) e^{G_i-G_j}) (:100-108), the
+// reference forms T = (I + L)^-1 by solve_triangular (:110-113) and then
+// U = T diag(beta) V, W = T diag(beta e^G) K (:115-116).  Here the two products
+// with T are merged into one triangular solve per chunk,
+//     (I + L) V_new = diag(beta) V - diag(beta e^G) (K S)         (:133-134)
+// done by block forward substitution over the four 16-token blocks; only the
+// 16x16 diagonal blocks are inverted explicitly.  Then
+//     O  = scale e^G (Q S) + P V_new,  P = lower(scale (q_i.k_j) e^{G_i-G_j})  (:130-137)
+//     S <- e^{G_last} S + K^T diag(e^{G_last - G}) V_new           (:139-142)
 //
-// Work mapping.  One workgroup per (sequence, value head, dv-block of BV = 16*NWC
-// columns) walks that sequence's chunks in order.  Wavefront w owns state
-// columns [16w, 16w+16) of the block: its fp32 slice S[dk][16] stays in MFMA
-// accumulator registers for the whole sequence, and every product that touches
-// it (K S, Q S, V_new, O, the state update) runs on that wavefront alone.  The
-// per-chunk work that does not touch S -- staging K, Q, V in LDS, K K^T and Q K^T
-// on MFMA, the 64x64 triangular inverse -- is shared by all wavefronts between
-// workgroup barriers.
+// Work mapping.  One workgroup of 4 wavefronts per (sequence, value head,
+// 64-column block of dv) walks that sequence's chunks in order.  Wavefront w
+// owns state columns [16w, 16w+16) of the block: its fp32 slice S[dk][16] stays
+// in MFMA accumulator registers for the whole sequence, and every product that
+// touches it (K S, Q S, the solve, O, the state update) runs on that wavefront
+// alone.  The per-chunk work that does not touch S -- staging K, Q, V in LDS,
+// K K^T and Q K^T, the diagonal-block inverses -- is shared between workgroup
+// barriers.  The next chunk's global loads are issued into registers before the
+// state pipeline starts, so their latency hides behind it.
 //
 // Precision.  MFMA inputs are bf16 with fp32 accumulation.  q, k, v are bf16 on
-// the layer path (exact), or fp32 split into hi+lo bf16 pairs (MODE_F32).  T and
-// the state-update operand diag(e^{G_last-G}) V_new are always split hi+lo; with
-// bf16 inputs S enters K S / Q S, and P, V_new enter P V_new, as single bf16
-// (their rounding reaches only the bf16-tolerance output).
+// the layer path (exact), or fp32 split into hi+lo bf16 pairs (MODE_F32).  The
+// solve's operands (L blocks, diagonal inverses, right-hand sides) and the
+// state-update operand diag(e^{G_last-G}) V_new are always split hi+lo; with bf16
+// inputs S enters K S / Q S, and P, V_new enter P V_new, as single bf16 (their
+// rounding reaches only the bf16-tolerance output).
 //
 // Modes: MODE_BF16 / MODE_F32 read q, k, v, g, beta (core function) and store o
-// in fp32; MODE_LAYER reads the raw in_proj outputs, applies the causal conv +
-// SiLU + L2 norm and the gates in the load stage, and stores the gated-RMSNorm
-// output in bf16 (deltanet.py:243-293); it needs BV == dv.
+// in fp32.  MODE_LAYER reads the raw in_proj outputs, applies the causal conv +
+// SiLU + L2 norm and the gates while staging (deltanet.py:243-250), and ends in
+// the gated RMSNorm (deltanet.py:282-293): fused when one workgroup holds all of
+// dv, otherwise through a bf16 o buffer and per-token partial sums of o^2 that
+// the epilogue kernel (gdn_epilogue.hip) normalises.
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -38,55 +45,63 @@ namespace omx {
 
 namespace {
 
-constexpr int C = 64;        // chunk length (deltanet.py:59)
-constexpr int LDT = C + 8;   // row stride (elements) of [x][token] bf16 arrays
-constexpr int LDF = C + 4;   // row stride of the fp32 64x64 T array
+constexpr int C = 64;          // chunk length (deltanet.py:59)
+constexpr int NWC = 4;         // column wavefronts per workgroup
+constexpr int NT = 64 * NWC;   // threads per workgroup
+constexpr int BV = 16 * NWC;   // state columns per workgroup
+constexpr int LDT = C + 8;     // row stride (elements) of 64-wide bf16 arrays
+constexpr int LDD = 16 + 4;    // row stride of 16-wide diagonal-block arrays
 constexpr int MODE_BF16 = 0, MODE_F32 = 1, MODE_LAYER = 2;
 
-template <int DK, int NWC, int MODE>
+template <int DK, int MODE>
 struct Cfg {
-  static constexpr int NT = 64 * NWC;               // threads
-  static constexpr int BV = 16 * NWC;               // state columns per workgroup
-  static constexpr bool IS = MODE == MODE_F32;      // q/k/v split hi+lo
-  static constexpr bool OS = MODE == MODE_F32;      // output-path operands split
+  static constexpr bool IS = MODE == MODE_F32;  // q/k/v split hi+lo
+  static constexpr bool OS = MODE == MODE_F32;  // output-path operands split
   static constexpr int NS = IS ? 2 : 1;
-  static constexpr int LDK = DK + 8;                // row stride of [token][dk] arrays
+  static constexpr int RAWW = IS ? 2 : 1;       // u32x4 words per 8-element input segment
+  static constexpr int LDK = DK + 8;            // row stride of [token][dk] arrays
+  static constexpr int SEGS = DK / 8;           // 8-element segments per q/k row
+  static constexpr int NI_KQ = 2 * C * SEGS / NT;
+  static constexpr int NI_V = C * (BV / 8) / NT;
   // shared arrays (bytes)
-  static constexpr int SZ_K = NS * C * LDK * 2;
-  static constexpr int SZ_KT = NS * DK * LDT * 2;
-  static constexpr int SZ_VT = NS * BV * LDT * 2;
-  static constexpr int SZ_T = C * LDF * 4;
+  static constexpr int SZ_K = NS * C * LDK * 2;   // K rows [token][dk] (hi, lo)
+  static constexpr int SZ_KT = NS * DK * LDT * 2; // K^T [dk][token]
+  static constexpr int SZ_VT = NS * BV * LDT * 2; // V^T [col][token]
+  static constexpr int SZ_LO = 2 * C * LDT * 2;   // off-diagonal blocks of L (hi, lo)
+  static constexpr int SZ_LD = C * LDD * 4;       // diagonal blocks of L, fp32
+  static constexpr int SZ_TD = 2 * C * LDD * 2;   // inverses of the diagonal blocks (hi, lo)
   static constexpr int SZ_P = (OS ? 2 : 1) * C * LDT * 2;
   static constexpr int SZ_SC = 8 * C * 4;
-  // per-wave scratch: S^T (start of phase B), then K S^T, then V_new^T + Vt^T hi/lo
+  // per-wave scratch: S^T (K S, Q S), then U^T (hi, lo) and Vt^T (hi, lo)
   static constexpr int WS_S = NS * 16 * LDK * 2;
-  static constexpr int WS_KS = NS * 16 * LDT * 2;
-  static constexpr int WS_V = ((OS ? 2 : 1) + 2) * 16 * LDT * 2;
-  static constexpr int WS = WS_S > WS_V ? (WS_S > WS_KS ? WS_S : WS_KS) : (WS_V > WS_KS ? WS_V : WS_KS);
+  static constexpr int WS_U = 4 * 16 * LDT * 2;
+  static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
   static constexpr int SZ_W = NWC * WS;
-  // layer mode: raw conv history (K-1 = 3 rows of q|k|v-block) and norm partial sums
-  static constexpr int HIST_W = 2 * DK + BV;
-  static constexpr int SZ_H = MODE == MODE_LAYER ? 3 * HIST_W * 2 : 0;
+  static constexpr int SZ_HIST = MODE == MODE_LAYER ? 3 * (2 * DK + BV) * 2 : 0;
   static constexpr int SZ_NP = MODE == MODE_LAYER ? C * NWC * 4 : 0;
   static constexpr int OFF_K = 0;
   static constexpr int OFF_Q = OFF_K + SZ_K;
   static constexpr int OFF_KT = OFF_Q + SZ_K;
   static constexpr int OFF_VT = OFF_KT + SZ_KT;
-  static constexpr int OFF_T = OFF_VT + SZ_VT;
-  static constexpr int OFF_P = OFF_T + SZ_T;
+  static constexpr int OFF_LO = OFF_VT + SZ_VT;
+  static constexpr int OFF_LD = OFF_LO + SZ_LO;
+  static constexpr int OFF_TD = OFF_LD + SZ_LD;
+  static constexpr int OFF_P = OFF_TD + SZ_TD;
   static constexpr int OFF_SC = OFF_P + SZ_P;
   static constexpr int OFF_W = OFF_SC + SZ_SC;
-  static constexpr int OFF_H = OFF_W + SZ_W;
-  static constexpr int OFF_NP = OFF_H + SZ_H;
+  static constexpr int OFF_HIST = OFF_W + SZ_W;
+  static constexpr int OFF_NP = OFF_HIST + SZ_HIST;
   static constexpr int TOTAL = OFF_NP + SZ_NP;
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
-  static_assert(SZ_W >= 32 * 33 * 4, "T-merge temp lives in the wave scratch");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
+  static_assert(NI_KQ * NT == 2 * C * SEGS && NI_V * NT == C * (BV / 8), "item split");
 };
 
-// lower-triangular 16x16 tiles of a 64x64 matrix, (row block, col block)
-__constant__ int kTri[10][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1},
-                                {2, 2}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
+// the 20 tiles of K K^T and Q K^T that A2 computes: (which, row block, col block)
+__constant__ int kTiles[20][3] = {
+    {0, 0, 0}, {0, 1, 1}, {0, 2, 2}, {0, 3, 3}, {0, 1, 0}, {0, 2, 0}, {0, 2, 1}, {0, 3, 0},
+    {0, 3, 1}, {0, 3, 2}, {1, 0, 0}, {1, 1, 0}, {1, 1, 1}, {1, 2, 0}, {1, 2, 1}, {1, 2, 2},
+    {1, 3, 0}, {1, 3, 1}, {1, 3, 2}, {1, 3, 3}};
 
 template <bool AS, bool BS>
 __device__ __forceinline__ f32x4 mm(f32x4 acc, u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl) {
@@ -96,7 +111,14 @@ __device__ __forceinline__ f32x4 mm(f32x4 acc, u32x4 ah, u32x4 al, u32x4 bh, u32
   return acc;
 }
 
-// hi/lo fragment pair from a bf16 array pair (lo array at +lo_off elements).
+// acc += (ah + al)(bh + bl) without the lo*lo term, 16x16x16
+__device__ __forceinline__ f32x4 mm3k16(f32x4 acc, u32x2 ah, u32x2 al, u32x2 bh, u32x2 bl) {
+  acc = mma16k16(ah, bh, acc);
+  acc = mma16k16(ah, bl, acc);
+  acc = mma16k16(al, bh, acc);
+  return acc;
+}
+
 template <bool SPLIT>
 __device__ __forceinline__ void frag2(const bf16_t* base, int lo_off, int ld, int row0, int k0,
                                       u32x4& hi, u32x4& lo) {
@@ -105,87 +127,160 @@ __device__ __forceinline__ void frag2(const bf16_t* base, int lo_off, int ld, in
   else lo = hi;
 }
 
-// A fragment of T diag(colscale) (negated if NEG), split hi/lo: rows row0.., k0..
-template <bool NEG>
-__device__ __forceinline__ void frag_t(const float* sT, const float* colscale, int row0, int k0,
-                                       u32x4& hi, u32x4& lo) {
-  const int l = lane_id();
-  const float* src = sT + (row0 + (l & 15)) * LDF + k0 + 8 * (l >> 4);
-  const float* cs = colscale + k0 + 8 * (l >> 4);
-  float x[8];
-  const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
-  const float4 ca = *(const float4*)cs, cb = *(const float4*)(cs + 4);
-  x[0] = a.x * ca.x; x[1] = a.y * ca.y; x[2] = a.z * ca.z; x[3] = a.w * ca.w;
-  x[4] = b.x * cb.x; x[5] = b.y * cb.y; x[6] = b.z * cb.z; x[7] = b.w * cb.w;
-  if (NEG) {
+// unpack 8 input values (bf16 or fp32) from raw prefetch words
+template <bool F32>
+__device__ __forceinline__ void unpack8(const u32x4* w, float* x) {
+  if constexpr (F32) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = -x[e];
+    for (int e = 0; e < 4; ++e) {
+      x[e] = __uint_as_float(w[0][e]);
+      x[4 + e] = __uint_as_float(w[1][e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __uint_as_float(w[0][e] << 16);
+      x[2 * e + 1] = __uint_as_float(w[0][e] & 0xffff0000u);
+    }
   }
-  split8(x, hi, lo);
 }
 
-// Store 8 values as bf16 (and their lo parts) into a [token][dk] row and a
-// [dk][token] column.
-template <bool SPLIT>
-__device__ __forceinline__ void stage_row(bf16_t* row_hi, int row_lo_off, bf16_t* colT,
-                                          int colT_lo_off, const float* x) {
-  bf16_t h[8], l8[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    h[e] = f2bf(x[e]);
-    l8[e] = f2bf(x[e] - bf2f(h[e]));
+template <bool F32>
+__device__ __forceinline__ void load_raw(const void* base, long long elem, u32x4* w) {
+  if constexpr (F32) {
+    const u32x4* p = (const u32x4*)((const float*)base + elem);
+    w[0] = p[0];
+    w[1] = p[1];
+  } else {
+    w[0] = *(const u32x4*)((const bf16_t*)base + elem);
   }
-  if (row_hi) {
-    *(u32x4*)row_hi = u32x4{pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7])};
-    if constexpr (SPLIT)
-      *(u32x4*)(row_hi + row_lo_off) =
-          u32x4{pack2(l8[0], l8[1]), pack2(l8[2], l8[3]), pack2(l8[4], l8[5]), pack2(l8[6], l8[7])};
+}
+
+// 8 values -> packed bf16 words (hi, or the lo parts)
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+  return u32x4{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]),
+               pack_bf16(x[6], x[7])};
+}
+__device__ __forceinline__ u32x4 pack8_lo(const float* x) {
+  return u32x4{pack_bf16(lo_part(x[0]), lo_part(x[1])), pack_bf16(lo_part(x[2]), lo_part(x[3])),
+               pack_bf16(lo_part(x[4]), lo_part(x[5])), pack_bf16(lo_part(x[6]), lo_part(x[7]))};
+}
+
+// write 8 values of one token into a [token][.] row and/or the transposed [.][token] column
+template <bool SPLIT>
+__device__ __forceinline__ void stage8(bf16_t* row, int row_lo, bf16_t* colT, int colT_lo,
+                                       const float* x) {
+  const u32x4 h = pack8(x);
+  u32x4 lo{};
+  if constexpr (SPLIT) lo = pack8_lo(x);
+  if (row) {
+    *(u32x4*)row = h;
+    if constexpr (SPLIT) *(u32x4*)(row + row_lo) = lo;
   }
   if (colT) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      colT[e * LDT] = h[e];
-      if constexpr (SPLIT) colT[e * LDT + colT_lo_off] = l8[e];
-    }
-  }
-}
-
-template <typename T_>
-__device__ __forceinline__ void load8(const T_* p, float* x) {
-  if constexpr (sizeof(T_) == 2) {
-    const u32x4 w = *(const u32x4*)p;
-#pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[2 * e] = bf2f((bf16_t)(w[e] & 0xffffu));
-      x[2 * e + 1] = bf2f((bf16_t)(w[e] >> 16));
+      colT[(2 * e) * LDT] = (bf16_t)(h[e] & 0xffffu);
+      colT[(2 * e + 1) * LDT] = (bf16_t)(h[e] >> 16);
+      if constexpr (SPLIT) {
+        colT[(2 * e) * LDT + colT_lo] = (bf16_t)(lo[e] & 0xffffu);
+        colT[(2 * e + 1) * LDT + colT_lo] = (bf16_t)(lo[e] >> 16);
+      }
     }
-  } else {
-    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
   }
 }
 
-template <int DK, int NWC, int MODE>
-__global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
-  using Q_ = Cfg<DK, NWC, MODE>;
-  constexpr int NT = Q_::NT, BV = Q_::BV, LDK = Q_::LDK;
+// Per-thread register prefetch of one chunk's inputs.
+template <int DK, int MODE>
+struct Prefetch {
+  using Q_ = Cfg<DK, MODE>;
+  u32x4 kq[Q_::NI_KQ][Q_::RAWW];
+  u32x4 v[Q_::NI_V][Q_::RAWW];
+  float g0, g1;  // wave 0: g and beta (core) or a and b (layer) of token t0 + lane
+};
+
+template <int DK, int MODE>
+__device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE>& pf,
+                                         long long t0, int nvalid, int hk, int h, int col0) {
+  using Q_ = Cfg<DK, MODE>;
+  constexpr bool F32 = MODE == MODE_F32;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < Q_::NI_KQ; ++k) {
+    const int it = tid + k * NT;
+    const int which = it / (C * Q_::SEGS);  // 0 = k, 1 = q
+    const int r = (it / Q_::SEGS) % C, seg = it % Q_::SEGS;
+    if (r < nvalid) {
+      const long long tok = t0 + r;
+      if constexpr (MODE == MODE_LAYER) {
+        const int ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
+        load_raw<false>(p.mixed_qkv, tok * p.conv_dim + ch, pf.kq[k]);
+      } else {
+        const void* base = which == 0 ? p.k : p.q;
+        const long long ld = which == 0 ? p.k_ld : p.q_ld;
+        load_raw<F32>(base, tok * ld + (long long)hk * DK + seg * 8, pf.kq[k]);
+      }
+    } else {
+#pragma unroll
+      for (int w = 0; w < Q_::RAWW; ++w) pf.kq[k][w] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < Q_::NI_V; ++k) {
+    const int it = tid + k * NT;
+    const int r = it / (BV / 8), seg = it % (BV / 8);
+    if (r < nvalid) {
+      const long long tok = t0 + r;
+      if constexpr (MODE == MODE_LAYER)
+        load_raw<false>(p.mixed_qkv,
+                        tok * p.conv_dim + 2 * p.Hk * DK + (long long)h * p.DV + col0 + seg * 8,
+                        pf.v[k]);
+      else
+        load_raw<F32>(p.v, tok * p.v_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
+    } else {
+#pragma unroll
+      for (int w = 0; w < Q_::RAWW; ++w) pf.v[k][w] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  pf.g0 = 0.f;
+  pf.g1 = 0.f;
+  if (tid < 64 && tid < nvalid) {
+    const long long idx = (t0 + tid) * p.Hv + h;
+    if constexpr (MODE == MODE_LAYER) {
+      pf.g0 = bf2f(((const bf16_t*)p.a)[idx]);
+      pf.g1 = bf2f(((const bf16_t*)p.b)[idx]);
+    } else {
+      pf.g0 = p.g[idx];
+      pf.g1 = p.beta[idx];
+    }
+  }
+}
+
+template <int DK, int MODE>
+__global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
+  using Q_ = Cfg<DK, MODE>;
+  constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
-  using InT = typename std::conditional<MODE == MODE_F32, float, bf16_t>::type;
+  constexpr bool F32 = MODE == MODE_F32;
   __shared__ __align__(16) unsigned char smem[Q_::TOTAL];
   bf16_t* sK = (bf16_t*)(smem + Q_::OFF_K);
   bf16_t* sQ = (bf16_t*)(smem + Q_::OFF_Q);
   bf16_t* sKT = (bf16_t*)(smem + Q_::OFF_KT);
   bf16_t* sVT = (bf16_t*)(smem + Q_::OFF_VT);
-  float* sT = (float*)(smem + Q_::OFF_T);
+  bf16_t* sLo = (bf16_t*)(smem + Q_::OFF_LO);
+  float* sLd = (float*)(smem + Q_::OFF_LD);
+  bf16_t* sTd = (bf16_t*)(smem + Q_::OFF_TD);
   bf16_t* sP = (bf16_t*)(smem + Q_::OFF_P);
-  float* sG = (float*)(smem + Q_::OFF_SC);       // cumulative log decay G
-  float* sBeta = sG + C;                          // beta
-  float* sBE = sG + 2 * C;                        // beta e^G
-  float* sEG = sG + 3 * C;                        // e^G
-  float* sEL = sG + 4 * C;                        // e^{G_last - G}
-  float* sX = (float*)(smem + Q_::OFF_W);         // T-merge temp (phase A only)
+  float* sG = (float*)(smem + Q_::OFF_SC);  // cumulative log decay G
+  float* sBeta = sG + C;                     // beta
+  float* sBE = sG + 2 * C;                   // beta e^G
+  float* sEG = sG + 3 * C;                   // e^G
+  float* sEL = sG + 4 * C;                   // e^{G_last - G}
+  bf16_t* sHist = (bf16_t*)(smem + Q_::OFF_HIST);  // layer: raw inputs of the 3 previous tokens
+  float* sNP = (float*)(smem + Q_::OFF_NP);        // layer: [token][wave] sums of o^2
   constexpr int K_LO = C * LDK, KT_LO = DK * LDT, VT_LO = BV * LDT, P_LO = C * LDT;
+  constexpr int LO_LO = C * LDT, TD_LO = C * LDD;
+  constexpr int HW = 2 * DK + BV;  // channels of one history row
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int nb = p.nb;
@@ -195,9 +290,8 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
   const int gqa = p.Hv / p.Hk;
   const int hk = h / gqa;
   const int DV = p.DV;
-  const int col0 = blk * BV;             // first state column of this workgroup
+  const int col0 = blk * BV;
 
-  // sequence token range [s0, s1) in global token indices
   long long s0, s1;
   if (p.cu_seqlens) {
     // clamp to [0, T] so a malformed offsets array can never index out of bounds
@@ -210,9 +304,24 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
   }
   const int nchunks = (int)((s1 - s0 + C - 1) / C);
 
-  // zero T and P once: their strictly-upper 16x16 tiles are never written
-  for (int i = tid; i < C * LDF; i += NT) sT[i] = 0.f;
-  for (int i = tid; i < (OS ? 2 : 1) * C * LDT; i += NT) sP[i] = 0;
+  // zero P once: its strictly-upper 16x16 tiles are never written
+  for (int i = tid; i < (OS ? 2 : 1) * C * LDT / 2; i += NT) ((uint32_t*)sP)[i] = 0u;
+  if constexpr (MODE == MODE_LAYER) {
+    // conv history before the first token: conv_state_in (oldest tap first) or zeros
+    const int K = p.conv_k;
+    for (int it = tid; it < 3 * HW; it += NT) {
+      const int tap = it / HW, ci = it % HW;  // tap 0 holds time s0 - 3
+      int ch;
+      if (ci < DK) ch = hk * DK + ci;
+      else if (ci < 2 * DK) ch = p.Hk * DK + hk * DK + (ci - DK);
+      else ch = 2 * p.Hk * DK + h * DV + col0 + (ci - 2 * DK);
+      bf16_t val = 0;
+      const int slot = (K - 1) - (3 - tap);  // cache slot of time s0 - (3 - tap)
+      if (p.conv_state_in && slot >= 0)
+        val = ((const bf16_t*)p.conv_state_in)[((size_t)n * p.conv_dim + ch) * (K - 1) + slot];
+      sHist[it] = val;
+    }
+  }
 
   // state slice S[dk][16w + (0..15)] in MFMA C layout: S[t][v] = S[16t + 4lq + v][16w + lr]
   f32x4 S[DK / 16];
@@ -221,38 +330,62 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) S[t][v] = p.initial_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV];
+      for (int v = 0; v < 4; ++v)
+        S[t][v] = p.initial_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV];
   } else {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) S[t] = zero4();
   }
 
-  const InT* qg = (const InT*)p.q;
-  const InT* kg = (const InT*)p.k;
-  const InT* vg = (const InT*)p.v;
   bf16_t* wscr = (bf16_t*)(smem + Q_::OFF_W + wave * Q_::WS);
+  bf16_t* wS = wscr;                  // S^T [16][LDK] (hi, lo)
+  bf16_t* wU = wscr;                  // U^T [16][LDT] hi, then lo
+  bf16_t* wVt = wscr + 2 * 16 * LDT;  // Vt^T [16][LDT] hi, then lo
+  constexpr int WS_LO = 16 * LDK, W_LO = 16 * LDT;
+
+  Prefetch<DK, MODE> pf;
+  if (nchunks > 0) prefetch<DK, MODE>(p, pf, s0, (int)((s1 - s0) < C ? (s1 - s0) : C), hk, h, col0);
 
   for (int j = 0; j < nchunks; ++j) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
-    __syncthreads();  // previous chunk's readers are done with the shared arrays
+    __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
-    // ------------------------------------------------------------ A1: stage K, Q, V, gates
-    {
-      constexpr int SEGS = DK / 8;
-      for (int it = tid; it < C * SEGS * 2; it += NT) {
-        const int which = it / (C * SEGS);  // 0 = k, 1 = q
+    // ------------------------------------------------------------ A1: stage the chunk
+    if (wave == 0) {
+      float g = pf.g0, bt = pf.g1;
+      if constexpr (MODE == MODE_LAYER) {
+        // gates, deltanet.py:248-250: beta in bf16, g in fp32
+        if (l < nvalid) {
+          g = -expf(p.A_log[h]) * softplusf_(pf.g0 + p.dt_bias[h]);
+          bt = round_bf(sigmoidf_(pf.g1));
+        } else {
+          g = 0.f;
+          bt = 0.f;
+        }
+      }
+      float G = g;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float y = __shfl_up(G, o, 64);
+        if (l >= o) G += y;
+      }
+      const float Gl = __shfl(G, 63, 64);
+      const float eg = __expf(G);
+      sG[l] = G;
+      sBeta[l] = bt;
+      sBE[l] = bt * eg;
+      sEG[l] = eg;
+      sEL[l] = __expf(Gl - G);
+    }
+    if constexpr (MODE != MODE_LAYER) {
+#pragma unroll
+      for (int k = 0; k < Q_::NI_KQ; ++k) {
+        const int it = tid + k * NT;
+        const int which = it / (C * SEGS);
         const int r = (it / SEGS) % C, seg = it % SEGS;
         float x[8];
-        if (r < nvalid) {
-          const long long tok = t0 + r;
-          const InT* src = which == 0 ? kg + tok * p.k_ld + (long long)hk * DK + seg * 8
-                                      : qg + tok * p.q_ld + (long long)hk * DK + seg * 8;
-          load8(src, x);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.f;
-        }
+        unpack8<F32>(pf.kq[k], x);
         if (p.qk_l2norm) {
           float ss = 0.f;
 #pragma unroll
@@ -262,50 +395,133 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = IS ? x[e] * inv : round_bf(x[e] * inv);
         }
-        if (which == 0)
-          stage_row<IS>(sK + r * LDK + seg * 8, K_LO, sKT + (seg * 8) * LDT + r, KT_LO, x);
-        else
-          stage_row<IS>(sQ + r * LDK + seg * 8, K_LO, nullptr, 0, x);
+        if (which == 0) stage8<IS>(sK + r * LDK + seg * 8, K_LO, sKT + seg * 8 * LDT + r, KT_LO, x);
+        else stage8<IS>(sQ + r * LDK + seg * 8, K_LO, nullptr, 0, x);
       }
-      constexpr int VSEGS = BV / 8;
-      for (int it = tid; it < C * VSEGS; it += NT) {
-        const int r = it / VSEGS, seg = it % VSEGS;
+#pragma unroll
+      for (int k = 0; k < Q_::NI_V; ++k) {
+        const int it = tid + k * NT;
+        const int r = it / (BV / 8), seg = it % (BV / 8);
         float x[8];
-        if (r < nvalid) {
-          load8(vg + (t0 + r) * p.v_ld + (long long)h * DV + col0 + seg * 8, x);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.f;
-        }
-        stage_row<IS>(nullptr, 0, sVT + (seg * 8) * LDT + r, VT_LO, x);
+        unpack8<F32>(pf.v[k], x);
+        stage8<IS>(nullptr, 0, sVT + seg * 8 * LDT + r, VT_LO, x);
       }
-      if (wave == 0) {
-        float g = 0.f, bt = 0.f;
-        if (l < nvalid) {
-          g = p.g[(t0 + l) * p.Hv + h];
-          bt = p.beta[(t0 + l) * p.Hv + h];
-        }
-        float G = g;
+    } else {
+      // raw rows: q -> sQ, k -> sK, v -> P (as [token][col]); the conv reads them next
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const float y = __shfl_up(G, o, 64);
-          if (l >= o) G += y;
+      for (int k = 0; k < Q_::NI_KQ; ++k) {
+        const int it = tid + k * NT;
+        const int which = it / (C * SEGS);
+        const int r = (it / SEGS) % C, seg = it % SEGS;
+        *(u32x4*)((which == 0 ? sK : sQ) + r * LDK + seg * 8) = pf.kq[k][0];
+      }
+#pragma unroll
+      for (int k = 0; k < Q_::NI_V; ++k) {
+        const int it = tid + k * NT;
+        const int r = it / (BV / 8), seg = it % (BV / 8);
+        *(u32x4*)(sP + r * LDT + seg * 8) = pf.v[k][0];
+      }
+      __syncthreads();
+      // causal depthwise conv (deltanet.py:35-50) + SiLU, each rounded to bf16 like the
+      // reference's bf16 ops; weights cast to bf16 (deltanet.py:243)
+      const int K = p.conv_k;
+      float ykq[Q_::NI_KQ][8], yv[Q_::NI_V][8];
+#pragma unroll
+      for (int k = 0; k < Q_::NI_KQ + Q_::NI_V; ++k) {
+        const bool isv = k >= Q_::NI_KQ;
+        const int it = tid + (isv ? k - Q_::NI_KQ : k) * NT;
+        int r, seg, ci, ch, ld;
+        const bf16_t* rows;
+        if (!isv) {
+          const int which = it / (C * SEGS);
+          r = (it / SEGS) % C;
+          seg = it % SEGS;
+          rows = which == 0 ? sK : sQ;
+          ld = LDK;
+          ci = (which == 0 ? DK : 0) + seg * 8;
+          ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
+        } else {
+          r = it / (BV / 8);
+          seg = it % (BV / 8);
+          rows = sP;
+          ld = LDT;
+          ci = 2 * DK + seg * 8;
+          ch = 2 * p.Hk * DK + h * DV + col0 + seg * 8;
         }
-        const float Gl = __shfl(G, 63, 64);
-        const float eg = expf(G);
-        sG[l] = G;
-        sBeta[l] = bt;
-        sBE[l] = bt * eg;
-        sEG[l] = eg;
-        sEL[l] = expf(Gl - G);
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+        for (int jt = 0; jt < K; ++jt) {
+          const int rr = r - (K - 1) + jt;  // token row within the chunk
+          float xv[8];
+          if (rr >= 0) {
+            const u32x4 w = *(const u32x4*)(rows + rr * ld + seg * 8);
+            unpack8<false>(&w, xv);
+          } else if (rr >= -3) {
+            const u32x4 w = *(const u32x4*)(sHist + (3 + rr) * HW + ci);
+            unpack8<false>(&w, xv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = 0.f;
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += round_bf(p.conv_w[(size_t)(ch + e) * K + jt]) * xv[e];
+        }
+        float* y = isv ? yv[k - Q_::NI_KQ] : ykq[k];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = r < nvalid ? round_bf(siluf_(round_bf(acc[e]))) : 0.f;
+      }
+      __syncthreads();
+      // raw V is no longer needed in P: restore the zeros of P's strictly-upper tiles
+      for (int i = tid; i < C * LDT / 2; i += NT) ((uint32_t*)sP)[i] = 0u;
+      // history for the next chunk: raw inputs of tokens 61..63 (still in the prefetch)
+#pragma unroll
+      for (int k = 0; k < Q_::NI_KQ; ++k) {
+        const int it = tid + k * NT;
+        const int which = it / (C * SEGS);
+        const int r = (it / SEGS) % C, seg = it % SEGS;
+        if (r >= C - 3) *(u32x4*)(sHist + (r - (C - 3)) * HW + (which == 0 ? DK : 0) + seg * 8) = pf.kq[k][0];
+      }
+#pragma unroll
+      for (int k = 0; k < Q_::NI_V; ++k) {
+        const int it = tid + k * NT;
+        const int r = it / (BV / 8), seg = it % (BV / 8);
+        if (r >= C - 3) *(u32x4*)(sHist + (r - (C - 3)) * HW + 2 * DK + seg * 8) = pf.v[k][0];
+      }
+#pragma unroll
+      for (int k = 0; k < Q_::NI_KQ; ++k) {
+        const int it = tid + k * NT;
+        const int which = it / (C * SEGS);
+        const int r = (it / SEGS) % C, seg = it % SEGS;
+        float* x = ykq[k];
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+        ss = group_sum<SEGS>(ss);
+        const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = round_bf(x[e] * inv);
+        if (which == 0) stage8<false>(sK + r * LDK + seg * 8, 0, sKT + seg * 8 * LDT + r, 0, x);
+        else stage8<false>(sQ + r * LDK + seg * 8, 0, nullptr, 0, x);
+      }
+#pragma unroll
+      for (int k = 0; k < Q_::NI_V; ++k) {
+        const int it = tid + k * NT;
+        const int r = it / (BV / 8), seg = it % (BV / 8);
+        stage8<false>(nullptr, 0, sVT + seg * 8 * LDT + r, 0, yv[k]);
       }
     }
     __syncthreads();
 
+    // issue the next chunk's loads; they land during this chunk's compute
+    if (j + 1 < nchunks) {
+      const long long tn = t0 + C;
+      prefetch<DK, MODE>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), hk, h, col0);
+    }
+
     // ------------------------------------------------------------ A2: K K^T -> L, Q K^T -> P
     for (int tile = wave; tile < 20; tile += NWC) {
-      const bool qk = tile >= 10;
-      const int bi = kTri[tile % 10][0], bj = kTri[tile % 10][1];
+      const int qk = kTiles[tile][0], bi = kTiles[tile][1], bj = kTiles[tile][2];
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
@@ -319,159 +535,149 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = 16 * bi + 4 * lq + v;
-        const float dec = expf(sG[i] - Gm);
+        const float dec = __expf(sG[i] - Gm);
         if (!qk) {
-          sT[i * LDF + m] = (i > m) ? sBeta[i] * acc[v] * dec : 0.f;
+          const float lv = (i > m) ? sBeta[i] * acc[v] * dec : 0.f;
+          if (bi == bj) {
+            sLd[i * LDD + lr] = lv;
+          } else {
+            sLo[i * LDT + m] = f2bf(lv);
+            sLo[LO_LO + i * LDT + m] = f2bf(lo_part(lv));
+          }
         } else {
           const float pv = (i >= m) ? p.scale * acc[v] * dec : 0.f;
-          const bf16_t ph = f2bf(pv);
-          sP[i * LDT + m] = ph;
-          if constexpr (OS) sP[P_LO + i * LDT + m] = f2bf(pv - bf2f(ph));
+          sP[i * LDT + m] = f2bf(pv);
+          if constexpr (OS) sP[P_LO + i * LDT + m] = f2bf(lo_part(pv));
         }
       }
     }
-    __syncthreads();
 
-    // ------------------------------------------------------------ A3: T = (I + L)^-1
-    // diagonal 16x16 blocks by forward substitution, one column per lane
-    if (wave < 4 && l < 16) {
-      const int b0 = 16 * wave, c = l;
-      float x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float acc = (i == c) ? 1.f : 0.f;
-#pragma unroll
-        for (int m = 0; m < i; ++m) acc -= sT[(b0 + i) * LDF + b0 + m] * x[m];
-        x[i] = acc;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sT[(b0 + i) * LDF + b0 + c] = x[i];
-    }
-    __syncthreads();
-    // 16 -> 32: T_hl = -T_hh L_hl T_ll for (h, l) = (1, 0) and (3, 2)
-    for (int it = tid; it < 512; it += NT) {
-      const int pr = it >> 8, i = (it >> 4) & 15, c = it & 15;
-      const int lo = 32 * pr, hi = lo + 16;
-      float acc = 0.f;
-      for (int m = c; m < 16; ++m) acc += sT[(hi + i) * LDF + lo + m] * sT[(lo + m) * LDF + lo + c];
-      sX[pr * 16 * 17 + i * 17 + c] = acc;
-    }
-    __syncthreads();
-    for (int it = tid; it < 512; it += NT) {
-      const int pr = it >> 8, i = (it >> 4) & 15, c = it & 15;
-      const int lo = 32 * pr, hi = lo + 16;
-      float acc = 0.f;
-      for (int m = 0; m <= i; ++m) acc += sT[(hi + i) * LDF + hi + m] * sX[pr * 16 * 17 + m * 17 + c];
-      sT[(hi + i) * LDF + lo + c] = -acc;
-    }
-    __syncthreads();
-    // 32 -> 64: T_[32:64][0:32] = -T_[32:64][32:64] L_[32:64][0:32] T_[0:32][0:32]
-    for (int it = tid; it < 1024; it += NT) {
-      const int i = it >> 5, c = it & 31;
-      float acc = 0.f;
-      for (int m = c; m < 32; ++m) acc += sT[(32 + i) * LDF + m] * sT[m * LDF + c];
-      sX[i * 33 + c] = acc;
-    }
-    __syncthreads();
-    for (int it = tid; it < 1024; it += NT) {
-      const int i = it >> 5, c = it & 31;
-      float acc = 0.f;
-      for (int m = 0; m <= i; ++m) acc += sT[(32 + i) * LDF + 32 + m] * sX[m * 33 + c];
-      sT[(32 + i) * LDF + c] = -acc;
-    }
-    __syncthreads();
-
-    // ------------------------------------------------------------ B: this wave's 16 columns
-    bf16_t* wS = wscr;                    // S^T [16][LDK] (hi, lo)
-    bf16_t* wKS = wscr;                   // (K S)^T [16][LDT]
-    bf16_t* wVN = wscr;                   // V_new^T [16][LDT] (hi, lo if OS)
-    bf16_t* wVt = wscr + (OS ? 2 : 1) * 16 * LDT;  // Vt^T hi, then lo
-    constexpr int WS_LO = 16 * LDK, W_LO = 16 * LDT;
-
-    // B0: S^T into the scratch as the B operand of K S and Q S
+    // ------------------------------------------------------------ B1: K S, Q S, right-hand side
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {
       if constexpr (IS) store_ct_split(wS, wS + WS_LO, LDK, 16 * t, 0, S[t]);
       else store_ct_bf16(wS, LDK, 16 * t, 0, S[t]);
     }
     wave_lds_fence();
-    // B1/B2: K S and Q S for the 4 token tiles
-    f32x4 KS[4], QS[4];
+    f32x4 R[4], QS[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      KS[i] = zero4();
+      f32x4 ks = zero4();
       QS[i] = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
         u32x4 bh, bl, ah, al;
         frag2<IS>(wS, WS_LO, LDK, 0, 32 * s, bh, bl);
         frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s, ah, al);
-        KS[i] = mm<IS, IS>(KS[i], ah, al, bh, bl);
+        ks = mm<IS, IS>(ks, ah, al, bh, bl);
         frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s, ah, al);
         QS[i] = mm<IS, IS>(QS[i], ah, al, bh, bl);
       }
+      // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
+      const int r0 = 16 * i + 4 * lq;
+      const u32x2 vw = *(const u32x2*)(sVT + (16 * wave + lr) * LDT + r0);
+      float vv[4] = {__uint_as_float(vw[0] << 16), __uint_as_float(vw[0] & 0xffff0000u),
+                     __uint_as_float(vw[1] << 16), __uint_as_float(vw[1] & 0xffff0000u)};
+      if constexpr (IS) {
+        const u32x2 vl = *(const u32x2*)(sVT + VT_LO + (16 * wave + lr) * LDT + r0);
+        vv[0] += __uint_as_float(vl[0] << 16);
+        vv[1] += __uint_as_float(vl[0] & 0xffff0000u);
+        vv[2] += __uint_as_float(vl[1] << 16);
+        vv[3] += __uint_as_float(vl[1] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) R[i][v] = sBeta[r0 + v] * vv[v] - sBE[r0 + v] * ks[v];
     }
-    wave_lds_fence();
-    // B3: (K S)^T into the scratch (over S^T, whose reads are complete)
+    __syncthreads();  // L and P complete
+
+    // ------------------------------------------------------------ A3: diagonal-block inverses
+    // T_bb = (I + L_bb)^-1 by forward substitution, one column per lane
+    if (l < 16) {
+      const int b0 = 16 * wave, c = l;
+      float x[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (IS) store_ct_split(wKS, wKS + W_LO, LDT, 16 * i, 0, KS[i]);
-      else store_ct_bf16(wKS, LDT, 16 * i, 0, KS[i]);
-    }
-    wave_lds_fence();
-    // B4: V_new = T diag(beta) V - T diag(beta e^G) (K S); T is lower triangular
-    f32x4 VN[4];
+      for (int i = 0; i < 16; ++i) {
+        float acc = (i == c) ? 1.f : 0.f;
+        const float* row = sLd + (b0 + i) * LDD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      VN[i] = zero4();
+        for (int m = 0; m < i; ++m) acc -= row[m] * x[m];
+        x[i] = acc;
+      }
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 1 && i < 2) continue;
-        u32x4 th, tl, bh, bl;
-        frag_t<false>(sT, sBeta, 16 * i, 32 * s, th, tl);
-        frag2<IS>(sVT + (16 * wave) * LDT, VT_LO, LDT, 0, 32 * s, bh, bl);
-        VN[i] = mm<true, IS>(VN[i], th, tl, bh, bl);
-        frag_t<true>(sT, sBE, 16 * i, 32 * s, th, tl);
-        frag2<IS>(wKS, W_LO, LDT, 0, 32 * s, bh, bl);
-        VN[i] = mm<true, IS>(VN[i], th, tl, bh, bl);
+      for (int i = 0; i < 16; ++i) {
+        sTd[(b0 + i) * LDD + c] = f2bf(x[i]);
+        sTd[TD_LO + (b0 + i) * LDD + c] = f2bf(lo_part(x[i]));
       }
     }
-    wave_lds_fence();
-    // B5: V_new^T and Vt^T = (diag(e^{G_last - G}) V_new)^T into the scratch
+    __syncthreads();
+
+    // ------------------------------------------------------------ B2: the solve, per wave
+    // (I + L) U = R by block forward substitution; U^T stays in the scratch (hi, lo)
+    f32x4 U[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      f32x4 acc = R[b];
+#pragma unroll
+      for (int jb = 0; jb < b; ++jb) {
+        // acc -= L_b,jb U_jb: the A operand is negated (a sign flip is exact in bf16)
+        const u32x2 ah = frag4_bf16(sLo, LDT, 16 * b, 16 * jb) ^ 0x80008000u;
+        const u32x2 al = frag4_bf16(sLo + LO_LO, LDT, 16 * b, 16 * jb) ^ 0x80008000u;
+        const u32x2 bh = frag4_bf16(wU, LDT, 0, 16 * jb);
+        const u32x2 bl = frag4_bf16(wU + W_LO, LDT, 0, 16 * jb);
+        acc = mm3k16(acc, ah, al, bh, bl);
+      }
+      store_ct_split(wU, wU + W_LO, LDT, 16 * b, 0, acc);
+      wave_lds_fence();
+      const u32x2 th = frag4_bf16(sTd, LDD, 16 * b, 0);
+      const u32x2 tl = frag4_bf16(sTd + TD_LO, LDD, 16 * b, 0);
+      const u32x2 rh = frag4_bf16(wU, LDT, 0, 16 * b);
+      const u32x2 rl = frag4_bf16(wU + W_LO, LDT, 0, 16 * b);
+      U[b] = mm3k16(zero4(), th, tl, rh, rl);
+      wave_lds_fence();
+      store_ct_split(wU, wU + W_LO, LDT, 16 * b, 0, U[b]);
+      wave_lds_fence();
+    }
+    // Vt = diag(e^{G_last - G}) V_new for the state update
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (OS) store_ct_split(wVN, wVN + W_LO, LDT, 16 * i, 0, VN[i]);
-      else store_ct_bf16(wVN, LDT, 16 * i, 0, VN[i]);
       f32x4 vt;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) vt[v] = VN[i][v] * sEL[16 * i + 4 * lq + v];
+      for (int v = 0; v < 4; ++v) vt[v] = U[i][v] * sEL[16 * i + 4 * lq + v];
       store_ct_split(wVt, wVt + W_LO, LDT, 16 * i, 0, vt);
     }
     wave_lds_fence();
-    // B6: O = e^G (Q S) scale + P V_new
+
+    // ------------------------------------------------------------ B3: O = scale e^G (Q S) + P V_new
+    f32x4 OUT[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 o;
+      f32x4& o = OUT[i];
 #pragma unroll
       for (int v = 0; v < 4; ++v) o[v] = p.scale * sEG[16 * i + 4 * lq + v] * QS[i][v];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        if (s == 1 && i < 2) continue;
+        if (s == 1 && i < 2) continue;  // P is lower triangular
         u32x4 ah, al, bh, bl;
         frag2<OS>(sP, P_LO, LDT, 16 * i, 32 * s, ah, al);
-        frag2<OS>(wVN, W_LO, LDT, 0, 32 * s, bh, bl);
+        frag2<OS>(wU, W_LO, LDT, 0, 32 * s, bh, bl);
         o = mm<OS, OS>(o, ah, al, bh, bl);
       }
       if constexpr (MODE != MODE_LAYER) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int r = 16 * i + 4 * lq + v;
-          if (r < nvalid)
-            p.o[((t0 + r) * p.Hv + h) * (long long)DV + col0 + 16 * wave + lr] = o[v];
+          if (r < nvalid) p.o[((t0 + r) * p.Hv + h) * (long long)DV + col0 + 16 * wave + lr] = o[v];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float ss = group_sum<16>(o[v] * o[v]);
+          if (lr == 0) sNP[(16 * i + 4 * lq + v) * NWC + wave] = ss;
         }
       }
     }
-    // B7: S <- e^{G_last} S + K^T Vt
+
+    // ------------------------------------------------------------ B4: S <- e^{G_last} S + K^T Vt
     const float gl = sEG[C - 1];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {
@@ -485,49 +691,104 @@ __global__ __launch_bounds__(64 * NWC) void chunk_kernel(ChunkParams p) {
         S[t] = mm<IS, true>(S[t], ah, al, bh, bl);
       }
     }
+
+    if constexpr (MODE == MODE_LAYER) {
+      // gated RMSNorm epilogue (deltanet.py:282-293), fp32 like the reference
+      __syncthreads();
+      const int col = col0 + 16 * wave + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int r = 16 * i + 4 * lq + v;
+          if (r < nvalid) {
+            float ss = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < NWC; ++w2) ss += sNP[r * NWC + w2];
+            const size_t idx = ((size_t)(t0 + r) * p.Hv + h) * DV + col;
+            if (nb == 1) {
+              const float rn = rsqrtf(ss / (float)DV + p.eps);
+              const float zz = bf2f(((const bf16_t*)p.z)[idx]);
+              ((bf16_t*)p.out)[idx] = f2bf(p.norm_w[col] * (OUT[i][v] * rn) * siluf_(zz));
+            } else {
+              // unnormalised o in bf16 and this block's share of sum(o^2)
+              ((bf16_t*)p.o_part)[idx] = f2bf(OUT[i][v]);
+              if (wave == 0 && lr == 0) p.ss_part[((size_t)(t0 + r) * p.Hv + h) * nb + blk] = ss;
+            }
+          }
+        }
+      }
+    }
   }
 
   if (p.final_state) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) p.final_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV] = S[t][v];
+      for (int v = 0; v < 4; ++v)
+        p.final_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV] = S[t][v];
+  }
+
+  if constexpr (MODE == MODE_LAYER) {
+    // conv cache after the prefill: the last K-1 raw inputs of the sequence.  q/k
+    // channels are written by the first value head of their key head only.
+    if (p.conv_state_out) {
+      const int K = p.conv_k;
+      const bool own_qk = (h % gqa) == 0 && blk == 0;
+      for (int it = tid; it < HW * (K - 1); it += NT) {
+        const int ci = it / (K - 1), jj = it % (K - 1);
+        if (ci < 2 * DK && !own_qk) continue;
+        int ch;
+        if (ci < DK) ch = hk * DK + ci;
+        else if (ci < 2 * DK) ch = p.Hk * DK + hk * DK + (ci - DK);
+        else ch = 2 * p.Hk * DK + h * DV + col0 + (ci - 2 * DK);
+        const long long t = s1 - (K - 1) + jj;
+        bf16_t val = 0;
+        if (t >= s0) {
+          val = ((const bf16_t*)p.mixed_qkv)[t * p.conv_dim + ch];
+        } else if (p.conv_state_in) {
+          const int slot = (K - 1) - (int)(s0 - t);
+          val = ((const bf16_t*)p.conv_state_in)[((size_t)n * p.conv_dim + ch) * (K - 1) + slot];
+        }
+        ((bf16_t*)p.conv_state_out)[((size_t)n * p.conv_dim + ch) * (K - 1) + jj] = val;
+      }
+    }
   }
 }
 
-template <int DK, int NWC, int MODE>
+template <int DK, int MODE>
 hipError_t launch_cfg(const ChunkParams& p, hipStream_t stream) {
   const unsigned grid = (unsigned)(p.N * p.Hv * p.nb);
-  hipLaunchKernelGGL((chunk_kernel<DK, NWC, MODE>), dim3(grid), dim3(64 * NWC), 0, stream, p);
+  hipLaunchKernelGGL((chunk_kernel<DK, MODE>), dim3(grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
 }
 
 }  // namespace
 
-int chunk_block_cols(int dk, int dv, bool f32_inputs) {
-  // columns per workgroup: the whole dv when the LDS budget allows it
-  if (f32_inputs) return dv >= 64 ? 64 : dv;
-  return dv >= 128 ? 128 : dv;
-  (void)dk;
-}
+int chunk_block_cols() { return BV; }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
-  if (f32_inputs) return (dk == 32 || dk == 64) && (dv == 64 || dv == 128);
-  return (dk == 64 || dk == 128) && (dv == 64 || dv == 128);
+  if (dv % BV != 0 || dv > 256) return false;
+  if (f32_inputs) return dk == 32 || dk == 64;
+  return dk == 64 || dk == 128;
 }
 
+bool layer_dims_supported(int dk, int dv) { return chunk_dims_supported(dk, dv, false); }
+
 hipError_t launch_chunk(const ChunkParams& p, bool f32_inputs, hipStream_t stream) {
-  const int bv = p.DV / p.nb;
   if (f32_inputs) {
-    if (bv != 64) return hipErrorInvalidValue;
-    if (p.dk == 64) return launch_cfg<64, 4, MODE_F32>(p, stream);
-    if (p.dk == 32) return launch_cfg<32, 4, MODE_F32>(p, stream);
+    if (p.dk == 64) return launch_cfg<64, MODE_F32>(p, stream);
+    if (p.dk == 32) return launch_cfg<32, MODE_F32>(p, stream);
     return hipErrorInvalidValue;
   }
-  if (p.dk == 128 && bv == 128) return launch_cfg<128, 8, MODE_BF16>(p, stream);
-  if (p.dk == 128 && bv == 64) return launch_cfg<128, 4, MODE_BF16>(p, stream);
-  if (p.dk == 64 && bv == 128) return launch_cfg<64, 8, MODE_BF16>(p, stream);
-  if (p.dk == 64 && bv == 64) return launch_cfg<64, 4, MODE_BF16>(p, stream);
+  if (p.dk == 128) return launch_cfg<128, MODE_BF16>(p, stream);
+  if (p.dk == 64) return launch_cfg<64, MODE_BF16>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_layer(const ChunkParams& p, hipStream_t stream) {
+  if (p.dk == 128) return launch_cfg<128, MODE_LAYER>(p, stream);
+  if (p.dk == 64) return launch_cfg<64, MODE_LAYER>(p, stream);
   return hipErrorInvalidValue;
 }
 

@@ -2,6 +2,7 @@
 //
 // bf16 values travel as raw uint16_t; conversions round to nearest even, which
 // is what a float32 -> bfloat16 cast does in the reference (jnp.astype).
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -13,11 +14,14 @@ typedef uint16_t bf16_t;
 
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16_t)((u >> 16) | 0x40);  // NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+// float -> bf16, round to nearest even (one v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// two floats -> packed bf16 pair (first in the low half), one instruction on gfx950
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)lo, (__bf16)hi});
 }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }

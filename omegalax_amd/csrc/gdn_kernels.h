@@ -57,6 +57,8 @@ struct ChunkParams {
   const void* conv_state_in;   // [N, conv_dim, K-1] bf16 or null
   void* conv_state_out;        // [N, conv_dim, K-1] bf16 or null
   void* out;                   // [tokens, Hv*DV] bf16
+  void* o_part;                // nb > 1: unnormalised o [tokens, Hv, DV] bf16 (workspace)
+  float* ss_part;              // nb > 1: per-block sums of o^2 [tokens, Hv, nb] (workspace)
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
@@ -67,8 +69,15 @@ struct ChunkParams {
 };
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs);
-int chunk_block_cols(int dk, int dv, bool f32_inputs);
+int chunk_block_cols();
 hipError_t launch_chunk(const ChunkParams& p, bool f32_inputs, hipStream_t stream);
+bool layer_dims_supported(int dk, int dv);
+hipError_t launch_layer(const ChunkParams& p, hipStream_t stream);
+
+// Gated RMSNorm over dv split across nb workgroups: out = w * o * rsqrt(sum/dv + eps) * silu(z).
+hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,
+                                const float* norm_w, void* out, long long rows, int dv, int nb,
+                                float eps, hipStream_t stream);
 
 bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();

@@ -1,0 +1,135 @@
+"""GPU parity of the fused layer prefill (conv + gates + chunked rule + gated norm).
+
+Reference semantics: deltanet.py:243-293 (oracle.gdn_prefill_layer).  Tolerances:
+bf16 output 2e-2, fp32 state 1e-3 (max-abs-normalised); the conv cache is raw
+data movement and must match bit for bit.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import gdn_oracle as O
+from omegalax_amd import workloads as W
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+STATE_TOL = 1e-3
+BF16_TOL = 2e-2
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def np_(t):
+    return t.detach().float().cpu().numpy()
+
+
+def gpu_prefill(t, dims, cu=None, S0=None, conv0=None):
+    from omegalax_amd import gdn_prefill
+    out, S, conv = gdn_prefill(
+        t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"], t["dt_bias"], t["norm_w"],
+        num_k_heads=dims["Hk"], head_k_dim=dims["dk"], num_v_heads=dims["Hv"],
+        head_v_dim=dims["dv"],
+        cu_seqlens=None if cu is None else torch.from_numpy(cu).cuda(),
+        initial_state=None if S0 is None else torch.from_numpy(S0).cuda(),
+        conv_state=None if conv0 is None else torch.from_numpy(conv0).cuda().bfloat16(),
+        output_final_state=True)
+    torch.cuda.synchronize()
+    return out, S, conv
+
+
+def ref_prefill(d, dims, cu=None, S0=None, conv0=None):
+    return O.gdn_prefill_layer(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"], d["A_log"],
+                               d["dt_bias"], d["norm_w"], **dims, cu_seqlens=cu,
+                               initial_state=S0, conv_state=conv0)
+
+
+@pytest.mark.parametrize("B,T,Hk,Hv,dk,dv", [
+    (2, 100, 2, 4, 128, 128),   # dv split over two workgroups: epilogue kernel
+    (1, 64, 1, 1, 64, 64),      # one workgroup holds dv: fused norm
+    (2, 3, 1, 2, 64, 64),       # shorter than the conv window
+    (1, 200, 2, 2, 64, 128),
+    (1, 130, 1, 2, 128, 64),
+])
+def test_layer_prefill_matches_oracle(B, T, Hk, Hv, dk, dv):
+    say(f"layer B={B} T={T} Hk={Hk} Hv={Hv} dk={dk} dv={dv}")
+    dims = dict(Hk=Hk, dk=dk, Hv=Hv, dv=dv)
+    d = W.layer_inputs(B, T, Hk, Hv, dk, dv, seed=T + dk)
+    t = W.to_device(d)
+    out, S, conv = gpu_prefill(t, dims)
+    ref, S_ref, conv_ref = ref_prefill(d, dims)
+    assert rel(np_(out), ref) < BF16_TOL
+    assert rel(np_(S), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv), conv_ref)
+
+
+def test_layer_varlen_with_carried_states():
+    say("layer varlen")
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    lens = [70, 0, 2, 129, 64]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    d = W.layer_inputs(1, T, **dims, seed=5)
+    rng = np.random.default_rng(6)
+    N = len(lens)
+    S0 = (0.02 * rng.standard_normal((N, 4, 128, 128))).astype(np.float32)
+    conv_dim = 2 * 2 * 128 + 4 * 128
+    conv0 = O.round_bf16(rng.standard_normal((N, conv_dim, 3)))
+    t = W.to_device(d)
+    out, S, conv = gpu_prefill(t, dims, cu, S0, conv0)
+    ref, S_ref, conv_ref = ref_prefill(d, dims, cu, S0, conv0)
+    assert rel(np_(out), ref) < BF16_TOL
+    assert rel(np_(S), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv), conv_ref)
+
+
+def test_prefill_then_decode_equals_longer_prefill():
+    """prefill(x[:n]) + decode steps x[n], x[n+1], ... == prefill(x) (GPU vs GPU)."""
+    from omegalax_amd import gdn_decode_step
+    say("prefill -> decode handoff")
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    T, n = 70, 66
+    d = W.layer_inputs(2, T, **dims, seed=9)
+    t = W.to_device(d)
+    full, S_full, conv_full = gpu_prefill(t, dims)
+    part = {k_: (v_[:, :n].contiguous() if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+            for k_, v_ in t.items()}
+    _, S, conv = gpu_prefill(part, dims)
+    for step in range(n, T):
+        o = gdn_decode_step(t["mixed_qkv"][:, step].contiguous(), t["z"][:, step].contiguous(),
+                            t["a"][:, step].contiguous(), t["b"][:, step].contiguous(),
+                            t["conv_w"], t["A_log"], t["dt_bias"], t["norm_w"], conv, S,
+                            num_k_heads=2, head_k_dim=128, num_v_heads=4, head_v_dim=128)
+        torch.cuda.synchronize()
+        assert rel(np_(o), np_(full[:, step])) < BF16_TOL, f"token {step}"
+    assert rel(np_(S), np_(S_full)) < STATE_TOL
+    assert np.array_equal(np_(conv), np_(conv_full))
+
+
+def test_layer_c1_shape_batch_slice():
+    """Config C1's shape (B=4, T=4096, Hk=16, Hv=32, d=128); batch row 0 against the oracle."""
+    say("layer C1 shape")
+    dims = dict(Hk=16, dk=128, Hv=32, dv=128)
+    d = W.layer_inputs(4, 4096)
+    t = W.to_device(d)
+    out, S, conv = gpu_prefill(t, dims)
+    d0 = {k_: (v_[:1] if k_ in ("mixed_qkv", "z", "a", "b") else v_) for k_, v_ in d.items()}
+    ref, S_ref, conv_ref = ref_prefill(d0, dims)
+    assert rel(np_(out[:1]), ref) < BF16_TOL
+    assert rel(np_(S[:1]), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv[:1]), conv_ref)
+    # batch rows are independent: row 3 of the batched run equals a run on row 3 alone
+    t3 = {k_: (v_[3:4].contiguous() if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+          for k_, v_ in t.items()}
+    out3, S3, _ = gpu_prefill(t3, dims)
+    assert torch.equal(out3, out[3:4]) and torch.equal(S3, S[3:4])
