@@ -1,17 +1,17 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X GatedDeltaNet path on one GPU; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|core]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode]
 
 Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   prefill  config C1: GDN layer prefill from projection outputs (mixed_qkv, z, a, b)
            to the gated-norm output, B=4 T=4096 Hk=16 Hv=32 d=128 (headline).
            A "step" is one omx_gdn_prefill call over the whole batch.
   decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
-  core     config C4-shaped chunked rule at the core-function boundary.
-The headline line reports prefill tokens/s with the chunked-scan kernel's MFMA
-roofline, and carries the decode step's HBM roofline as "decode".  Only one GPU
-is used: --gpus above 1 exits with a message.
+The headline line reports prefill tokens/s with the MFMA roofline of the chunked
+kernel, timed at the core-function boundary (chunk_gated_delta_rule on the same
+shapes), and carries the decode step's HBM roofline as "decode".  Only one GPU is
+used: --gpus above 1 exits with a message.
 
 Kernel durations come from HIP events recorded on the stream the kernels run on
 (torch's current stream, which the library launches on).
@@ -47,23 +47,27 @@ def _say(msg):
 
 
 def time_launches(fn, steps, warmup):
-    """Run fn warmup+steps times; return (wall seconds of the timed steps, mean event ms per call)."""
+    """Run fn warmup+steps times back to back.
+
+    Returns (wall seconds of the timed steps, ms per call from one pair of HIP
+    events around all timed calls on the current stream -- the stream the
+    library launches on).  The timed region is bracketed by a device
+    synchronisation on both sides.
+    """
     import torch
     for _ in range(warmup):
         fn()
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s, e in evs:
-        s.record()
+    start.record()
+    for _ in range(steps):
         fn()
-        e.record()
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in evs]
-    return wall, float(np.mean(per))
+    return wall, start.elapsed_time(end) / steps
 
 
 def cpu_cores():
@@ -171,7 +175,8 @@ def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
 
 
 def cpu_prefill_baseline(budget_s=15.0):
-    """Oracle layer prefill (numpy, fp32 chunked core) on a bounded C1 sample: B=1, T=512."""
+    """Oracle layer prefill (numpy restatement, fp32 core like the reference) on a bounded
+    C1 sample: B=1, T=512, the C1 head layout; numpy's BLAS uses the visible cores."""
     from oracle import gdn_oracle as O
     from omegalax_amd import workloads as W
     B, T = 1, 512
@@ -180,11 +185,12 @@ def cpu_prefill_baseline(budget_s=15.0):
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < budget_s or n == 0:
         O.gdn_prefill_layer(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"], d["A_log"],
-                            d["dt_bias"], d["norm_w"], Hk=16, dk=128, Hv=32, dv=128)
+                            d["dt_bias"], d["norm_w"], Hk=16, dk=128, Hv=32, dv=128,
+                            dtype=np.float32)
         n += 1
     el = time.perf_counter() - t0
     return {"value": B * T * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
-            "sample": f"{n} runs of the numpy oracle layer prefill, B={B} T={T}, C1 head layout"}
+            "sample": f"{n} runs of the numpy fp32 layer prefill restatement, B={B} T={T}, C1 head layout"}
 
 
 def main():

@@ -297,13 +297,15 @@ def _conv_silu(x_BTC, conv_w, history, act_round):
 
 def gdn_prefill_layer(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, Hk, dk, Hv, dv,
                       eps=1e-6, chunk_size=64, cu_seqlens=None, initial_state=None,
-                      conv_state=None, act_round=round_bf16):
+                      conv_state=None, act_round=round_bf16, dtype=np.float64):
     """GDN prefill from projections to the gated-norm output: deltanet.py:243-293.
 
     mixed_qkv [B,T,conv_dim], z [B,T,Hv,dv], a/b [B,T,Hv] (activation-dtype values),
     conv_w [conv_dim, K], A_log/dt_bias [Hv], norm_w [dv].
     Optional: cu_seqlens (B == 1; conv history and state reset per sequence),
     initial_state [N,Hv,dk,dv], conv_state [N,conv_dim,K-1] (history before each sequence).
+    ``dtype`` is the precision of the chunked core (float64 for checking, float32 for the
+    CPU baseline, which is the reference's own precision).
     Returns (out [B,T,Hv*dv] rounded by act_round, final_state [N,Hv,dk,dv],
     conv_state_out [N,conv_dim,K-1]).
     """
@@ -327,7 +329,7 @@ def gdn_prefill_layer(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, Hk,
     g, beta = gates(a, b, A_log, dt_bias, act_round)
     o, S = chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state=initial_state,
                                   output_final_state=True, cu_seqlens=cu_seqlens,
-                                  act_round=act_round)
+                                  act_round=act_round, dtype=dtype)
     out = gated_rmsnorm(o.reshape(-1, dv), np.asarray(z).reshape(-1, dv), norm_w, eps,
                         act_round).reshape(B, T, Hv * dv)
     # conv state after the prefill: the last K-1 raw inputs of each sequence (HF
