@@ -226,8 +226,8 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
     REQUIRE(mixed_qkv && z && a && b && out, "%s: an activation pointer is NULL", fn);
   REQUIRE(conv_w && A_log && dt_bias && norm_w, "%s: a parameter pointer is NULL", fn);
   REQUIRE(need == 0 || workspace, "%s: workspace is NULL", fn);
-  REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 4) && aligned(out, 4)),
-          "%s: mixed_qkv must be 16-byte, z and out 4-byte aligned", fn);
+  REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 16) && aligned(out, 16)),
+          "%s: mixed_qkv, z and out must be 16-byte aligned", fn);
   REQUIRE(!workspace || aligned(workspace, 16), "%s: workspace must be 16-byte aligned", fn);
   omx::ChunkParams p{};
   p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b;

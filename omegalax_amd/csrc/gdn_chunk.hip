@@ -77,8 +77,10 @@ struct Cfg {
   static constexpr int WS_U = 4 * 16 * LDT * 2;
   static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
   static constexpr int SZ_W = NWC * WS;
-  static constexpr int SZ_HIST = MODE == MODE_LAYER ? 3 * (2 * DK + BV) * 2 : 0;
+  static constexpr int HW = 2 * DK + BV;          // channels of this workgroup (q | k | v block)
+  static constexpr int SZ_HIST = MODE == MODE_LAYER ? 3 * HW * 2 : 0;
   static constexpr int SZ_NP = MODE == MODE_LAYER ? C * NWC * 4 : 0;
+  static constexpr int SZ_CW = MODE == MODE_LAYER ? 4 * HW * 4 : 0;  // conv weights [tap][ch]
   static constexpr int OFF_K = 0;
   static constexpr int OFF_Q = OFF_K + SZ_K;
   static constexpr int OFF_KT = OFF_Q + SZ_K;
@@ -91,7 +93,9 @@ struct Cfg {
   static constexpr int OFF_W = OFF_SC + SZ_SC;
   static constexpr int OFF_HIST = OFF_W + SZ_W;
   static constexpr int OFF_NP = OFF_HIST + SZ_HIST;
-  static constexpr int TOTAL = OFF_NP + SZ_NP;
+  static constexpr int OFF_CW = OFF_NP + SZ_NP;
+  static constexpr int TOTAL = OFF_CW + SZ_CW;
+  static_assert(SZ_W >= NS * C * LDT * 2, "V rows are staged in the wave scratch");
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
   static_assert(NI_KQ * NT == 2 * C * SEGS && NI_V * NT == C * (BV / 8), "item split");
@@ -278,15 +282,24 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   float* sEL = sG + 4 * C;                   // e^{G_last - G}
   bf16_t* sHist = (bf16_t*)(smem + Q_::OFF_HIST);  // layer: raw inputs of the 3 previous tokens
   float* sNP = (float*)(smem + Q_::OFF_NP);        // layer: [token][wave] sums of o^2
+  float* sCW = (float*)(smem + Q_::OFF_CW);        // layer: bf16-rounded conv weights [tap][ch]
+  bf16_t* sVrow = (bf16_t*)(smem + Q_::OFF_W);     // V rows [token][col] while staging
   constexpr int K_LO = C * LDK, KT_LO = DK * LDT, VT_LO = BV * LDT, P_LO = C * LDT;
   constexpr int LO_LO = C * LDT, TD_LO = C * LDD;
-  constexpr int HW = 2 * DK + BV;  // channels of one history row
+  constexpr int VROW_LO = C * LDT;  // lo copy of the staged V rows (fp32 inputs)
+  constexpr int HW = Q_::HW;
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lq = l >> 4, lr = l & 15;
+  // XCD-aware numbering: workgroups are dealt round-robin over the 8 XCDs
+  // (blockIdx % 8); renumber so that consecutive work items -- the gqa x nb
+  // workgroups reading the same key head's q/k -- run on one XCD and share its L2.
+  const unsigned nwg = gridDim.x, xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+  const unsigned per = nwg / 8, rem = nwg % 8;
+  const int wid = (int)(xcd * per + (xcd < rem ? xcd : rem) + slot);
   const int nb = p.nb;
-  const int blk = blockIdx.x % nb;
-  const int h = (blockIdx.x / nb) % p.Hv;
-  const int n = blockIdx.x / (nb * p.Hv);
+  const int blk = wid % nb;
+  const int h = (wid / nb) % p.Hv;
+  const int n = wid / (nb * p.Hv);
   const int gqa = p.Hv / p.Hk;
   const int hk = h / gqa;
   const int DV = p.DV;
@@ -320,6 +333,14 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       if (p.conv_state_in && slot >= 0)
         val = ((const bf16_t*)p.conv_state_in)[((size_t)n * p.conv_dim + ch) * (K - 1) + slot];
       sHist[it] = val;
+    }
+    for (int it = tid; it < K * HW; it += NT) {
+      const int tap = it / HW, ci = it % HW;
+      int ch;
+      if (ci < DK) ch = hk * DK + ci;
+      else if (ci < 2 * DK) ch = p.Hk * DK + hk * DK + (ci - DK);
+      else ch = 2 * p.Hk * DK + h * DV + col0 + (ci - 2 * DK);
+      sCW[it] = round_bf(p.conv_w[(size_t)ch * K + tap]);  // cast to bf16 as at deltanet.py:243
     }
   }
 
@@ -379,6 +400,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       sEL[l] = __expf(Gl - G);
     }
     if constexpr (MODE != MODE_LAYER) {
+      // K and Q rows (L2-normalised at input precision, deltanet.py:65-66), V rows
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         const int it = tid + k * NT;
@@ -390,13 +412,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
           float ss = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-          ss = group_sum<SEGS>(ss);
+          ss = group_sum_dpp<SEGS>(ss);
           const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
           for (int e = 0; e < 8; ++e) x[e] = IS ? x[e] * inv : round_bf(x[e] * inv);
         }
-        if (which == 0) stage8<IS>(sK + r * LDK + seg * 8, K_LO, sKT + seg * 8 * LDT + r, KT_LO, x);
-        else stage8<IS>(sQ + r * LDK + seg * 8, K_LO, nullptr, 0, x);
+        stage8<IS>((which == 0 ? sK : sQ) + r * LDK + seg * 8, K_LO, nullptr, 0, x);
       }
 #pragma unroll
       for (int k = 0; k < Q_::NI_V; ++k) {
@@ -404,10 +425,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         const int r = it / (BV / 8), seg = it % (BV / 8);
         float x[8];
         unpack8<F32>(pf.v[k], x);
-        stage8<IS>(nullptr, 0, sVT + seg * 8 * LDT + r, VT_LO, x);
+        stage8<IS>(sVrow + r * LDT + seg * 8, VROW_LO, nullptr, 0, x);
       }
     } else {
-      // raw rows: q -> sQ, k -> sK, v -> P (as [token][col]); the conv reads them next
+      // raw rows: q -> sQ, k -> sK, v -> sVrow; the conv reads them next
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         const int it = tid + k * NT;
@@ -419,18 +440,18 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       for (int k = 0; k < Q_::NI_V; ++k) {
         const int it = tid + k * NT;
         const int r = it / (BV / 8), seg = it % (BV / 8);
-        *(u32x4*)(sP + r * LDT + seg * 8) = pf.v[k][0];
+        *(u32x4*)(sVrow + r * LDT + seg * 8) = pf.v[k][0];
       }
       __syncthreads();
       // causal depthwise conv (deltanet.py:35-50) + SiLU, each rounded to bf16 like the
-      // reference's bf16 ops; weights cast to bf16 (deltanet.py:243)
+      // reference's bf16 ops; the weights in sCW are already bf16 values (deltanet.py:243)
       const int K = p.conv_k;
       float ykq[Q_::NI_KQ][8], yv[Q_::NI_V][8];
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ + Q_::NI_V; ++k) {
         const bool isv = k >= Q_::NI_KQ;
         const int it = tid + (isv ? k - Q_::NI_KQ : k) * NT;
-        int r, seg, ci, ch, ld;
+        int r, seg, ci, ld;
         const bf16_t* rows;
         if (!isv) {
           const int which = it / (C * SEGS);
@@ -439,14 +460,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
           rows = which == 0 ? sK : sQ;
           ld = LDK;
           ci = (which == 0 ? DK : 0) + seg * 8;
-          ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
         } else {
           r = it / (BV / 8);
           seg = it % (BV / 8);
-          rows = sP;
+          rows = sVrow;
           ld = LDT;
           ci = 2 * DK + seg * 8;
-          ch = 2 * p.Hk * DK + h * DV + col0 + seg * 8;
         }
         float acc[8];
 #pragma unroll
@@ -457,23 +476,20 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
           if (rr >= 0) {
             const u32x4 w = *(const u32x4*)(rows + rr * ld + seg * 8);
             unpack8<false>(&w, xv);
-          } else if (rr >= -3) {
+          } else {
             const u32x4 w = *(const u32x4*)(sHist + (3 + rr) * HW + ci);
             unpack8<false>(&w, xv);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) xv[e] = 0.f;
           }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += round_bf(p.conv_w[(size_t)(ch + e) * K + jt]) * xv[e];
+          const float4 w0 = *(const float4*)(sCW + jt * HW + ci);
+          const float4 w1 = *(const float4*)(sCW + jt * HW + ci + 4);
+          acc[0] += w0.x * xv[0]; acc[1] += w0.y * xv[1]; acc[2] += w0.z * xv[2]; acc[3] += w0.w * xv[3];
+          acc[4] += w1.x * xv[4]; acc[5] += w1.y * xv[5]; acc[6] += w1.z * xv[6]; acc[7] += w1.w * xv[7];
         }
         float* y = isv ? yv[k - Q_::NI_KQ] : ykq[k];
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = r < nvalid ? round_bf(siluf_(round_bf(acc[e]))) : 0.f;
       }
       __syncthreads();
-      // raw V is no longer needed in P: restore the zeros of P's strictly-upper tiles
-      for (int i = tid; i < C * LDT / 2; i += NT) ((uint32_t*)sP)[i] = 0u;
       // history for the next chunk: raw inputs of tokens 61..63 (still in the prefetch)
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
@@ -488,6 +504,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         const int r = it / (BV / 8), seg = it % (BV / 8);
         if (r >= C - 3) *(u32x4*)(sHist + (r - (C - 3)) * HW + 2 * DK + seg * 8) = pf.v[k][0];
       }
+      // conv outputs: q, k rows L2-normalised (deltanet.py:65-66), v rows
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         const int it = tid + k * NT;
@@ -497,27 +514,44 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-        ss = group_sum<SEGS>(ss);
+        ss = group_sum_dpp<SEGS>(ss);
         const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = round_bf(x[e] * inv);
-        if (which == 0) stage8<false>(sK + r * LDK + seg * 8, 0, sKT + seg * 8 * LDT + r, 0, x);
-        else stage8<false>(sQ + r * LDK + seg * 8, 0, nullptr, 0, x);
+        stage8<false>((which == 0 ? sK : sQ) + r * LDK + seg * 8, 0, nullptr, 0, x);
       }
 #pragma unroll
       for (int k = 0; k < Q_::NI_V; ++k) {
         const int it = tid + k * NT;
         const int r = it / (BV / 8), seg = it % (BV / 8);
-        stage8<false>(nullptr, 0, sVT + seg * 8 * LDT + r, 0, yv[k]);
+        stage8<false>(sVrow + r * LDT + seg * 8, 0, nullptr, 0, yv[k]);
       }
     }
     __syncthreads();
-
-    // issue the next chunk's loads; they land during this chunk's compute
-    if (j + 1 < nchunks) {
-      const long long tn = t0 + C;
-      prefetch<DK, MODE>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), hk, h, col0);
+    // K^T and V^T from the staged rows.  A wavefront reads 64 consecutive elements of
+    // one row per load and writes one 16-byte run of 8 tokens per lane, both free of
+    // LDS bank conflicts.
+    for (int tt = tid; tt < (DK + BV) * (C / 8); tt += NT) {
+      const bool isv = tt >= DK * (C / 8);
+      const int u = isv ? tt - DK * (C / 8) : tt;
+      const int width = isv ? BV : DK;
+      const int d = u % width, g8 = u / width;
+      const bf16_t* src = isv ? sVrow : sK;
+      const int ld = isv ? LDT : LDK;
+      bf16_t* dst = (isv ? sVT : sKT) + d * LDT + 8 * g8;
+#pragma unroll
+      for (int half = 0; half < (IS ? 2 : 1); ++half) {
+        const int soff = half ? (isv ? VROW_LO : K_LO) : 0;
+        const int doff = half ? (isv ? VT_LO : KT_LO) : 0;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = (uint32_t)src[soff + (8 * g8 + 2 * e) * ld + d] |
+                 ((uint32_t)src[soff + (8 * g8 + 2 * e + 1) * ld + d] << 16);
+        *(u32x4*)(dst + doff) = u32x4{w[0], w[1], w[2], w[3]};
+      }
     }
+    __syncthreads();
 
     // ------------------------------------------------------------ A2: K K^T -> L, Q K^T -> P
     for (int tile = wave; tile < 20; tile += NWC) {
@@ -611,6 +645,12 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
     __syncthreads();
 
+    // issue the next chunk's loads; they land during the rest of this chunk
+    if (j + 1 < nchunks) {
+      const long long tn = t0 + C;
+      prefetch<DK, MODE>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), hk, h, col0);
+    }
+
     // ------------------------------------------------------------ B2: the solve, per wave
     // (I + L) U = R by block forward substitution; U^T stays in the scratch (hi, lo)
     f32x4 U[4];
@@ -671,7 +711,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       } else {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float ss = group_sum<16>(o[v] * o[v]);
+          const float ss = group_sum_dpp<16>(o[v] * o[v]);
           if (lr == 0) sNP[(16 * i + 4 * lq + v) * NWC + wave] = ss;
         }
       }

@@ -48,4 +48,23 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// lane permutation within rows of 16 lanes by a DPP control word (no LDS traffic)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over aligned groups of WIDTH (4, 8 or 16) lanes with DPP butterflies:
+// quad_perm [1,0,3,2] and [2,3,0,1] sum each quad; row_half_mirror pairs the two
+// quads of each 8-lane half; row_mirror pairs the two halves of each 16-lane row.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(WIDTH == 4 || WIDTH == 8 || WIDTH == 16, "dpp group width");
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  if constexpr (WIDTH >= 8) v += dpp_f<0x141>(v);
+  if constexpr (WIDTH >= 16) v += dpp_f<0x140>(v);
+  return v;
+}
+
 }  // namespace omx

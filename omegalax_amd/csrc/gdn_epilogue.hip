@@ -5,7 +5,7 @@
 // kernel splits dv over nb workgroups, each writes its columns of o (bf16) and
 // its share of sum(o^2) (fp32, from the fp32 o); this kernel adds the shares
 // and applies the norm.  Memory-bound: two bf16 reads and one bf16 write per
-// element, one thread per pair of columns.
+// element, one thread per 8 columns (16-byte accesses).
 #include "gdn_common.h"
 #include "gdn_kernels.h"
 
@@ -13,25 +13,32 @@ namespace omx {
 
 namespace {
 
-__global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint32_t* __restrict__ o_part,
+__global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restrict__ o_part,
                                                             const float* __restrict__ ss_part,
-                                                            const uint32_t* __restrict__ z,
+                                                            const uint4* __restrict__ z,
                                                             const float* __restrict__ norm_w,
-                                                            uint32_t* __restrict__ out,
-                                                            long long pairs, int dv, int nb,
+                                                            uint4* __restrict__ out,
+                                                            long long octets, int dv, int nb,
                                                             float eps) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= pairs) return;
-  const int half = dv / 2;
-  const long long row = i / half;
-  const int c = 2 * (int)(i % half);
+  if (i >= octets) return;
+  const int per_row = dv / 8;
+  const long long row = i / per_row;
+  const int c = 8 * (int)(i % per_row);
   float ss = 0.f;
   for (int b = 0; b < nb; ++b) ss += ss_part[row * nb + b];
   const float rn = rsqrtf(ss / (float)dv + eps);
-  const uint32_t ow = o_part[i], zw = z[i];
-  const float o0 = __uint_as_float(ow << 16), o1 = __uint_as_float(ow & 0xffff0000u);
-  const float z0 = __uint_as_float(zw << 16), z1 = __uint_as_float(zw & 0xffff0000u);
-  out[i] = pack_bf16(norm_w[c] * (o0 * rn) * siluf_(z0), norm_w[c + 1] * (o1 * rn) * siluf_(z1));
+  const uint4 ow = o_part[i], zw = z[i];
+  const uint32_t ov[4] = {ow.x, ow.y, ow.z, ow.w}, zv[4] = {zw.x, zw.y, zw.z, zw.w};
+  uint32_t r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float o0 = __uint_as_float(ov[e] << 16), o1 = __uint_as_float(ov[e] & 0xffff0000u);
+    const float z0 = __uint_as_float(zv[e] << 16), z1 = __uint_as_float(zv[e] & 0xffff0000u);
+    r[e] = pack_bf16(norm_w[c + 2 * e] * (o0 * rn) * siluf_(z0),
+                     norm_w[c + 2 * e + 1] * (o1 * rn) * siluf_(z1));
+  }
+  out[i] = make_uint4(r[0], r[1], r[2], r[3]);
 }
 
 }  // namespace
@@ -39,12 +46,12 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint32_t* __re
 hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,
                                 const float* norm_w, void* out, long long rows, int dv, int nb,
                                 float eps, hipStream_t stream) {
-  const long long pairs = rows * (dv / 2);
-  if (pairs == 0) return hipSuccess;
-  const unsigned grid = (unsigned)((pairs + 255) / 256);
+  const long long octets = rows * (dv / 8);
+  if (octets == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((octets + 255) / 256);
   hipLaunchKernelGGL(norm_epilogue_kernel, dim3(grid), dim3(256), 0, stream,
-                     (const uint32_t*)o_part, ss_part, (const uint32_t*)z, norm_w, (uint32_t*)out,
-                     pairs, dv, nb, eps);
+                     (const uint4*)o_part, ss_part, (const uint4*)z, norm_w, (uint4*)out, octets,
+                     dv, nb, eps);
   return hipGetLastError();
 }
 
