@@ -65,8 +65,7 @@ struct Cfg {
   static constexpr int NI_V = C * (BV / 8) / NT;
   // shared arrays (bytes)
   static constexpr int SZ_K = NS * C * LDK * 2;   // K rows [token][dk] (hi, lo)
-  static constexpr int SZ_KT = NS * DK * LDT * 2; // K^T [dk][token]
-  static constexpr int SZ_VT = NS * BV * LDT * 2; // V^T [col][token]
+  static constexpr int SZ_V = NS * C * LDT * 2;   // V rows [token][col]
   static constexpr int SZ_LO = 2 * C * LDT * 2;   // off-diagonal blocks of L (hi, lo)
   static constexpr int SZ_LD = C * LDD * 4;       // diagonal blocks of L, fp32
   static constexpr int SZ_TD = 2 * C * LDD * 2;   // inverses of the diagonal blocks (hi, lo)
@@ -83,9 +82,8 @@ struct Cfg {
   static constexpr int SZ_CW = MODE == MODE_LAYER ? 4 * HW * 4 : 0;  // conv weights [tap][ch]
   static constexpr int OFF_K = 0;
   static constexpr int OFF_Q = OFF_K + SZ_K;
-  static constexpr int OFF_KT = OFF_Q + SZ_K;
-  static constexpr int OFF_VT = OFF_KT + SZ_KT;
-  static constexpr int OFF_LO = OFF_VT + SZ_VT;
+  static constexpr int OFF_V = OFF_Q + SZ_K;
+  static constexpr int OFF_LO = OFF_V + SZ_V;
   static constexpr int OFF_LD = OFF_LO + SZ_LO;
   static constexpr int OFF_TD = OFF_LD + SZ_LD;
   static constexpr int OFF_P = OFF_TD + SZ_TD;
@@ -95,17 +93,26 @@ struct Cfg {
   static constexpr int OFF_NP = OFF_HIST + SZ_HIST;
   static constexpr int OFF_CW = OFF_NP + SZ_NP;
   static constexpr int TOTAL = OFF_CW + SZ_CW;
-  static_assert(SZ_W >= NS * C * LDT * 2, "V rows are staged in the wave scratch");
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
   static_assert(NI_KQ * NT == 2 * C * SEGS && NI_V * NT == C * (BV / 8), "item split");
 };
 
-// the 20 tiles of K K^T and Q K^T that A2 computes: (which, row block, col block)
-__constant__ int kTiles[20][3] = {
-    {0, 0, 0}, {0, 1, 1}, {0, 2, 2}, {0, 3, 3}, {0, 1, 0}, {0, 2, 0}, {0, 2, 1}, {0, 3, 0},
-    {0, 3, 1}, {0, 3, 2}, {1, 0, 0}, {1, 1, 0}, {1, 1, 1}, {1, 2, 0}, {1, 2, 1}, {1, 2, 2},
-    {1, 3, 0}, {1, 3, 1}, {1, 3, 2}, {1, 3, 3}};
+// The 20 lower-triangular 16x16 tiles of K K^T (0..9, diagonal first) and Q K^T
+// (10..19), each coded in 5 bits as qk << 4 | row block << 2 | col block and
+// packed into two words, so a wave decodes its tiles with scalar shifts.
+constexpr int kTileList[20] = {0x00, 0x05, 0x0A, 0x0F, 0x04, 0x08, 0x09, 0x0C, 0x0D, 0x0E,
+                               0x10, 0x14, 0x15, 0x18, 0x19, 0x1A, 0x1C, 0x1D, 0x1E, 0x1F};
+constexpr unsigned long long pack_tiles(int first, int count) {
+  unsigned long long w = 0;
+  for (int t = 0; t < count; ++t) w |= (unsigned long long)kTileList[first + t] << (5 * t);
+  return w;
+}
+constexpr unsigned long long kTilesLo = pack_tiles(0, 12), kTilesHi = pack_tiles(12, 8);
+
+__device__ __forceinline__ int tile_code(int t) {
+  return t < 12 ? (int)((kTilesLo >> (5 * t)) & 31) : (int)((kTilesHi >> (5 * (t - 12))) & 31);
+}
 
 template <bool AS, bool BS>
 __device__ __forceinline__ f32x4 mm(f32x4 acc, u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl) {
@@ -269,24 +276,21 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   __shared__ __align__(16) unsigned char smem[Q_::TOTAL];
   bf16_t* sK = (bf16_t*)(smem + Q_::OFF_K);
   bf16_t* sQ = (bf16_t*)(smem + Q_::OFF_Q);
-  bf16_t* sKT = (bf16_t*)(smem + Q_::OFF_KT);
-  bf16_t* sVT = (bf16_t*)(smem + Q_::OFF_VT);
-  bf16_t* sLo = (bf16_t*)(smem + Q_::OFF_LO);
+  bf16_t* sV = (bf16_t*)(smem + Q_::OFF_V);
+  bf16_t* sLoT = (bf16_t*)(smem + Q_::OFF_LO);   // L^T off-diagonal blocks [m][i] (hi, lo)
   float* sLd = (float*)(smem + Q_::OFF_LD);
-  bf16_t* sTd = (bf16_t*)(smem + Q_::OFF_TD);
-  bf16_t* sP = (bf16_t*)(smem + Q_::OFF_P);
-  float* sG = (float*)(smem + Q_::OFF_SC);  // cumulative log decay G
-  float* sBeta = sG + C;                     // beta
-  float* sBE = sG + 2 * C;                   // beta e^G
-  float* sEG = sG + 3 * C;                   // e^G
-  float* sEL = sG + 4 * C;                   // e^{G_last - G}
+  bf16_t* sTdT = (bf16_t*)(smem + Q_::OFF_TD);   // diagonal inverses, transposed (hi, lo)
+  bf16_t* sPT = (bf16_t*)(smem + Q_::OFF_P);     // P^T [m][i]
+  float* sG2 = (float*)(smem + Q_::OFF_SC);  // cumulative log decay G, times log2(e)
+  float* sBeta = sG2 + C;                     // beta
+  float* sBE = sG2 + 2 * C;                   // beta e^G
+  float* sEG = sG2 + 3 * C;                   // e^G
+  float* sEL = sG2 + 4 * C;                   // e^{G_last - G}
   bf16_t* sHist = (bf16_t*)(smem + Q_::OFF_HIST);  // layer: raw inputs of the 3 previous tokens
   float* sNP = (float*)(smem + Q_::OFF_NP);        // layer: [token][wave] sums of o^2
   float* sCW = (float*)(smem + Q_::OFF_CW);        // layer: bf16-rounded conv weights [tap][ch]
-  bf16_t* sVrow = (bf16_t*)(smem + Q_::OFF_W);     // V rows [token][col] while staging
-  constexpr int K_LO = C * LDK, KT_LO = DK * LDT, VT_LO = BV * LDT, P_LO = C * LDT;
+  constexpr int K_LO = C * LDK, V_LO = C * LDT, P_LO = C * LDT;
   constexpr int LO_LO = C * LDT, TD_LO = C * LDD;
-  constexpr int VROW_LO = C * LDT;  // lo copy of the staged V rows (fp32 inputs)
   constexpr int HW = Q_::HW;
 
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -318,7 +322,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   const int nchunks = (int)((s1 - s0 + C - 1) / C);
 
   // zero P once: its strictly-upper 16x16 tiles are never written
-  for (int i = tid; i < (OS ? 2 : 1) * C * LDT / 2; i += NT) ((uint32_t*)sP)[i] = 0u;
+  for (int i = tid; i < (OS ? 2 : 1) * C * LDT / 2; i += NT) ((uint32_t*)sPT)[i] = 0u;
   if constexpr (MODE == MODE_LAYER) {
     // conv history before the first token: conv_state_in (oldest tap first) or zeros
     const int K = p.conv_k;
@@ -393,7 +397,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       }
       const float Gl = __shfl(G, 63, 64);
       const float eg = __expf(G);
-      sG[l] = G;
+      sG2[l] = G * 1.4426950408889634f;
       sBeta[l] = bt;
       sBE[l] = bt * eg;
       sEG[l] = eg;
@@ -425,10 +429,10 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         const int r = it / (BV / 8), seg = it % (BV / 8);
         float x[8];
         unpack8<F32>(pf.v[k], x);
-        stage8<IS>(sVrow + r * LDT + seg * 8, VROW_LO, nullptr, 0, x);
+        stage8<IS>(sV + r * LDT + seg * 8, V_LO, nullptr, 0, x);
       }
     } else {
-      // raw rows: q -> sQ, k -> sK, v -> sVrow; the conv reads them next
+      // raw rows: q -> sQ, k -> sK, v -> sV; the conv reads them next
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         const int it = tid + k * NT;
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       for (int k = 0; k < Q_::NI_V; ++k) {
         const int it = tid + k * NT;
         const int r = it / (BV / 8), seg = it % (BV / 8);
-        *(u32x4*)(sVrow + r * LDT + seg * 8) = pf.v[k][0];
+        *(u32x4*)(sV + r * LDT + seg * 8) = pf.v[k][0];
       }
       __syncthreads();
       // causal depthwise conv (deltanet.py:35-50) + SiLU, each rounded to bf16 like the
@@ -463,7 +467,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         } else {
           r = it / (BV / 8);
           seg = it % (BV / 8);
-          rows = sVrow;
+          rows = sV;
           ld = LDT;
           ci = 2 * DK + seg * 8;
         }
@@ -524,38 +528,22 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       for (int k = 0; k < Q_::NI_V; ++k) {
         const int it = tid + k * NT;
         const int r = it / (BV / 8), seg = it % (BV / 8);
-        stage8<false>(sVrow + r * LDT + seg * 8, 0, nullptr, 0, yv[k]);
-      }
-    }
-    __syncthreads();
-    // K^T and V^T from the staged rows.  A wavefront reads 64 consecutive elements of
-    // one row per load and writes one 16-byte run of 8 tokens per lane, both free of
-    // LDS bank conflicts.
-    for (int tt = tid; tt < (DK + BV) * (C / 8); tt += NT) {
-      const bool isv = tt >= DK * (C / 8);
-      const int u = isv ? tt - DK * (C / 8) : tt;
-      const int width = isv ? BV : DK;
-      const int d = u % width, g8 = u / width;
-      const bf16_t* src = isv ? sVrow : sK;
-      const int ld = isv ? LDT : LDK;
-      bf16_t* dst = (isv ? sVT : sKT) + d * LDT + 8 * g8;
-#pragma unroll
-      for (int half = 0; half < (IS ? 2 : 1); ++half) {
-        const int soff = half ? (isv ? VROW_LO : K_LO) : 0;
-        const int doff = half ? (isv ? VT_LO : KT_LO) : 0;
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = (uint32_t)src[soff + (8 * g8 + 2 * e) * ld + d] |
-                 ((uint32_t)src[soff + (8 * g8 + 2 * e + 1) * ld + d] << 16);
-        *(u32x4*)(dst + doff) = u32x4{w[0], w[1], w[2], w[3]};
+        stage8<false>(sV + r * LDT + seg * 8, 0, nullptr, 0, yv[k]);
       }
     }
     __syncthreads();
 
     // ------------------------------------------------------------ A2: K K^T -> L, Q K^T -> P
-    for (int tile = wave; tile < 20; tile += NWC) {
-      const int qk = kTiles[tile][0], bi = kTiles[tile][1], bj = kTiles[tile][2];
+    // Wave w computes tiles w, w+4, ..., w+16 of kTileCode: first its diagonal K K^T
+    // tile (w, w), which it inverts itself right away, then four more.  L and P are
+    // written transposed (one vector store per lane) and read back through
+    // ds_read_b64_tr_b16 as row-major operands.
+#pragma unroll
+    for (int ti = 0; ti < 5; ++ti) {
+      const int tile = wave + 4 * ti;
+      const int code = tile_code(tile);
+      const bool qk = code & 16;
+      const int bi = (code >> 2) & 3, bj = code & 3;
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
@@ -565,24 +553,64 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         acc = mm<IS, IS>(acc, ah, al, bh, bl);
       }
       const int m = 16 * bj + lr;
-      const float Gm = sG[m];
+      const float Gm = sG2[m];
+      const float4 Gi = *(const float4*)(sG2 + 16 * bi + 4 * lq);
+      const float gi[4] = {Gi.x, Gi.y, Gi.z, Gi.w};
+      f32x4 val;
+      if (!qk) {
+        const float4 Bi = *(const float4*)(sBeta + 16 * bi + 4 * lq);
+        const float bt[4] = {Bi.x, Bi.y, Bi.z, Bi.w};
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int i = 16 * bi + 4 * lq + v;
-        const float dec = __expf(sG[i] - Gm);
-        if (!qk) {
-          const float lv = (i > m) ? sBeta[i] * acc[v] * dec : 0.f;
-          if (bi == bj) {
-            sLd[i * LDD + lr] = lv;
-          } else {
-            sLo[i * LDT + m] = f2bf(lv);
-            sLo[LO_LO + i * LDT + m] = f2bf(lo_part(lv));
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * bi + 4 * lq + v;
+          val[v] = (i > m) ? bt[v] * acc[v] * __builtin_amdgcn_exp2f(gi[v] - Gm) : 0.f;
+        }
+        if (bi == bj) {
+          // this wave's diagonal block: T_ww = (I + L_ww)^-1 by forward substitution,
+          // one column per lane (lanes 16..63 repeat the work and do not store)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) sLd[(16 * bi + 4 * lq + v) * LDD + lr] = val[v];
+          wave_lds_fence();
+          const int c = l & 15;
+          float x[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float* row = sLd + (16 * bi + i) * LDD;
+            float a0 = (i == c) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+            for (int mm2 = 0; mm2 < i; mm2 += 4) {
+              const float4 r4 = *(const float4*)(row + mm2);
+              a0 -= r4.x * x[mm2];
+              if (mm2 + 1 < i) a1 -= r4.y * x[mm2 + 1];
+              if (mm2 + 2 < i) a0 -= r4.z * x[mm2 + 2];
+              if (mm2 + 3 < i) a1 -= r4.w * x[mm2 + 3];
+            }
+            x[i] = a0 + a1;
+          }
+          if (l < 16) {
+            // T_ww^T row c = column c of T_ww, hi and lo
+            bf16_t* dh = sTdT + (16 * bi + c) * LDD;
+            bf16_t* dl = dh + TD_LO;
+#pragma unroll
+            for (int h8 = 0; h8 < 2; ++h8) {
+              float hv[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) hv[e] = x[8 * h8 + e];
+              *(u32x4*)(dh + 8 * h8) = pack8(hv);
+              *(u32x4*)(dl + 8 * h8) = pack8_lo(hv);
+            }
           }
         } else {
-          const float pv = (i >= m) ? p.scale * acc[v] * dec : 0.f;
-          sP[i * LDT + m] = f2bf(pv);
-          if constexpr (OS) sP[P_LO + i * LDT + m] = f2bf(lo_part(pv));
+          store_ct_split(sLoT, sLoT + LO_LO, LDT, 16 * bi, 16 * bj, val);
         }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * bi + 4 * lq + v;
+          val[v] = (i >= m) ? p.scale * acc[v] * __builtin_amdgcn_exp2f(gi[v] - Gm) : 0.f;
+        }
+        if constexpr (OS) store_ct_split(sPT, sPT + P_LO, LDT, 16 * bi, 16 * bj, val);
+        else store_ct_bf16(sPT, LDT, 16 * bi, 16 * bj, val);
       }
     }
 
@@ -609,11 +637,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       }
       // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
       const int r0 = 16 * i + 4 * lq;
-      const u32x2 vw = *(const u32x2*)(sVT + (16 * wave + lr) * LDT + r0);
+      const u32x2 vw = rows4_tr(sV, LDT, 16 * i, 16 * wave);
       float vv[4] = {__uint_as_float(vw[0] << 16), __uint_as_float(vw[0] & 0xffff0000u),
                      __uint_as_float(vw[1] << 16), __uint_as_float(vw[1] & 0xffff0000u)};
       if constexpr (IS) {
-        const u32x2 vl = *(const u32x2*)(sVT + VT_LO + (16 * wave + lr) * LDT + r0);
+        const u32x2 vl = rows4_tr(sV + V_LO, LDT, 16 * i, 16 * wave);
         vv[0] += __uint_as_float(vl[0] << 16);
         vv[1] += __uint_as_float(vl[0] & 0xffff0000u);
         vv[2] += __uint_as_float(vl[1] << 16);
@@ -622,28 +650,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) R[i][v] = sBeta[r0 + v] * vv[v] - sBE[r0 + v] * ks[v];
     }
-    __syncthreads();  // L and P complete
-
-    // ------------------------------------------------------------ A3: diagonal-block inverses
-    // T_bb = (I + L_bb)^-1 by forward substitution, one column per lane
-    if (l < 16) {
-      const int b0 = 16 * wave, c = l;
-      float x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float acc = (i == c) ? 1.f : 0.f;
-        const float* row = sLd + (b0 + i) * LDD;
-#pragma unroll
-        for (int m = 0; m < i; ++m) acc -= row[m] * x[m];
-        x[i] = acc;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sTd[(b0 + i) * LDD + c] = f2bf(x[i]);
-        sTd[TD_LO + (b0 + i) * LDD + c] = f2bf(lo_part(x[i]));
-      }
-    }
-    __syncthreads();
+    __syncthreads();  // L^T, P^T and the diagonal inverses complete
 
     // issue the next chunk's loads; they land during the rest of this chunk
     if (j + 1 < nchunks) {
@@ -660,16 +667,16 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 #pragma unroll
       for (int jb = 0; jb < b; ++jb) {
         // acc -= L_b,jb U_jb: the A operand is negated (a sign flip is exact in bf16)
-        const u32x2 ah = frag4_bf16(sLo, LDT, 16 * b, 16 * jb) ^ 0x80008000u;
-        const u32x2 al = frag4_bf16(sLo + LO_LO, LDT, 16 * b, 16 * jb) ^ 0x80008000u;
+        const u32x2 ah = rows4_tr(sLoT, LDT, 16 * jb, 16 * b) ^ 0x80008000u;
+        const u32x2 al = rows4_tr(sLoT + LO_LO, LDT, 16 * jb, 16 * b) ^ 0x80008000u;
         const u32x2 bh = frag4_bf16(wU, LDT, 0, 16 * jb);
         const u32x2 bl = frag4_bf16(wU + W_LO, LDT, 0, 16 * jb);
         acc = mm3k16(acc, ah, al, bh, bl);
       }
       store_ct_split(wU, wU + W_LO, LDT, 16 * b, 0, acc);
       wave_lds_fence();
-      const u32x2 th = frag4_bf16(sTd, LDD, 16 * b, 0);
-      const u32x2 tl = frag4_bf16(sTd + TD_LO, LDD, 16 * b, 0);
+      const u32x2 th = rows4_tr(sTdT, LDD, 16 * b, 0);
+      const u32x2 tl = rows4_tr(sTdT + TD_LO, LDD, 16 * b, 0);
       const u32x2 rh = frag4_bf16(wU, LDT, 0, 16 * b);
       const u32x2 rl = frag4_bf16(wU + W_LO, LDT, 0, 16 * b);
       U[b] = mm3k16(zero4(), th, tl, rh, rl);
@@ -698,7 +705,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       for (int s = 0; s < 2; ++s) {
         if (s == 1 && i < 2) continue;  // P is lower triangular
         u32x4 ah, al, bh, bl;
-        frag2<OS>(sP, P_LO, LDT, 16 * i, 32 * s, ah, al);
+        ah = frag_tr(sPT, LDT, 32 * s, 16 * i);
+        al = OS ? frag_tr(sPT + P_LO, LDT, 32 * s, 16 * i) : ah;
         frag2<OS>(wU, W_LO, LDT, 0, 32 * s, bh, bl);
         o = mm<OS, OS>(o, ah, al, bh, bl);
       }
@@ -726,7 +734,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         u32x4 ah, al, bh, bl;
-        frag2<IS>(sKT, KT_LO, LDT, 16 * t, 32 * s, ah, al);
+        ah = frag_tr(sK, LDK, 32 * s, 16 * t);
+        al = IS ? frag_tr(sK + K_LO, LDK, 32 * s, 16 * t) : ah;
         frag2<true>(wVt, W_LO, LDT, 0, 32 * s, bh, bl);
         S[t] = mm<IS, true>(S[t], ah, al, bh, bl);
       }

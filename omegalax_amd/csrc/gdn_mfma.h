@@ -51,6 +51,34 @@ __device__ __forceinline__ u32x2 frag4_bf16(const bf16_t* base, int ld, int row0
 
 __device__ __forceinline__ float lo_part(float x) { return x - round_bf(x); }
 
+// Transposed 16-bit LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes
+// the lanes' 4-element rows (8 bytes at each lane's address) form a 16x4 block M,
+// and lane 4a+b receives {M[a][b], M[a+4][b], M[a+8][b], M[a+12][b]} (mapping
+// verified on MI355X).  Pointing source lane s at row base + s/4, column 4*(s%4)
+// of a row-major array therefore hands each lane 4 consecutive rows of its own
+// column: an MFMA operand whose contraction runs down the rows.
+__device__ __forceinline__ u32x2 ds_read_tr(const bf16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// 16x32 operand whose contraction runs down the rows of a row-major [k][col]
+// bf16 array (stride ld): lane (q, r) gets rows k0 + 8q .. +7 of column col0 + r.
+__device__ __forceinline__ u32x4 frag_tr(const bf16_t* base, int ld, int k0, int col0) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  const bf16_t* p = base + (k0 + 8 * q + (s >> 2)) * ld + col0 + 4 * (s & 3);
+  const u32x2 a = ds_read_tr(p), b = ds_read_tr(p + 4 * ld);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// Four consecutive rows row0 + 4q .. +3 of column col0 + r (the MFMA C layout) of a
+// row-major bf16 array, as 4 bf16 in two words.
+__device__ __forceinline__ u32x2 rows4_tr(const bf16_t* base, int ld, int row0, int col0) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  return ds_read_tr(base + (row0 + 4 * q + (s >> 2)) * ld + col0 + 4 * (s & 3));
+}
+
 // Store a C fragment transposed as bf16 into a [col][row] array (row stride ld):
 // the lane's 4 values (rows 4q..4q+3 of the tile) are contiguous there.
 __device__ __forceinline__ void store_ct_bf16(bf16_t* base, int ld, int row0, int col0, f32x4 c) {
