@@ -71,9 +71,9 @@ struct Cfg {
   static constexpr int SZ_TD = 2 * C * LDD * 2;   // inverses of the diagonal blocks (hi, lo)
   static constexpr int SZ_P = (OS ? 2 : 1) * C * LDT * 2;
   static constexpr int SZ_SC = 8 * C * 4;
-  // per-wave scratch: S^T (K S, Q S), then U^T (hi, lo) and Vt^T (hi, lo)
+  // per-wave scratch: S^T (K S, Q S), then Vt^T (hi, lo)
   static constexpr int WS_S = NS * 16 * LDK * 2;
-  static constexpr int WS_U = 4 * 16 * LDT * 2;
+  static constexpr int WS_U = 2 * 16 * LDT * 2;
   static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
   static constexpr int SZ_W = NWC * WS;
   static constexpr int HW = 2 * DK + BV;          // channels of this workgroup (q | k | v block)
@@ -221,37 +221,34 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
     const int it = tid + k * NT;
     const int which = it / (C * Q_::SEGS);  // 0 = k, 1 = q
     const int r = (it / Q_::SEGS) % C, seg = it % Q_::SEGS;
-    if (r < nvalid) {
-      const long long tok = t0 + r;
-      if constexpr (MODE == MODE_LAYER) {
-        const int ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
-        load_raw<false>(p.mixed_qkv, tok * p.conv_dim + ch, pf.kq[k]);
-      } else {
-        const void* base = which == 0 ? p.k : p.q;
-        const long long ld = which == 0 ? p.k_ld : p.q_ld;
-        load_raw<F32>(base, tok * ld + (long long)hk * DK + seg * 8, pf.kq[k]);
-      }
+    // rows past the sequence end load the last valid row (in bounds) and are zeroed
+    const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
+    if constexpr (MODE == MODE_LAYER) {
+      const int ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
+      load_raw<false>(p.mixed_qkv, tok * p.conv_dim + ch, pf.kq[k]);
     } else {
-#pragma unroll
-      for (int w = 0; w < Q_::RAWW; ++w) pf.kq[k][w] = u32x4{0u, 0u, 0u, 0u};
+      const void* base = which == 0 ? p.k : p.q;
+      const long long ld = which == 0 ? p.k_ld : p.q_ld;
+      load_raw<F32>(base, tok * ld + (long long)hk * DK + seg * 8, pf.kq[k]);
     }
+    const unsigned keep = r < nvalid ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int w = 0; w < Q_::RAWW; ++w) pf.kq[k][w] &= keep;
   }
 #pragma unroll
   for (int k = 0; k < Q_::NI_V; ++k) {
     const int it = tid + k * NT;
     const int r = it / (BV / 8), seg = it % (BV / 8);
-    if (r < nvalid) {
-      const long long tok = t0 + r;
-      if constexpr (MODE == MODE_LAYER)
-        load_raw<false>(p.mixed_qkv,
-                        tok * p.conv_dim + 2 * p.Hk * DK + (long long)h * p.DV + col0 + seg * 8,
-                        pf.v[k]);
-      else
-        load_raw<F32>(p.v, tok * p.v_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
-    } else {
+    const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
+    if constexpr (MODE == MODE_LAYER)
+      load_raw<false>(p.mixed_qkv,
+                      tok * p.conv_dim + 2 * p.Hk * DK + (long long)h * p.DV + col0 + seg * 8,
+                      pf.v[k]);
+    else
+      load_raw<F32>(p.v, tok * p.v_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
+    const unsigned keep = r < nvalid ? 0xffffffffu : 0u;
 #pragma unroll
-      for (int w = 0; w < Q_::RAWW; ++w) pf.v[k][w] = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int w = 0; w < Q_::RAWW; ++w) pf.v[k][w] &= keep;
   }
   pf.g0 = 0.f;
   pf.g1 = 0.f;
@@ -273,27 +270,32 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
   constexpr bool F32 = MODE == MODE_F32;
-  __shared__ __align__(16) unsigned char smem[Q_::TOTAL];
-  bf16_t* sK = (bf16_t*)(smem + Q_::OFF_K);
-  bf16_t* sQ = (bf16_t*)(smem + Q_::OFF_Q);
-  bf16_t* sV = (bf16_t*)(smem + Q_::OFF_V);
-  bf16_t* sLoT = (bf16_t*)(smem + Q_::OFF_LO);   // L^T off-diagonal blocks [m][i] (hi, lo)
-  float* sLd = (float*)(smem + Q_::OFF_LD);
-  bf16_t* sTdT = (bf16_t*)(smem + Q_::OFF_TD);   // diagonal inverses, transposed (hi, lo)
-  bf16_t* sPT = (bf16_t*)(smem + Q_::OFF_P);     // P^T [m][i]
-  float* sG2 = (float*)(smem + Q_::OFF_SC);  // cumulative log decay G, times log2(e)
+  // Each buffer is its own __shared__ object, so the compiler can tell their
+  // accesses apart and overlap loads of one with stores to another.
+  __shared__ __align__(16) bf16_t sK[Q_::SZ_K / 2];
+  __shared__ __align__(16) bf16_t sQ[Q_::SZ_K / 2];
+  __shared__ __align__(16) bf16_t sV[Q_::SZ_V / 2];
+  __shared__ __align__(16) bf16_t sLoT[Q_::SZ_LO / 2];  // L^T off-diagonal blocks [m][i] (hi, lo)
+  __shared__ __align__(16) float sLd[Q_::SZ_LD / 4];    // diagonal blocks of L, fp32
+  __shared__ __align__(16) bf16_t sTdT[Q_::SZ_TD / 2];  // diagonal inverses, transposed (hi, lo)
+  __shared__ __align__(16) bf16_t sPT[Q_::SZ_P / 2];    // P^T [m][i]
+  __shared__ __align__(16) float sG2[Q_::SZ_SC / 4];    // cumulative log decay G, times log2(e)
+  __shared__ __align__(16) bf16_t sWS[Q_::SZ_W / 2];    // per-wave scratch
+  __shared__ __align__(16) bf16_t sHist[Q_::SZ_HIST / 2 + 8];  // layer: raw inputs of 3 previous tokens
+  __shared__ __align__(16) float sNP[Q_::SZ_NP / 4 + 4];       // layer: [token][wave] sums of o^2
+  __shared__ __align__(16) float sCW[Q_::SZ_CW / 4 + 4];       // layer: bf16-rounded conv weights
   float* sBeta = sG2 + C;                     // beta
   float* sBE = sG2 + 2 * C;                   // beta e^G
   float* sEG = sG2 + 3 * C;                   // e^G
   float* sEL = sG2 + 4 * C;                   // e^{G_last - G}
-  bf16_t* sHist = (bf16_t*)(smem + Q_::OFF_HIST);  // layer: raw inputs of the 3 previous tokens
-  float* sNP = (float*)(smem + Q_::OFF_NP);        // layer: [token][wave] sums of o^2
-  float* sCW = (float*)(smem + Q_::OFF_CW);        // layer: bf16-rounded conv weights [tap][ch]
   constexpr int K_LO = C * LDK, V_LO = C * LDT, P_LO = C * LDT;
   constexpr int LO_LO = C * LDT, TD_LO = C * LDD;
   constexpr int HW = Q_::HW;
 
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, lq = l >> 4, lr = l & 15;
+  // the wavefront index is uniform across the wave: readfirstlane puts it in an
+  // SGPR so wave-dependent tile choices and branches stay scalar
+  const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // XCD-aware numbering: workgroups are dealt round-robin over the 8 XCDs
   // (blockIdx % 8); renumber so that consecutive work items -- the gqa x nb
   // workgroups reading the same key head's q/k -- run on one XCD and share its L2.
@@ -362,10 +364,9 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     for (int t = 0; t < DK / 16; ++t) S[t] = zero4();
   }
 
-  bf16_t* wscr = (bf16_t*)(smem + Q_::OFF_W + wave * Q_::WS);
+  bf16_t* wscr = sWS + wave * (Q_::WS / 2);
   bf16_t* wS = wscr;                  // S^T [16][LDK] (hi, lo)
-  bf16_t* wU = wscr;                  // U^T [16][LDT] hi, then lo
-  bf16_t* wVt = wscr + 2 * 16 * LDT;  // Vt^T [16][LDT] hi, then lo
+  bf16_t* wVt = wscr;                 // Vt^T [16][LDT] hi, then lo
   constexpr int WS_LO = 16 * LDK, W_LO = 16 * LDT;
 
   Prefetch<DK, MODE> pf;
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
           ss = group_sum_dpp<SEGS>(ss);
           const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = IS ? x[e] * inv : round_bf(x[e] * inv);
+          for (int e = 0; e < 8; ++e) x[e] *= inv;  // bf16 inputs: the bf16 pack below rounds
         }
         stage8<IS>((which == 0 ? sK : sQ) + r * LDK + seg * 8, K_LO, nullptr, 0, x);
       }
@@ -477,21 +478,18 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         for (int jt = 0; jt < K; ++jt) {
           const int rr = r - (K - 1) + jt;  // token row within the chunk
           float xv[8];
-          if (rr >= 0) {
-            const u32x4 w = *(const u32x4*)(rows + rr * ld + seg * 8);
-            unpack8<false>(&w, xv);
-          } else {
-            const u32x4 w = *(const u32x4*)(sHist + (3 + rr) * HW + ci);
-            unpack8<false>(&w, xv);
-          }
+          const bf16_t* src = rr >= 0 ? rows + rr * ld + seg * 8 : sHist + (3 + rr) * HW + ci;
+          const u32x4 w = *(const u32x4*)src;
+          unpack8<false>(&w, xv);
           const float4 w0 = *(const float4*)(sCW + jt * HW + ci);
           const float4 w1 = *(const float4*)(sCW + jt * HW + ci + 4);
           acc[0] += w0.x * xv[0]; acc[1] += w0.y * xv[1]; acc[2] += w0.z * xv[2]; acc[3] += w0.w * xv[3];
           acc[4] += w1.x * xv[4]; acc[5] += w1.y * xv[5]; acc[6] += w1.z * xv[6]; acc[7] += w1.w * xv[7];
         }
         float* y = isv ? yv[k - Q_::NI_KQ] : ykq[k];
+        const float keep = (float)(r < nvalid);  // padded rows are zero (branch-free)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = r < nvalid ? round_bf(siluf_(round_bf(acc[e]))) : 0.f;
+        for (int e = 0; e < 8; ++e) y[e] = round_bf(siluf_(round_bf(acc[e]))) * keep;
       }
       __syncthreads();
       // history for the next chunk: raw inputs of tokens 61..63 (still in the prefetch)
@@ -521,7 +519,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         ss = group_sum_dpp<SEGS>(ss);
         const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = round_bf(x[e] * inv);
+        for (int e = 0; e < 8; ++e) x[e] *= inv;  // rounded to bf16 by the pack in stage8
         stage8<false>((which == 0 ? sK : sQ) + r * LDK + seg * 8, 0, nullptr, 0, x);
       }
 #pragma unroll
@@ -538,20 +536,30 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     // tile (w, w), which it inverts itself right away, then four more.  L and P are
     // written transposed (one vector store per lane) and read back through
     // ds_read_b64_tr_b16 as row-major operands.
+    // Slot ti of wave w holds tile w + 4 ti: slot 0 is the wave's diagonal K K^T tile,
+    // slot 1 an off-diagonal K K^T tile, slots 3 and 4 Q K^T tiles, and slot 2 is
+    // K K^T for waves 0-1 and Q K^T for waves 2-3.
+    f32x4 tacc[5];
 #pragma unroll
-    for (int ti = 0; ti < 5; ++ti) {
-      const int tile = wave + 4 * ti;
-      const int code = tile_code(tile);
-      const bool qk = code & 16;
+    for (int ti = 0; ti < 5; ++ti) {  // all products first: no LDS stores in between
+      const int code = tile_code(wave + 4 * ti);
+      const bool qk = ti >= 3 || (ti == 2 && wave >= 2);
       const int bi = (code >> 2) & 3, bj = code & 3;
-      f32x4 acc = zero4();
+      tacc[ti] = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
         u32x4 ah, al, bh, bl;
         frag2<IS>(qk ? sQ : sK, K_LO, LDK, 16 * bi, 32 * s, ah, al);
         frag2<IS>(sK, K_LO, LDK, 16 * bj, 32 * s, bh, bl);
-        acc = mm<IS, IS>(acc, ah, al, bh, bl);
+        tacc[ti] = mm<IS, IS>(tacc[ti], ah, al, bh, bl);
       }
+    }
+#pragma unroll
+    for (int ti = 0; ti < 5; ++ti) {
+      const f32x4 acc = tacc[ti];
+      const int code = tile_code(wave + 4 * ti);
+      const bool qk = ti >= 3 || (ti == 2 && wave >= 2);
+      const int bi = (code >> 2) & 3, bj = code & 3;
       const int m = 16 * bj + lr;
       const float Gm = sG2[m];
       const float4 Gi = *(const float4*)(sG2 + 16 * bi + 4 * lq);
@@ -560,12 +568,15 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
       if (!qk) {
         const float4 Bi = *(const float4*)(sBeta + 16 * bi + 4 * lq);
         const float bt[4] = {Bi.x, Bi.y, Bi.z, Bi.w};
+        // branch-free: the exponent is clamped to <= 0 (the masked entries would
+        // overflow) and the strictly-lower mask multiplies the result
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int i = 16 * bi + 4 * lq + v;
-          val[v] = (i > m) ? bt[v] * acc[v] * __builtin_amdgcn_exp2f(gi[v] - Gm) : 0.f;
+          const float dec = __builtin_amdgcn_exp2f(fminf(gi[v] - Gm, 0.f));
+          val[v] = bt[v] * acc[v] * dec * (float)(i > m);
         }
-        if (bi == bj) {
+        if (ti == 0) {
           // this wave's diagonal block: T_ww = (I + L_ww)^-1 by forward substitution,
           // one column per lane (lanes 16..63 repeat the work and do not store)
 #pragma unroll
@@ -607,7 +618,8 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int i = 16 * bi + 4 * lq + v;
-          val[v] = (i >= m) ? p.scale * acc[v] * __builtin_amdgcn_exp2f(gi[v] - Gm) : 0.f;
+          const float dec = __builtin_amdgcn_exp2f(fminf(gi[v] - Gm, 0.f));
+          val[v] = p.scale * acc[v] * dec * (float)(i >= m);
         }
         if constexpr (OS) store_ct_split(sPT, sPT + P_LO, LDT, 16 * bi, 16 * bj, val);
         else store_ct_bf16(sPT, LDT, 16 * bi, 16 * bj, val);
@@ -659,8 +671,11 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
 
     // ------------------------------------------------------------ B2: the solve, per wave
-    // (I + L) U = R by block forward substitution; U^T stays in the scratch (hi, lo)
+    // (I + L) U = R by block forward substitution on 16x16x16 MFMAs.  A C-layout
+    // tile (lane (q, r) holds rows 4q..4q+3 of column r) is exactly the B operand
+    // layout of that MFMA, so R and U feed the next products from registers.
     f32x4 U[4];
+    u32x2 Uh[4], Ul[4];  // bf16 hi/lo of U blocks as B operands
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       f32x4 acc = R[b];
@@ -669,52 +684,57 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         // acc -= L_b,jb U_jb: the A operand is negated (a sign flip is exact in bf16)
         const u32x2 ah = rows4_tr(sLoT, LDT, 16 * jb, 16 * b) ^ 0x80008000u;
         const u32x2 al = rows4_tr(sLoT + LO_LO, LDT, 16 * jb, 16 * b) ^ 0x80008000u;
-        const u32x2 bh = frag4_bf16(wU, LDT, 0, 16 * jb);
-        const u32x2 bl = frag4_bf16(wU + W_LO, LDT, 0, 16 * jb);
-        acc = mm3k16(acc, ah, al, bh, bl);
+        acc = mm3k16(acc, ah, al, Uh[jb], Ul[jb]);
       }
-      store_ct_split(wU, wU + W_LO, LDT, 16 * b, 0, acc);
-      wave_lds_fence();
+      const u32x2 rh = u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])};
+      const u32x2 rl = u32x2{pack_bf16(lo_part(acc[0]), lo_part(acc[1])),
+                             pack_bf16(lo_part(acc[2]), lo_part(acc[3]))};
       const u32x2 th = rows4_tr(sTdT, LDD, 16 * b, 0);
       const u32x2 tl = rows4_tr(sTdT + TD_LO, LDD, 16 * b, 0);
-      const u32x2 rh = frag4_bf16(wU, LDT, 0, 16 * b);
-      const u32x2 rl = frag4_bf16(wU + W_LO, LDT, 0, 16 * b);
       U[b] = mm3k16(zero4(), th, tl, rh, rl);
-      wave_lds_fence();
-      store_ct_split(wU, wU + W_LO, LDT, 16 * b, 0, U[b]);
-      wave_lds_fence();
+      Uh[b] = u32x2{pack_bf16(U[b][0], U[b][1]), pack_bf16(U[b][2], U[b][3])};
+      Ul[b] = u32x2{pack_bf16(lo_part(U[b][0]), lo_part(U[b][1])),
+                    pack_bf16(lo_part(U[b][2]), lo_part(U[b][3]))};
     }
     // Vt = diag(e^{G_last - G}) V_new for the state update
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 vt;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) vt[v] = U[i][v] * sEL[16 * i + 4 * lq + v];
+      const float4 el = *(const float4*)(sEL + 16 * i + 4 * lq);
+      vt[0] = U[i][0] * el.x; vt[1] = U[i][1] * el.y; vt[2] = U[i][2] * el.z; vt[3] = U[i][3] * el.w;
       store_ct_split(wVt, wVt + W_LO, LDT, 16 * i, 0, vt);
     }
-    wave_lds_fence();
 
     // ------------------------------------------------------------ B3: O = scale e^G (Q S) + P V_new
     f32x4 OUT[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4& o = OUT[i];
+      const float4 eg = *(const float4*)(sEG + 16 * i + 4 * lq);
+      o[0] = p.scale * eg.x * QS[i][0]; o[1] = p.scale * eg.y * QS[i][1];
+      o[2] = p.scale * eg.z * QS[i][2]; o[3] = p.scale * eg.w * QS[i][3];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) o[v] = p.scale * sEG[16 * i + 4 * lq + v] * QS[i][v];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 1 && i < 2) continue;  // P is lower triangular
-        u32x4 ah, al, bh, bl;
-        ah = frag_tr(sPT, LDT, 32 * s, 16 * i);
-        al = OS ? frag_tr(sPT + P_LO, LDT, 32 * s, 16 * i) : ah;
-        frag2<OS>(wU, W_LO, LDT, 0, 32 * s, bh, bl);
-        o = mm<OS, OS>(o, ah, al, bh, bl);
+      for (int jb = 0; jb <= i; ++jb) {  // P is lower triangular
+        const u32x2 ah = rows4_tr(sPT, LDT, 16 * jb, 16 * i);
+        o = mma16k16(ah, Uh[jb], o);
+        if constexpr (OS) {
+          const u32x2 al = rows4_tr(sPT + P_LO, LDT, 16 * jb, 16 * i);
+          o = mma16k16(ah, Ul[jb], o);
+          o = mma16k16(al, Uh[jb], o);
+        }
       }
       if constexpr (MODE != MODE_LAYER) {
+        float* orow = p.o + (t0 * p.Hv + h) * (long long)DV + col0 + 16 * wave + lr;
+        const long long rs = (long long)p.Hv * DV;  // row stride of o
+        if (nvalid == C) {  // uniform: every row of a full chunk is stored
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int r = 16 * i + 4 * lq + v;
-          if (r < nvalid) p.o[((t0 + r) * p.Hv + h) * (long long)DV + col0 + 16 * wave + lr] = o[v];
+          for (int v = 0; v < 4; ++v) orow[(16 * i + 4 * lq + v) * rs] = o[v];
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = 16 * i + 4 * lq + v;
+            if (r < nvalid) orow[r * rs] = o[v];
+          }
         }
       } else {
 #pragma unroll
@@ -726,6 +746,7 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
     }
 
     // ------------------------------------------------------------ B4: S <- e^{G_last} S + K^T Vt
+    wave_lds_fence();  // Vt^T stores above are visible to the wave's fragment loads
     const float gl = sEG[C - 1];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {

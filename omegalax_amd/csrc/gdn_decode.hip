@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   __syncthreads();
 
   // L2 norm of q and k at the input precision (deltanet.py:30-32, 65-66)
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   if (wave < 2) {
     const float* src = wave == 0 ? s_q : s_k;
     float ss = 0.f;
