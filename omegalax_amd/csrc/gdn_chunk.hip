@@ -221,7 +221,8 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
     const int it = tid + k * NT;
     const int which = it / (C * Q_::SEGS);  // 0 = k, 1 = q
     const int r = (it / Q_::SEGS) % C, seg = it % Q_::SEGS;
-    // rows past the sequence end load the last valid row (in bounds) and are zeroed
+    // rows past the sequence end load the last valid row (in bounds); staging zeroes
+    // them, so the loaded registers are not touched until the data is needed
     const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
     if constexpr (MODE == MODE_LAYER) {
       const int ch = (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8;
@@ -231,9 +232,6 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
       const long long ld = which == 0 ? p.k_ld : p.q_ld;
       load_raw<F32>(base, tok * ld + (long long)hk * DK + seg * 8, pf.kq[k]);
     }
-    const unsigned keep = r < nvalid ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int w = 0; w < Q_::RAWW; ++w) pf.kq[k][w] &= keep;
   }
 #pragma unroll
   for (int k = 0; k < Q_::NI_V; ++k) {
@@ -246,9 +244,6 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
                       pf.v[k]);
     else
       load_raw<F32>(p.v, tok * p.v_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
-    const unsigned keep = r < nvalid ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int w = 0; w < Q_::RAWW; ++w) pf.v[k][w] &= keep;
   }
   pf.g0 = 0.f;
   pf.g1 = 0.f;
@@ -413,6 +408,9 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         const int r = (it / SEGS) % C, seg = it % SEGS;
         float x[8];
         unpack8<F32>(pf.kq[k], x);
+        const float keep = (float)(r < nvalid);  // padded rows are zero
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= keep;
         if (p.qk_l2norm) {
           float ss = 0.f;
 #pragma unroll
@@ -430,10 +428,14 @@ __global__ __launch_bounds__(NT) void chunk_kernel(ChunkParams p) {
         const int r = it / (BV / 8), seg = it % (BV / 8);
         float x[8];
         unpack8<F32>(pf.v[k], x);
+        const float keep = (float)(r < nvalid);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= keep;
         stage8<IS>(sV + r * LDT + seg * 8, V_LO, nullptr, 0, x);
       }
     } else {
-      // raw rows: q -> sQ, k -> sK, v -> sV; the conv reads them next
+      // raw rows: q -> sQ, k -> sK, v -> sV; the conv reads them next.  Padded rows
+      // (copies of the last valid row) feed only padded outputs, which are zeroed.
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         const int it = tid + k * NT;
