@@ -72,8 +72,15 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
                       int64_t chunk_size, float scale, int qk_l2norm, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/*
+ * Bytes of device workspace omx_gdn_chunk_fwd needs for these shapes and in_dtype
+ * (N = number of sequences).  It holds the per-(chunk, value head) records of the
+ * chunk-parallel preparation (the inverse T = (I + L)^-1 and P of each chunk,
+ * deltanet.py:100-113, 130-131, and the chunk's gate vectors), the normalised
+ * q and k, and the chunk offsets of packed sequences.  Pass it 256-byte aligned.
+ */
 size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
-                                        int64_t dk, int64_t dv, int64_t N);
+                                        int64_t dk, int64_t dv, int64_t N, int in_dtype);
 
 /*
  * GatedDeltaNet prefill from the projection outputs to the gated-norm output.
@@ -104,6 +111,12 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
                     int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Bytes of device workspace omx_gdn_prefill needs (256-byte aligned): the chunk
+ * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v, and
+ * when dv > 64 the unnormalised bf16 o and per-block sums of o^2 that the
+ * gated-norm epilogue combines.
+ */
 size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
                                       int64_t dv, int64_t N);
 

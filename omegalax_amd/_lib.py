@@ -31,7 +31,7 @@ SIGNATURES = {
     "omx_gdn_abi_version": (_i, []),
     "omx_gdn_chunk_fwd": (_i, [_p, _p, _p, _i, _p, _p, _p, _p, _i64, _p, _p,
                                _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _sz, _p]),
-    "omx_gdn_chunk_fwd_workspace_size": (_sz, [_i64] * 7),
+    "omx_gdn_chunk_fwd_workspace_size": (_sz, [_i64] * 7 + [_i]),
     "omx_gdn_prefill": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _i64, _p, _p, _p, _p, _p,
                              _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "omx_gdn_prefill_workspace_size": (_sz, [_i64] * 7),

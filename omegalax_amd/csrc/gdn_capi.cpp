@@ -49,6 +49,47 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
     if (!(cond)) return fail(OMX_GDN_EINVAL, __VA_ARGS__); \
   } while (0)
 
+// Workspace of the chunked prefill, offsets aligned to 256 bytes: the records of
+// the preparation kernel (one per chunk slot and value head; a sequence adds at
+// most one partial chunk, so ceil(tokens/64) + N slots cover any packing), the
+// normalised k and q, (layer) the conv output of v and the split-dv norm
+// buffers, and the chunk offsets of packed sequences.
+struct ChunkWs {
+  size_t rec, kn, qn, vc, opart, sspart, off, total;
+};
+
+ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
+                 int mode) {
+  ChunkWs w{};
+  if (B < 0 || T < 0 || Hk < 0 || Hv < 0 || dk < 0 || dv < 0 || N < 0) return w;
+  const size_t tokens = (size_t)(B * T);
+  const size_t slots = (tokens + 63) / 64 + (size_t)N;
+  const size_t elem = mode == omx::kModeF32 ? 4 : 2;
+  size_t o = 0;
+  w.rec = o;
+  o += align_up(slots * (size_t)Hv * (size_t)omx::chunk_record_bytes(mode), 256);
+  w.kn = o;
+  o += align_up(tokens * (size_t)(Hk * dk) * elem, 256);
+  w.qn = o;
+  o += align_up(tokens * (size_t)(Hk * dk) * elem, 256);
+  if (mode == omx::kModeLayer) {
+    w.vc = o;
+    o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
+    const int64_t cols = omx::chunk_block_cols();
+    if (dv > cols) {
+      const size_t nb = (size_t)((dv + cols - 1) / cols);
+      w.opart = o;
+      o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
+      w.sspart = o;
+      o += align_up(tokens * (size_t)Hv * nb * 4, 256);
+    }
+  }
+  w.off = o;
+  o += align_up((size_t)(N + 1) * 4, 256);
+  w.total = o;
+  return w;
+}
+
 int check_heads(const char* fn, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv) {
   REQUIRE(Hk >= 1 && Hv >= 1, "%s: head counts must be positive (Hk=%lld, Hv=%lld)", fn,
           (long long)Hk, (long long)Hv);
@@ -66,7 +107,7 @@ extern "C" {
 
 const char* omx_gdn_last_error(void) { return g_last_error.c_str(); }
 
-int omx_gdn_abi_version(void) { return 100; }
+int omx_gdn_abi_version(void) { return 101; }
 
 int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
                         const float* conv_w, const float* A_log, const float* dt_bias,
@@ -126,11 +167,53 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
 }  // extern "C"
 
 // ---------------------------------------------------------------------------- prefill
+namespace {
+
+// Point the kernels at the workspace and launch: chunk plan (packed sequences),
+// preparation over all chunks, then the scan; all on `stream`, in order.
+hipError_t launch_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int mode,
+                          hipStream_t stream) {
+  char* base = (char*)workspace;
+  p.nch = (p.T + 63) / 64;
+  p.n_rec = p.cu_seqlens ? (int)((p.T + 63) / 64 + p.N) : p.N * p.nch;
+  p.rec = (unsigned char*)(base + ws.rec);
+  p.chunk_off = p.cu_seqlens ? (int32_t*)(base + ws.off) : nullptr;
+  const bool norm = p.qk_l2norm || mode == omx::kModeLayer;
+  p.kn = norm ? base + ws.kn : nullptr;
+  p.qn = norm ? base + ws.qn : nullptr;
+  if (norm) {
+    p.ks = p.kn;
+    p.qs = p.qn;
+    p.ks_ld = p.qs_ld = (long long)p.Hk * p.dk;
+  } else {
+    p.ks = p.k;
+    p.qs = p.q;
+    p.ks_ld = p.k_ld;
+    p.qs_ld = p.q_ld;
+  }
+  if (mode == omx::kModeLayer) {
+    p.vc = base + ws.vc;
+    p.vs = p.vc;
+    p.vs_ld = (long long)p.Hv * p.DV;
+  } else {
+    p.vs = p.v;
+    p.vs_ld = p.v_ld;
+  }
+  hipError_t e = hipSuccess;
+  if (p.cu_seqlens) e = omx::launch_chunk_plan(p, stream);
+  if (e == hipSuccess) e = omx::launch_prep(p, mode, stream);
+  if (e == hipSuccess) e = omx::launch_scan(p, mode, stream);
+  return e;
+}
+
+}  // namespace
+
 extern "C" {
 
-size_t omx_gdn_chunk_fwd_workspace_size(int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                        int64_t) {
-  return 0;  // the chunked kernel keeps every intermediate in registers and LDS
+size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                        int64_t dv, int64_t N, int in_dtype) {
+  return chunk_ws(B, T, Hk, Hv, dk, dv, N,
+                  in_dtype == OMX_GDN_F32 ? omx::kModeF32 : omx::kModeBF16).total;
 }
 
 int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
@@ -139,8 +222,6 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
                       int64_t Hv, int64_t dk, int64_t dv, int64_t chunk_size, float scale,
                       int qk_l2norm, void* workspace, size_t workspace_bytes, void* stream) {
   const char* fn = "omx_gdn_chunk_fwd";
-  (void)workspace;
-  (void)workspace_bytes;
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
@@ -160,7 +241,13 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   if (!omx::chunk_dims_supported((int)dk, (int)dv, f32))
     return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled for %s inputs",
                 fn, (long long)dk, (long long)dv, f32 ? "fp32" : "bf16");
+  const int mode = f32 ? omx::kModeF32 : omx::kModeBF16;
+  const ChunkWs ws = chunk_ws(B, T, Hk, Hv, dk, dv, N, mode);
+  REQUIRE(workspace_bytes >= ws.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, ws.total);
   if (N == 0 || (B * T == 0 && !final_state)) return ok();
+  REQUIRE(workspace && aligned(workspace, 256), "%s: workspace must be non-NULL and 256-byte aligned",
+          fn);
   REQUIRE(o || B * T == 0, "%s: o is NULL", fn);
   if (B * T > 0) REQUIRE(q && k && v && g && beta, "%s: a required pointer is NULL", fn);
   const size_t al = f32 ? 16 : 16;
@@ -175,21 +262,13 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   p.nb = (int)(dv / omx::chunk_block_cols());
   p.scale = scale; p.qk_l2norm = qk_l2norm ? 1 : 0;
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
-  return launch_status(omx::launch_chunk(p, f32, (hipStream_t)stream), fn);
+  REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
+  return launch_status(launch_chunked(p, ws, workspace, mode, (hipStream_t)stream), fn);
 }
 
 size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
                                       int64_t dv, int64_t N) {
-  (void)Hk;
-  (void)dk;
-  (void)N;
-  // dv wider than one workgroup's column block: bf16 o and per-block sums of o^2
-  const int64_t cols = omx::chunk_block_cols();
-  if (dv <= cols || B <= 0 || T <= 0 || Hv <= 0) return 0;
-  const int64_t nb = (dv + cols - 1) / cols;
-  const int64_t rows = B * T * Hv;
-  const size_t o_bytes = align_up((size_t)(rows * dv * 2), 256);
-  return o_bytes + align_up((size_t)(rows * nb * 4), 256);
+  return chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer).total;
 }
 
 int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
@@ -217,7 +296,8 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   if (!omx::layer_dims_supported((int)dk, (int)dv))
     return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled", fn,
                 (long long)dk, (long long)dv);
-  const size_t need = omx_gdn_prefill_workspace_size(B, T, Hk, Hv, dk, dv, N);
+  const ChunkWs ws = chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer);
+  const size_t need = ws.total;
   REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes is smaller than the %zu needed", fn,
           workspace_bytes, need);
   if (N == 0) return ok();
@@ -225,10 +305,10 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   if (tokens > 0)
     REQUIRE(mixed_qkv && z && a && b && out, "%s: an activation pointer is NULL", fn);
   REQUIRE(conv_w && A_log && dt_bias && norm_w, "%s: a parameter pointer is NULL", fn);
-  REQUIRE(need == 0 || workspace, "%s: workspace is NULL", fn);
+  REQUIRE(workspace && aligned(workspace, 256), "%s: workspace must be non-NULL and 256-byte aligned",
+          fn);
   REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 16) && aligned(out, 16)),
           "%s: mixed_qkv, z and out must be 16-byte aligned", fn);
-  REQUIRE(!workspace || aligned(workspace, 16), "%s: workspace must be 16-byte aligned", fn);
   omx::ChunkParams p{};
   p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b;
   p.conv_w = conv_w; p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w;
@@ -242,11 +322,12 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   p.eps = eps;
   p.qk_l2norm = 1;
   if (p.nb > 1) {
-    p.o_part = workspace;
-    p.ss_part = (float*)((char*)workspace + align_up((size_t)(tokens * Hv * dv * 2), 256));
+    p.o_part = (char*)workspace + ws.opart;
+    p.ss_part = (float*)((char*)workspace + ws.sspart);
   }
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
-  hipError_t e = omx::launch_layer(p, (hipStream_t)stream);
+  REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
+  hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
   if (e == hipSuccess && p.nb > 1)
     e = omx::launch_norm_epilogue(p.o_part, p.ss_part, z, norm_w, out, tokens * Hv, (int)dv, p.nb,
                                   eps, (hipStream_t)stream);

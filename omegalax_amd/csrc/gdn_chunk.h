@@ -1,0 +1,129 @@
+// Shared definitions of the two chunked-prefill kernels: the chunk-parallel
+// preparation kernel (gdn_prep.hip) and the recurrent scan (gdn_chunk.hip).
+//
+// The preparation kernel writes, for every (chunk, value head), a record that
+// the scan reads back in one piece:
+//   T = (I + L)^-1, the inverse of the chunk's unit lower-triangular system
+//       (deltanet.py:100-113), as bf16 hi + lo MFMA A-operand fragments;
+//   P = lower(scale (q_i . k_j) e^{G_i - G_j}) (deltanet.py:130-131), bf16 (hi + lo
+//       for fp32 inputs), as A-operand fragments;
+//   the gate vectors beta, beta e^G, e^G and e^{G_last - G} (fp32).
+// A 16x16 tile (bi, bj) of a 64x64 lower-triangular matrix M is stored as the
+// 16x16x16 MFMA A operand: lane (q, r) = (lane / 16, lane % 16) holds
+// M[16 bi + r][16 bj + 4q .. 4q + 3] as four bf16 in one 8-byte word; tile
+// index bi (bi + 1) / 2 + bj, 512 bytes per tile, lanes in order.
+#pragma once
+
+#include "gdn_common.h"
+#include "gdn_kernels.h"
+#include "gdn_mfma.h"
+
+namespace omx {
+
+constexpr int kC = 64;      // chunk length (deltanet.py:59)
+constexpr int kNT = 256;    // threads per workgroup in both kernels
+constexpr int kLDT = kC + 8;   // row stride (elements) of 64-wide bf16 LDS arrays
+constexpr int kLDD = 16 + 4;   // row stride of 16-wide LDS arrays
+constexpr int MODE_BF16 = kModeBF16, MODE_F32 = kModeF32, MODE_LAYER = kModeLayer;
+
+// record layout (bytes)
+constexpr int kTileBytes = 64 * 8;           // one A-operand tile, all lanes
+constexpr int kRecT = 0;                     // 10 tiles x {hi, lo}
+constexpr int kRecP = kRecT + 20 * kTileBytes;  // 10 tiles (hi)
+constexpr int kRecG = kRecP + 10 * kTileBytes;  // 4 x 64 fp32 gate vectors
+constexpr int kRecPL = kRecG + 4 * kC * 4;      // fp32 inputs: 10 tiles of P lo parts
+constexpr int kRecBytesBF16 = kRecPL;           // 16384
+constexpr int kRecBytesF32 = kRecPL + 10 * kTileBytes;  // 21504
+constexpr int kGateBeta = 0, kGateBE = 1, kGateEG = 2, kGateEL = 3;  // rows of the gate block
+
+__host__ __device__ constexpr int rec_bytes(int mode) {
+  return mode == MODE_F32 ? kRecBytesF32 : kRecBytesBF16;
+}
+__host__ __device__ constexpr int tile_index(int bi, int bj) { return bi * (bi + 1) / 2 + bj; }
+
+template <bool AS, bool BS>
+__device__ __forceinline__ f32x4 mm(f32x4 acc, u32x4 ah, u32x4 al, u32x4 bh, u32x4 bl) {
+  acc = mma16(ah, bh, acc);
+  if constexpr (BS) acc = mma16(ah, bl, acc);
+  if constexpr (AS) acc = mma16(al, bh, acc);
+  return acc;
+}
+
+// acc += (ah + al)(bh + bl) without the lo*lo term, 16x16x16
+__device__ __forceinline__ f32x4 mm3k16(f32x4 acc, u32x2 ah, u32x2 al, u32x2 bh, u32x2 bl) {
+  acc = mma16k16(ah, bh, acc);
+  acc = mma16k16(ah, bl, acc);
+  acc = mma16k16(al, bh, acc);
+  return acc;
+}
+
+template <bool SPLIT>
+__device__ __forceinline__ void frag2(const bf16_t* base, int lo_off, int ld, int row0, int k0,
+                                      u32x4& hi, u32x4& lo) {
+  hi = frag_bf16(base, ld, row0, k0);
+  if constexpr (SPLIT) lo = frag_bf16(base + lo_off, ld, row0, k0);
+  else lo = hi;
+}
+
+// bf16 hi and lo parts of a C-layout tile, packed as a 16x16x16 B operand
+__device__ __forceinline__ u32x2 pack_hi4(f32x4 x) {
+  return u32x2{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
+}
+__device__ __forceinline__ u32x2 pack_lo4(f32x4 x) {
+  return u32x2{pack_bf16(lo_part(x[0]), lo_part(x[1])), pack_bf16(lo_part(x[2]), lo_part(x[3]))};
+}
+
+// unpack 8 input values (bf16 or fp32) from raw load words
+template <bool F32>
+__device__ __forceinline__ void unpack8(const u32x4* w, float* x) {
+  if constexpr (F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = __uint_as_float(w[0][e]);
+      x[4 + e] = __uint_as_float(w[1][e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = __uint_as_float(w[0][e] << 16);
+      x[2 * e + 1] = __uint_as_float(w[0][e] & 0xffff0000u);
+    }
+  }
+}
+
+template <bool F32>
+__device__ __forceinline__ void load_raw(const void* base, long long elem, u32x4* w) {
+  if constexpr (F32) {
+    const u32x4* p = (const u32x4*)((const float*)base + elem);
+    w[0] = p[0];
+    w[1] = p[1];
+  } else {
+    w[0] = *(const u32x4*)((const bf16_t*)base + elem);
+  }
+}
+
+// 8 values -> packed bf16 words (hi, or the lo parts)
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+  return u32x4{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]),
+               pack_bf16(x[6], x[7])};
+}
+__device__ __forceinline__ u32x4 pack8_lo(const float* x) {
+  return u32x4{pack_bf16(lo_part(x[0]), lo_part(x[1])), pack_bf16(lo_part(x[2]), lo_part(x[3])),
+               pack_bf16(lo_part(x[4]), lo_part(x[5])), pack_bf16(lo_part(x[6]), lo_part(x[7]))};
+}
+
+// Sequence n's token range [s0, s1): packed by cu_seqlens (clamped to [0, T], so a
+// malformed offsets array cannot index out of bounds) or batch row n.
+__device__ __forceinline__ void seq_range(const int32_t* cu, int n, int T, long long& s0,
+                                          long long& s1) {
+  if (cu) {
+    const long long lo = cu[n], hi = cu[n + 1];
+    s0 = lo < 0 ? 0 : (lo > T ? T : lo);
+    s1 = hi < s0 ? s0 : (hi > T ? T : hi);
+  } else {
+    s0 = (long long)n * T;
+    s1 = s0 + T;
+  }
+}
+
+}  // namespace omx

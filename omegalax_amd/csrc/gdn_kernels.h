@@ -66,13 +66,33 @@ struct ChunkParams {
   int N, T, Hk, Hv, dk, DV, nb, conv_k, conv_dim;
   float scale, eps;
   int qk_l2norm;
+  // workspace written by the preparation kernel, read by the scan
+  void* kn;                    // normalised k [tokens, Hk, dk] in the input precision, or null
+  void* qn;                    // normalised q, likewise
+  void* vc;                    // layer: conv + SiLU output of v [tokens, Hv, DV] bf16
+  unsigned char* rec;          // per (chunk, value head) records, layout in gdn_chunk.h
+  int32_t* chunk_off;          // cu_seqlens: [N+1] first chunk index of each sequence; else null
+  int nch;                     // chunks per sequence without cu_seqlens
+  int n_rec;                   // chunk slots the preparation kernel covers
+  // the scan's k, q, v rows: kn/qn/vc or the raw inputs, with row strides (elements)
+  const void* ks;
+  const void* qs;
+  const void* vs;
+  long long ks_ld, qs_ld, vs_ld;
 };
+
+// kernel modes of the chunked prefill (template arguments of both kernels)
+constexpr int kModeBF16 = 0, kModeF32 = 1, kModeLayer = 2;
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs);
 int chunk_block_cols();
-hipError_t launch_chunk(const ChunkParams& p, bool f32_inputs, hipStream_t stream);
 bool layer_dims_supported(int dk, int dv);
-hipError_t launch_layer(const ChunkParams& p, hipStream_t stream);
+// bytes of one (chunk, value head) record for a mode
+int chunk_record_bytes(int mode);
+// cu_seqlens -> chunk_off (one workgroup); then the preparation kernel and the scan
+hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);
+hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream);
+hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream);
 
 // Gated RMSNorm over dv split across nb workgroups: out = w * o * rsqrt(sum/dv + eps) * silu(z).
 hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,

@@ -111,7 +111,7 @@ def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=6
     fs = torch.empty((N, H, A, U), dtype=torch.float32, device=dev) if output_final_state else None
     sc = float(A ** -0.5) if scale is None else float(scale)
     L = _lib.lib()
-    ws_bytes = L.omx_gdn_chunk_fwd_workspace_size(B, T, Hk, H, A, U, N)
+    ws_bytes = L.omx_gdn_chunk_fwd_workspace_size(B, T, Hk, H, A, U, N, _dtype_code(q))
     ws = _workspace(ws_bytes, dev)
     _lib.call("omx_gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), _dtype_code(q), _ptr(g), _ptr(beta),
               _ptr(initial_state), _ptr(cu_seqlens), N, _ptr(o), _ptr(fs), B, T, Hk, H, A, U,
