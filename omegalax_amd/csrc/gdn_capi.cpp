@@ -52,8 +52,8 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Workspace of the chunked prefill, offsets aligned to 256 bytes: the records of
 // the preparation kernel (one per chunk slot and value head; a sequence adds at
 // most one partial chunk, so ceil(tokens/64) + N slots cover any packing), the
-// normalised k and q, (layer) the conv output of v and the split-dv norm
-// buffers, and the chunk offsets of packed sequences.
+// normalised k and q, (layer) the conv output of v, the bf16 o and the partial
+// sums of o^2 for the gated norm, and the chunk offsets of packed sequences.
 struct ChunkWs {
   size_t rec, kn, qn, vc, opart, sspart, off, total;
 };
@@ -75,14 +75,10 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
   if (mode == omx::kModeLayer) {
     w.vc = o;
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
-    const int64_t cols = omx::chunk_block_cols();
-    if (dv > cols) {
-      const size_t nb = (size_t)((dv + cols - 1) / cols);
-      w.opart = o;
-      o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
-      w.sspart = o;
-      o += align_up(tokens * (size_t)Hv * nb * 4, 256);
-    }
+    w.opart = o;
+    o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
+    w.sspart = o;
+    o += align_up(tokens * (size_t)Hv * (size_t)omx::layer_norm_parts((int)dv) * 4, 256);
   }
   w.off = o;
   o += align_up((size_t)(N + 1) * 4, 256);
@@ -321,16 +317,14 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   p.scale = 1.0f / sqrtf((float)dk);
   p.eps = eps;
   p.qk_l2norm = 1;
-  if (p.nb > 1) {
-    p.o_part = (char*)workspace + ws.opart;
-    p.ss_part = (float*)((char*)workspace + ws.sspart);
-  }
+  p.o_part = (char*)workspace + ws.opart;
+  p.ss_part = (float*)((char*)workspace + ws.sspart);
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
   REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
-  if (e == hipSuccess && p.nb > 1)
-    e = omx::launch_norm_epilogue(p.o_part, p.ss_part, z, norm_w, out, tokens * Hv, (int)dv, p.nb,
-                                  eps, (hipStream_t)stream);
+  if (e == hipSuccess)
+    e = omx::launch_norm_epilogue(p.o_part, p.ss_part, z, norm_w, out, tokens * Hv, (int)dv,
+                                  omx::layer_norm_parts((int)dv), eps, (hipStream_t)stream);
   return launch_status(e, fn);
 }
 

@@ -25,10 +25,10 @@
 // so does the state-update operand diag(e^{G_last-G}) V_new; with bf16 inputs S
 // enters K S / Q S, and P, V_new enter P V_new, as single bf16.
 //
-// Modes: MODE_BF16 / MODE_F32 (core function) store o in fp32.  MODE_LAYER ends
-// in the gated RMSNorm (deltanet.py:282-293): fused when one workgroup holds all
-// of dv, otherwise through a bf16 o buffer and per-token partial sums of o^2 that
-// the epilogue kernel (gdn_epilogue.hip) normalises.
+// Modes: MODE_BF16 / MODE_F32 (core function) store o in fp32.  MODE_LAYER stores
+// o in bf16 with each wavefront's partial sums of o^2 per token; the epilogue
+// kernel (gdn_epilogue.hip) adds them and applies the gated RMSNorm
+// (deltanet.py:282-293).
 #include <type_traits>
 
 #include "gdn_chunk.h"
@@ -63,7 +63,7 @@ struct Cfg {
   static constexpr int WS_U = 2 * 16 * LDT * 2;
   static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
   static constexpr int TOTAL =
-      2 * NS * C * LDK * 2 + NS * C * LDT * 2 + REC + NWC * WS + (MODE == MODE_LAYER ? C * NWC * 4 : 0);
+      2 * NS * C * LDK * 2 + NS * C * LDT * 2 + REC + NWC * WS;
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
   static_assert(NI_KQ * NT == 2 * C * SEGS && (C * SEGS) % NT == 0, "item split");
@@ -113,7 +113,9 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
 }
 
 template <int DK, int MODE>
-__global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
+// One workgroup per CU is the design point (the state fills the register file), so the
+// compiler may use the whole file instead of holding back for a second workgroup.
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void scan_kernel(ChunkParams p) {
   using Q_ = Cfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
@@ -125,7 +127,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
   __shared__ __align__(16) bf16_t sV[Q_::NS * C * LDT];
   __shared__ __align__(16) unsigned char sRec[Q_::REC];     // the chunk's record
   __shared__ __align__(16) bf16_t sWS[NWC * Q_::WS / 2];    // per-wave scratch
-  __shared__ __align__(16) float sNP[MODE == MODE_LAYER ? C * NWC : 4];  // layer: [token][wave] sums of o^2
   const float* sGate = (const float*)(sRec + kRecG);
   const float* sBeta = sGate + kGateBeta * C;  // beta
   const float* sBE = sGate + kGateBE * C;      // beta e^G
@@ -349,10 +350,19 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
           }
         }
       } else {
+        // unnormalised o in bf16 and this wave's share of sum(o^2) over its 16
+        // columns; the epilogue kernel adds the shares and applies the norm
+        const int col = col0 + 16 * wave + lr;
+        const int nparts = nb * NWC;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float ss = group_sum_dpp<16>(o[v] * o[v]);
-          if (lr == 0) sNP[(16 * i + 4 * lq + v) * NWC + wave] = ss;
+          const int r = 16 * i + 4 * lq + v;
+          if (r < nvalid) {
+            const size_t row = (size_t)(t0 + r) * p.Hv + h;
+            ((bf16_t*)p.o_part)[row * DV + col] = f2bf(o[v]);
+            if (lr == 0) p.ss_part[row * nparts + blk * NWC + wave] = ss;
+          }
         }
       }
     }
@@ -371,34 +381,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(ChunkParams p) {
         al = IS ? frag_tr(sK + K_LO, LDK, 32 * s, 16 * t) : ah;
         frag2<true>(wVt, W_LO, LDT, 0, 32 * s, bh, bl);
         S[t] = mm<IS, true>(S[t], ah, al, bh, bl);
-      }
-    }
-
-    if constexpr (MODE == MODE_LAYER) {
-      // gated RMSNorm epilogue (deltanet.py:282-293), fp32 like the reference
-      __syncthreads();
-      const int col = col0 + 16 * wave + lr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int r = 16 * i + 4 * lq + v;
-          if (r < nvalid) {
-            float ss = 0.f;
-#pragma unroll
-            for (int w2 = 0; w2 < NWC; ++w2) ss += sNP[r * NWC + w2];
-            const size_t idx = ((size_t)(t0 + r) * p.Hv + h) * DV + col;
-            if (nb == 1) {
-              const float rn = rsqrtf(ss / (float)DV + p.eps);
-              const float zz = bf2f(((const bf16_t*)p.z)[idx]);
-              ((bf16_t*)p.out)[idx] = f2bf(p.norm_w[col] * (OUT[i][v] * rn) * siluf_(zz));
-            } else {
-              // unnormalised o in bf16 and this block's share of sum(o^2)
-              ((bf16_t*)p.o_part)[idx] = f2bf(OUT[i][v]);
-              if (wave == 0 && lr == 0) p.ss_part[((size_t)(t0 + r) * p.Hv + h) * nb + blk] = ss;
-            }
-          }
-        }
       }
     }
   }
@@ -451,6 +433,8 @@ hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
 int chunk_block_cols() { return BV; }
 
 int chunk_record_bytes(int mode) { return rec_bytes(mode); }
+
+int layer_norm_parts(int dv) { return dv / BV * NWC; }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
   if (dv % BV != 0 || dv > 256) return false;

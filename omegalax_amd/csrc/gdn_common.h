@@ -67,4 +67,24 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
   return v;
 }
 
+// DPP move restricted to the rows in ROW_MASK; other rows (and lanes whose source
+// is outside the row) read 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_rows(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes: shifts by 1, 2, 4, 8 within each row of
+// 16 lanes, then lane 15 of rows 0 and 2 is added into rows 1 and 3 (row_bcast:15)
+// and lane 31 into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ float wave_scan_dpp(float v) {
+  v += dpp_rows<0x111, 0xf>(v);
+  v += dpp_rows<0x112, 0xf>(v);
+  v += dpp_rows<0x114, 0xf>(v);
+  v += dpp_rows<0x118, 0xf>(v);
+  v += dpp_rows<0x142, 0xa>(v);
+  v += dpp_rows<0x143, 0xc>(v);
+  return v;
+}
+
 }  // namespace omx

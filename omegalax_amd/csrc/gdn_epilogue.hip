@@ -1,11 +1,12 @@
-// Gated RMSNorm epilogue for prefills whose dv is split across workgroups.
+// Gated RMSNorm epilogue of the layer prefill.
 //
 // deltanet.py:282-293 normalises each (token, value head) row of the fp32 core
-// output: out = w * o * rsqrt(mean(o^2) + eps) * silu(z).  When the chunked
-// kernel splits dv over nb workgroups, each writes its columns of o (bf16) and
-// its share of sum(o^2) (fp32, from the fp32 o); this kernel adds the shares
-// and applies the norm.  Memory-bound: two bf16 reads and one bf16 write per
-// element, one thread per 8 columns (16-byte accesses).
+// output: out = w * o * rsqrt(mean(o^2) + eps) * silu(z).  The chunked scan
+// spreads a row's dv columns over several wavefronts (and workgroups); each
+// writes its columns of o (bf16) and its share of sum(o^2) (fp32, from the fp32
+// o).  This kernel adds the nparts shares and applies the norm.  Memory-bound:
+// two bf16 reads and one bf16 write per element, one thread per 8 columns
+// (16-byte accesses).
 #include "gdn_common.h"
 #include "gdn_kernels.h"
 
@@ -18,7 +19,7 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
                                                             const uint4* __restrict__ z,
                                                             const float* __restrict__ norm_w,
                                                             uint4* __restrict__ out,
-                                                            long long octets, int dv, int nb,
+                                                            long long octets, int dv, int nparts,
                                                             float eps) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i >= octets) return;
@@ -26,7 +27,7 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
   const long long row = i / per_row;
   const int c = 8 * (int)(i % per_row);
   float ss = 0.f;
-  for (int b = 0; b < nb; ++b) ss += ss_part[row * nb + b];
+  for (int b = 0; b < nparts; ++b) ss += ss_part[row * nparts + b];
   const float rn = rsqrtf(ss / (float)dv + eps);
   const uint4 ow = o_part[i], zw = z[i];
   const uint32_t ov[4] = {ow.x, ow.y, ow.z, ow.w}, zv[4] = {zw.x, zw.y, zw.z, zw.w};
@@ -44,14 +45,14 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
 }  // namespace
 
 hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,
-                                const float* norm_w, void* out, long long rows, int dv, int nb,
+                                const float* norm_w, void* out, long long rows, int dv, int nparts,
                                 float eps, hipStream_t stream) {
   const long long octets = rows * (dv / 8);
   if (octets == 0) return hipSuccess;
   const unsigned grid = (unsigned)((octets + 255) / 256);
   hipLaunchKernelGGL(norm_epilogue_kernel, dim3(grid), dim3(256), 0, stream,
                      (const uint4*)o_part, ss_part, (const uint4*)z, norm_w, (uint4*)out, octets,
-                     dv, nb, eps);
+                     dv, nparts, eps);
   return hipGetLastError();
 }
 

@@ -57,8 +57,8 @@ struct ChunkParams {
   const void* conv_state_in;   // [N, conv_dim, K-1] bf16 or null
   void* conv_state_out;        // [N, conv_dim, K-1] bf16 or null
   void* out;                   // [tokens, Hv*DV] bf16
-  void* o_part;                // nb > 1: unnormalised o [tokens, Hv, DV] bf16 (workspace)
-  float* ss_part;              // nb > 1: per-block sums of o^2 [tokens, Hv, nb] (workspace)
+  void* o_part;                // unnormalised o [tokens, Hv, DV] bf16 (workspace)
+  float* ss_part;              // partial sums of o^2 [tokens, Hv, layer_norm_parts(DV)] (workspace)
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
@@ -94,10 +94,13 @@ hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);
 hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream);
 hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream);
 
-// Gated RMSNorm over dv split across nb workgroups: out = w * o * rsqrt(sum/dv + eps) * silu(z).
+// Gated RMSNorm of the layer prefill from bf16 o and nparts partial sums of o^2 per
+// row: out = w * o * rsqrt(sum/dv + eps) * silu(z).
 hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,
-                                const float* norm_w, void* out, long long rows, int dv, int nb,
+                                const float* norm_w, void* out, long long rows, int dv, int nparts,
                                 float eps, hipStream_t stream);
+// partial sums of o^2 per (token, value head) row that the layer scan writes
+int layer_norm_parts(int dv);
 
 bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();

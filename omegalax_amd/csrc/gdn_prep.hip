@@ -16,6 +16,13 @@
 //     T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj,
 // on 16x16x16 MFMAs with hi+lo bf16 operands (fp32-accurate products).  The
 // outputs go to the per-(chunk, value head) record described in gdn_chunk.h.
+//
+// Layouts without transposes.  An MFMA result tile C = A B sits in registers as
+// lane (q, r) holding C[4q..4q+3][r]; read the other way round that is the
+// A-operand fragment of C^T.  So every tile that must leave as an A fragment is
+// computed transposed: the Gram tiles with the block roles swapped (K K^T is
+// symmetric; (Q K^T)^T = K Q^T), and the off-diagonal T blocks a second time as
+// T_ij^T = -X^T T_ii^T from the same two operands.
 #include "gdn_chunk.h"
 #include "gdn_kernels.h"
 
@@ -23,7 +30,7 @@ namespace omx {
 
 namespace {
 
-constexpr int C = kC, NT = kNT, LDT = kLDT, LDD = kLDD;
+constexpr int C = kC, NT = kNT, LDD = kLDD;
 
 template <int DK, int MODE>
 struct PrepCfg {
@@ -54,43 +61,12 @@ __device__ __forceinline__ int tile_code(int t) {
   return t < 12 ? (int)((kTilesLo >> (5 * t)) & 31) : (int)((kTilesHi >> (5 * (t - 12))) & 31);
 }
 
-// Causal depthwise conv + SiLU of 8 consecutive channels ch0.. at token row r of
-// the chunk (deltanet.py:35-50, 243): taps reach back K-1 tokens, into
-// conv_state_in (or zeros) before the sequence start.  Inputs, weights (cast to
-// bf16 as at :243), the conv sum and the SiLU output are rounded to bf16 like the
-// reference's bf16 ops; the sum itself accumulates in fp32.
-__device__ __forceinline__ void conv8(const ChunkParams& p, int n, long long s0, long long tok,
-                                      int ch0, const float (*wt)[4], float* y) {
-  const int K = p.conv_k;
-  float acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {  // token tok - d, weight tap K-1-d
-    if (d >= K) break;           // uniform
-    const long long t = tok - d;
-    float xv[8];
-    if (t >= s0) {
-      const u32x4 w = *(const u32x4*)((const bf16_t*)p.mixed_qkv + t * p.conv_dim + ch0);
-      unpack8<false>(&w, xv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[e] = 0.f;
-      if (p.conv_state_in) {
-        const int slot = (K - 1) - (int)(s0 - t);  // cache slot of time t (oldest first)
-        const bf16_t* cs = (const bf16_t*)p.conv_state_in + ((size_t)n * p.conv_dim + ch0) * (K - 1);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = bf2f(cs[e * (K - 1) + slot]);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += wt[e][d] * xv[e];
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = round_bf(siluf_(round_bf(acc[e])));
+__device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
+  *(u32x2*)(rec + off + lane_id() * 8) = f;
 }
 
-// conv weights of channels ch0..ch0+7, cast to bf16: wt[e][d] multiplies token t - d
+// conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243:
+// wt[e][d] multiplies the input d tokens back (tap K-1-d); taps beyond K are 0
 __device__ __forceinline__ void load_conv_w(const ChunkParams& p, int ch0, float (*wt)[4]) {
   const int K = p.conv_k;
 #pragma unroll
@@ -101,21 +77,180 @@ __device__ __forceinline__ void load_conv_w(const ChunkParams& p, int ch0, float
   }
 }
 
-// A C-layout tile (lane (q, r) holds rows 4q..4q+3 of column r) -> its A-operand
-// fragment (lane (q, r) holds row r, columns 4q..4q+3), through the wave's
-// scratch: stored transposed, read back with ds_read_b64_tr_b16.
-__device__ __forceinline__ u32x2 to_afrag(bf16_t* scr, f32x4 x, bool lo) {
-  const int l = lane_id();
-  const f32x4 y = lo ? f32x4{lo_part(x[0]), lo_part(x[1]), lo_part(x[2]), lo_part(x[3])} : x;
-  *(u32x2*)(scr + (l & 15) * LDD + 4 * (l >> 4)) = pack_hi4(y);
-  wave_lds_fence();
-  const u32x2 f = rows4_tr(scr, LDD, 0, 0);
-  wave_lds_fence();  // the next tile may reuse the scratch
-  return f;
+// Raw input row of 8 channels at token t: mixed_qkv inside the sequence, the conv
+// cache (oldest slot first) or zeros before it (deltanet.py:46).
+__device__ __forceinline__ u32x4 conv_input(const ChunkParams& p, int n, long long s0, long long t,
+                                            int ch0) {
+  if (t >= s0) return *(const u32x4*)((const bf16_t*)p.mixed_qkv + t * p.conv_dim + ch0);
+  u32x4 w{0u, 0u, 0u, 0u};
+  const int K = p.conv_k;
+  const int slot = (K - 1) - (int)(s0 - t);
+  if (p.conv_state_in && slot >= 0) {
+    const unsigned short* cs =
+        (const unsigned short*)p.conv_state_in + ((size_t)n * p.conv_dim + ch0) * (K - 1) + slot;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = (unsigned)cs[(2 * e) * (K - 1)] | ((unsigned)cs[(2 * e + 1) * (K - 1)] << 16);
+  }
+  return w;
 }
 
-__device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
-  *(u32x2*)(rec + off + lane_id() * 8) = f;
+// Causal depthwise conv + SiLU (deltanet.py:35-50, 243) of one 8-channel group over
+// chunk rows r0 .. r0+ROWS-1, streaming down the rows with the last three inputs
+// kept in registers.  conv_load issues every input row once (rows r0-3 ..
+// r0+ROWS-1); conv_compute consumes them.  Inputs, weights, the conv sum and the
+// SiLU output are rounded to bf16 like the reference's bf16 ops (the sum
+// accumulates in fp32); rows at or past nvalid give zeros.  emit(m, y) receives
+// row r0 + m.
+template <int ROWS>
+__device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long s0, long long t0,
+                                          int nvalid, int r0, int ch0, u32x4* raw) {
+#pragma unroll
+  for (int k = 0; k < ROWS + 3; ++k) {
+    int row = r0 - 3 + k;
+    row = row < nvalid ? row : nvalid - 1;  // padded rows: in bounds, zeroed below
+    raw[k] = conv_input(p, n, s0, t0 + row, ch0);
+  }
+}
+
+template <int ROWS, class Emit>
+__device__ __forceinline__ void conv_compute(const u32x4* raw, const float (*wt)[4], int nvalid,
+                                             int r0, Emit emit) {
+  float x3[8], x2[8], x1[8];  // inputs 3, 2 and 1 rows back
+  unpack8<false>(&raw[0], x3);
+  unpack8<false>(&raw[1], x2);
+  unpack8<false>(&raw[2], x1);
+#pragma unroll
+  for (int m = 0; m < ROWS; ++m) {
+    float x0[8], y[8];
+    unpack8<false>(&raw[m + 3], x0);
+    const float keep = (float)(r0 + m < nvalid);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float acc = wt[e][0] * x0[e] + wt[e][1] * x1[e] + wt[e][2] * x2[e] + wt[e][3] * x3[e];
+      y[e] = round_bf(siluf_(round_bf(acc))) * keep;
+      x3[e] = x2[e];
+      x2[e] = x1[e];
+      x1[e] = x0[e];
+    }
+    emit(m, y);
+  }
+}
+
+// conv_load then conv_compute, with the window and weights local to the call
+template <int ROWS, class Emit>
+__device__ __forceinline__ void conv_rows(const ChunkParams& p, int n, long long s0, long long t0,
+                                          int nvalid, int r0, int ch0, Emit emit) {
+  u32x4 raw[ROWS + 3];
+  float wt[8][4];
+  load_conv_w(p, ch0, wt);
+  conv_load<ROWS>(p, n, s0, t0, nvalid, r0, ch0, raw);
+  conv_compute<ROWS>(raw, wt, nvalid, r0, emit);
+}
+
+// L2 norm of a row spread over W lanes (8 values each), in fp32 like the
+// reference's norm at input precision; the bf16 pack that follows rounds it.
+template <int W>
+__device__ __forceinline__ void l2norm8(float* x) {
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = group_sum_dpp<W>(ss);
+  const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] *= inv;
+}
+
+// One (chunk, key head) task: chunk ci of sequence n (tokens [t0, t0 + nvalid)).
+struct PrepTask {
+  int ci, hk, n, nvalid;
+  long long s0, t0;
+};
+
+// Task index -> task.  Tasks are key-head major (task = hk * n_ci + ci), so the
+// consecutive tasks a workgroup walks share the key head and its conv weights.
+__device__ __forceinline__ PrepTask prep_task(const ChunkParams& p, int task, int n_ci) {
+  PrepTask t;
+  t.hk = task / n_ci;
+  t.ci = task % n_ci;
+  int c;
+  if (p.chunk_off) {
+    int lo = 0, hi = p.N;  // chunk_off[lo] <= ci < chunk_off[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.chunk_off[mid] <= t.ci) lo = mid;
+      else hi = mid;
+    }
+    t.n = lo;
+    c = t.ci - p.chunk_off[lo];
+  } else {
+    t.n = t.ci / p.nch;
+    c = t.ci % p.nch;
+  }
+  long long s1;
+  seq_range(p.cu_seqlens, t.n, p.T, t.s0, s1);
+  t.t0 = t.s0 + (long long)c * C;
+  t.nvalid = (int)((s1 - t.t0) < C ? (s1 - t.t0) : C);
+  return t;
+}
+
+constexpr int kGatePf = 4;  // value heads per key head whose gate inputs are prefetched
+
+// Core modes run persistent workgroups that prefetch their next task while
+// computing the current one.  The layer mode's conv window would need about 110
+// more registers across the compute phase, halving occupancy, so there each
+// workgroup runs a single task (the grid covers all tasks).
+template <int MODE>
+constexpr bool prep_persistent() { return MODE != MODE_LAYER; }
+
+// Per-thread register prefetch of one task's inputs: raw q/k rows (core modes)
+// and the gate inputs of the first kGatePf value heads (lane = token).
+template <int DK, int MODE>
+struct PrepPf {
+  static constexpr int NRAW = MODE == MODE_LAYER ? 1 : PrepCfg<DK, MODE>::NI_KQ * PrepCfg<DK, MODE>::RAWW;
+  u32x4 raw[NRAW];
+  float ga[kGatePf], gb[kGatePf];
+};
+
+template <int DK, int MODE>
+__device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTask& t,
+                                              PrepPf<DK, MODE>& pf) {
+  using Q_ = PrepCfg<DK, MODE>;
+  constexpr int SEGS = Q_::SEGS;
+  constexpr bool F32 = MODE == MODE_F32;
+  const int tid = threadIdx.x, l = tid & 63;
+  if constexpr (MODE == MODE_LAYER) {
+    // the conv input windows are loaded where they are consumed (holding them
+    // across the compute phase would halve the occupancy)
+  } else {
+#pragma unroll
+    for (int k = 0; k < Q_::NI_KQ; ++k) {
+      constexpr int PER = C * SEGS;
+      const int which = (k * NT) / PER;  // 0 = k, 1 = q (compile time)
+      const int rem = (k * NT) % PER + tid;
+      const int r = rem / SEGS, seg = rem % SEGS;
+      const long long tok = t.t0 + (r < t.nvalid ? r : t.nvalid - 1);  // padded rows: zeroed later
+      load_raw<F32>(which == 0 ? p.k : p.q,
+                    tok * (which == 0 ? p.k_ld : p.q_ld) + (long long)t.hk * DK + seg * 8,
+                    &pf.raw[k * Q_::RAWW]);
+    }
+  }
+  const int gqa = p.Hv / p.Hk;
+#pragma unroll
+  for (int gg = 0; gg < kGatePf; ++gg) {
+    pf.ga[gg] = 0.f;
+    pf.gb[gg] = 0.f;
+    if (gg < gqa && l < t.nvalid) {
+      const long long idx = (t.t0 + l) * p.Hv + t.hk * gqa + gg;
+      if constexpr (MODE == MODE_LAYER) {
+        pf.ga[gg] = bf2f(((const bf16_t*)p.a)[idx]);
+        pf.gb[gg] = bf2f(((const bf16_t*)p.b)[idx]);
+      } else {
+        pf.ga[gg] = p.g[idx];
+        pf.gb[gg] = p.beta[idx];
+      }
+    }
+  }
 }
 
 template <int DK, int MODE>
@@ -125,287 +260,319 @@ __global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
   constexpr bool IS = Q_::IS, F32 = MODE == MODE_F32;
   __shared__ __align__(16) bf16_t sK[Q_::NS * C * LDK];   // K rows [token][dk] (hi, lo)
   __shared__ __align__(16) bf16_t sQ[Q_::NS * C * LDK];   // Q rows
-  __shared__ __align__(16) bf16_t sLoT[2 * C * LDT];      // L^T off-diagonal blocks [m][i] (hi, lo)
+  __shared__ __align__(16) u32x2 sLf[10 * 2 * 64];        // L blocks as A fragments (hi, lo)
   __shared__ __align__(16) bf16_t sTdT[2 * C * LDD];      // diagonal inverses, transposed (hi, lo)
   __shared__ __align__(16) float sLd[C * LDD];            // diagonal blocks of L (wave w: rows 16w..)
   __shared__ __align__(16) float sGw[4 * 2 * C];          // per wave: G log2(e), beta
-  __shared__ __align__(16) bf16_t sX[4 * 16 * LDD];       // per wave: tile transposition
-  constexpr int K_LO = C * LDK, LO_LO = C * LDT, TD_LO = C * LDD;
+  __shared__ __align__(16) float sGin[kGatePf * 2 * C];   // the task's prefetched gate inputs
+  constexpr int K_LO = C * LDK, TD_LO = C * LDD;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hk = (int)(blockIdx.x % (unsigned)p.Hk);
-  const int ci = (int)(blockIdx.x / (unsigned)p.Hk);  // global chunk index
-  int n, c;
-  if (p.chunk_off) {
-    if (ci >= p.chunk_off[p.N]) return;  // past the last chunk (uniform)
-    int lo = 0, hi = p.N;                // chunk_off[lo] <= ci < chunk_off[hi]
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (p.chunk_off[mid] <= ci) lo = mid;
-      else hi = mid;
-    }
-    n = lo;
-    c = ci - p.chunk_off[n];
-  } else {
-    n = ci / p.nch;
-    c = ci % p.nch;
-  }
-  long long s0, s1;
-  seq_range(p.cu_seqlens, n, p.T, s0, s1);
-  const long long t0 = s0 + (long long)c * C;
-  const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
   const int gqa = p.Hv / p.Hk;
+  // tasks: (chunk, key head) pairs; workgroup b takes a contiguous block of them
+  const int n_ci = p.chunk_off ? p.chunk_off[p.N] : p.n_rec;
+  const int total = n_ci * p.Hk;
+  const int per = (total + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int first = (int)blockIdx.x * per;
+  const int last = first + per < total ? first + per : total;
 
-  // ---------------------------------------------------------------- q, k rows
-  // a thread's items keep one 8-channel segment of k and one of q
-  float wk[MODE == MODE_LAYER ? 8 : 1][4], wq[MODE == MODE_LAYER ? 8 : 1][4];
-  if constexpr (MODE == MODE_LAYER) {
-    const int seg = tid % SEGS;
-    load_conv_w(p, p.Hk * DK + hk * DK + seg * 8, wk);
-    load_conv_w(p, hk * DK + seg * 8, wq);
-  }
-#pragma unroll
-  for (int k = 0; k < Q_::NI_KQ; ++k) {
-    constexpr int PER = C * SEGS;
-    const int which = (k * NT) / PER;  // 0 = k, 1 = q (compile time)
-    const int rem = (k * NT) % PER + tid;
-    const int r = rem / SEGS, seg = rem % SEGS;
-    const long long tok = t0 + (r < nvalid ? r : nvalid - 1);  // padded rows: in bounds, zeroed
-    float x[8];
+  PrepPf<DK, MODE> pf;
+  if constexpr (prep_persistent<MODE>())
+    if (first < last) prep_prefetch<DK, MODE>(p, prep_task(p, first, n_ci), pf);
+
+  for (int task = first; task < (prep_persistent<MODE>() ? last : first + 1); ++task) {
+    if (!prep_persistent<MODE>() && task >= last) break;
+    const PrepTask tk = prep_task(p, task, n_ci);
+    if constexpr (!prep_persistent<MODE>()) prep_prefetch<DK, MODE>(p, tk, pf);
+    const int hk = tk.hk, ci = tk.ci, n = tk.n, nvalid = tk.nvalid;
+    const long long s0 = tk.s0, t0 = tk.t0;
+
+    // -------------------------------------------------------------- q, k, v rows
     if constexpr (MODE == MODE_LAYER) {
-      conv8(p, n, s0, tok, (which == 0 ? p.Hk * DK : 0) + hk * DK + seg * 8, which == 0 ? wk : wq, x);
-    } else {
-      u32x4 w[Q_::RAWW];
-      load_raw<F32>(which == 0 ? p.k : p.q, tok * (which == 0 ? p.k_ld : p.q_ld) + (long long)hk * DK + seg * 8, w);
-      unpack8<F32>(w, x);
-    }
-    const float keep = (float)(r < nvalid);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] *= keep;
-    if (p.qk_l2norm) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-      ss = group_sum_dpp<SEGS>(ss);
-      const float inv = rsqrtf(ss + 1e-6f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] *= inv;
-    }
-    // bf16 inputs: the normalised row is rounded to bf16 (the reference normalises
-    // in the input dtype); the pack below does the rounding
-    bf16_t* dst = (which == 0 ? sK : sQ) + r * LDK + seg * 8;
-    const u32x4 hw = pack8(x);
-    *(u32x4*)dst = hw;
-    if constexpr (IS) *(u32x4*)(dst + K_LO) = pack8_lo(x);
-    void* out = which == 0 ? p.kn : p.qn;
-    if (out && r < nvalid) {
-      const long long o = (t0 + r) * (long long)p.Hk * DK + (long long)hk * DK + seg * 8;
-      if constexpr (F32) {
-        float4* d4 = (float4*)((float*)out + o);
-        d4[0] = float4{x[0], x[1], x[2], x[3]};
-        d4[1] = float4{x[4], x[5], x[6], x[7]};
+      // wave 0: k, wave 1: q -- lane = 8-channel group g + SEGS * row part; each lane
+      // streams C / (64 / SEGS) rows, and the SEGS lanes of a row are adjacent, so
+      // the row's L2 norm is a DPP sum.  Waves 2-3: the v channels of the gqa value
+      // heads, 16 rows per item.
+      if (wave < 2) {
+        constexpr int RP = 64 / SEGS, ROWS = C / RP;
+        const int g = l % SEGS, r0 = (l / SEGS) * ROWS;
+        bf16_t* dst = (wave == 0 ? sK : sQ) + 8 * g;
+        bf16_t* gout = (bf16_t*)(wave == 0 ? p.kn : p.qn) + (long long)hk * DK + 8 * g;
+        conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (wave == 0 ? p.Hk * DK : 0) + hk * DK + 8 * g,
+                        [&](int m, float* y) {
+          l2norm8<SEGS>(y);
+          const u32x4 hw = pack8(y);
+          const int r = r0 + m;
+          *(u32x4*)(dst + r * LDK) = hw;
+          if (r < nvalid) *(u32x4*)(gout + (t0 + r) * (long long)p.Hk * DK) = hw;
+        });
       } else {
-        *(u32x4*)((bf16_t*)out + o) = hw;
-      }
-    }
-  }
-  if constexpr (MODE == MODE_LAYER) {
-    // v rows of the gqa value heads of this key head: conv + SiLU, bf16
-    const int VS = gqa * p.DV / 8;  // 8-channel segments
-    const int vch0 = 2 * p.Hk * DK + hk * gqa * p.DV;
-    for (int it = tid; it < nvalid * VS; it += NT) {
-      const int r = it / VS, sgi = it % VS;
-      float y[8], wv[8][4];
-      load_conv_w(p, vch0 + 8 * sgi, wv);
-      conv8(p, n, s0, t0 + r, vch0 + 8 * sgi, wv, y);
-      *(u32x4*)((bf16_t*)p.vc + (t0 + r) * (long long)p.Hv * p.DV + (long long)hk * gqa * p.DV +
-                8 * sgi) = pack8(y);
-    }
-  }
-  __syncthreads();
-
-  // ---------------------------------------------------------------- Gram tiles
-  f32x4 tacc[5];
-#pragma unroll
-  for (int ti = 0; ti < 5; ++ti) {
-    const int code = tile_code(wave + 4 * ti);
-    const bool qk = ti >= 3 || (ti == 2 && wave >= 2);
-    const int bi = (code >> 2) & 3, bj = code & 3;
-    tacc[ti] = zero4();
-#pragma unroll
-    for (int s = 0; s < DK / 32; ++s) {
-      u32x4 ah, al, bh, bl;
-      frag2<IS>(qk ? sQ : sK, K_LO, LDK, 16 * bi, 32 * s, ah, al);
-      frag2<IS>(sK, K_LO, LDK, 16 * bj, 32 * s, bh, bl);
-      tacc[ti] = mm<IS, IS>(tacc[ti], ah, al, bh, bl);
-    }
-  }
-
-  float* gw = sGw + wave * 2 * C;  // this wave's G log2(e) [0, C) and beta [C, 2C)
-  bf16_t* scr = sX + wave * 16 * LDD;
-  const size_t rec_stride = (size_t)rec_bytes(MODE);
-
-  for (int gg = 0; gg < gqa; ++gg) {
-    const int h = hk * gqa + gg;
-    unsigned char* rec = p.rec + ((size_t)ci * p.Hv + h) * rec_stride;
-
-    // gates of value head h, one token per lane; every wave scans its own copy
-    {
-      float g = 0.f, bt = 0.f;
-      if (l < nvalid) {
-        const long long idx = (t0 + l) * p.Hv + h;
-        if constexpr (MODE == MODE_LAYER) {
-          // deltanet.py:248-250: beta in bf16, g in fp32
-          g = -expf(p.A_log[h]) * softplusf_(bf2f(((const bf16_t*)p.a)[idx]) + p.dt_bias[h]);
-          bt = round_bf(sigmoidf_(bf2f(((const bf16_t*)p.b)[idx])));
-        } else {
-          g = p.g[idx];
-          bt = p.beta[idx];
+        const int VG = gqa * p.DV / 8;  // 8-channel groups of v
+        const int vch0 = 2 * p.Hk * DK + hk * gqa * p.DV;
+        bf16_t* vout = (bf16_t*)p.vc + (long long)hk * gqa * p.DV;
+        for (int it = tid - 128; it < VG * 4; it += 128) {
+          const int g = it % VG, r0 = (it / VG) * 16;
+          if (r0 >= nvalid) continue;
+          auto emit = [&](int m, float* y) {
+            const int r = r0 + m;
+            if (r < nvalid) *(u32x4*)(vout + (t0 + r) * (long long)p.Hv * p.DV + 8 * g) = pack8(y);
+          };
+          conv_rows<16>(p, n, s0, t0, nvalid, r0, vch0 + 8 * g, emit);
         }
       }
-      float G = g;
+    } else {
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float y = __shfl_up(G, o, 64);
-        if (l >= o) G += y;
+      for (int k = 0; k < Q_::NI_KQ; ++k) {
+        constexpr int PER = C * SEGS;
+        const int which = (k * NT) / PER;  // 0 = k, 1 = q (compile time)
+        const int rem = (k * NT) % PER + tid;
+        const int r = rem / SEGS, seg = rem % SEGS;
+        float x[8];
+        unpack8<F32>(&pf.raw[k * Q_::RAWW], x);
+        const float keep = (float)(r < nvalid);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= keep;
+        if (p.qk_l2norm) l2norm8<SEGS>(x);
+        // bf16 inputs: the normalised row is rounded to bf16 (the reference
+        // normalises in the input dtype); the pack below does the rounding
+        bf16_t* dst = (which == 0 ? sK : sQ) + r * LDK + seg * 8;
+        const u32x4 hw = pack8(x);
+        *(u32x4*)dst = hw;
+        if constexpr (IS) *(u32x4*)(dst + K_LO) = pack8_lo(x);
+        void* out = which == 0 ? p.kn : p.qn;
+        if (out && r < nvalid) {
+          const long long o = (t0 + r) * (long long)p.Hk * DK + (long long)hk * DK + seg * 8;
+          if constexpr (F32) {
+            float4* d4 = (float4*)((float*)out + o);
+            d4[0] = float4{x[0], x[1], x[2], x[3]};
+            d4[1] = float4{x[4], x[5], x[6], x[7]};
+          } else {
+            *(u32x4*)((bf16_t*)out + o) = hw;
+          }
+        }
       }
-      const float Gl = __shfl(G, 63, 64);
-      const float eg = __expf(G);
-      gw[l] = G * 1.4426950408889634f;
-      gw[C + l] = bt;
-      if (wave == 0) {
-        float* rg = (float*)(rec + kRecG);
-        rg[kGateBeta * C + l] = bt;
-        rg[kGateBE * C + l] = bt * eg;
-        rg[kGateEG * C + l] = eg;
-        rg[kGateEL * C + l] = __expf(Gl - G);
-      }
-      wave_lds_fence();
     }
+    if (wave == 0) {
+#pragma unroll
+      for (int gg = 0; gg < kGatePf; ++gg) {
+        sGin[gg * 2 * C + l] = pf.ga[gg];
+        sGin[gg * 2 * C + C + l] = pf.gb[gg];
+      }
+    }
+    // the next task's loads land while this one computes
+    if constexpr (prep_persistent<MODE>())
+      if (task + 1 < last) prep_prefetch<DK, MODE>(p, prep_task(p, task + 1, n_ci), pf);
+    __syncthreads();
 
-    // gate the wave's Gram tiles: L (strictly lower) and P (lower) blocks
-    f32x4 Tw = zero4();  // this wave's diagonal inverse T_ww, C layout
+    // -------------------------------------------------------------- Gram tiles
+    // Tile (bi, bj) is computed as (rows of block bj) x (rows of block bi)^T, so lane
+    // (q, r) holds entry [16 bi + r][16 bj + 4q + v]: the A fragment of the tile.
+    f32x4 tacc[5];
 #pragma unroll
     for (int ti = 0; ti < 5; ++ti) {
-      const f32x4 acc = tacc[ti];
       const int code = tile_code(wave + 4 * ti);
       const bool qk = ti >= 3 || (ti == 2 && wave >= 2);
       const int bi = (code >> 2) & 3, bj = code & 3;
-      const int m = 16 * bj + lr;
-      const float Gm = gw[m];
-      const float4 Gi = *(const float4*)(gw + 16 * bi + 4 * lq);
-      const float gi[4] = {Gi.x, Gi.y, Gi.z, Gi.w};
-      f32x4 val;
-      if (!qk) {
-        const float4 Bi = *(const float4*)(gw + C + 16 * bi + 4 * lq);
-        const float bt[4] = {Bi.x, Bi.y, Bi.z, Bi.w};
-        // branch-free: the exponent is clamped to <= 0 (masked entries would
-        // overflow) and the strictly-lower mask multiplies the result
+      tacc[ti] = zero4();
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = 16 * bi + 4 * lq + v;
-          const float dec = __builtin_amdgcn_exp2f(fminf(gi[v] - Gm, 0.f));
-          val[v] = bt[v] * acc[v] * dec * (float)(i > m);
-        }
-        if (ti == 0) {
-          // the diagonal block: T_ww = (I + L_ww)^-1 by forward substitution, one
-          // column per lane (lanes 16..63 repeat the columns of lanes 0..15)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) sLd[(16 * bi + 4 * lq + v) * LDD + lr] = val[v];
-          wave_lds_fence();
-          const int cc = l & 15;
-          float x[16];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const float* row = sLd + (16 * bi + i) * LDD;
-            float a0 = (i == cc) ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-            for (int mm2 = 0; mm2 < i; mm2 += 4) {
-              const float4 r4 = *(const float4*)(row + mm2);
-              a0 -= r4.x * x[mm2];
-              if (mm2 + 1 < i) a1 -= r4.y * x[mm2 + 1];
-              if (mm2 + 2 < i) a0 -= r4.z * x[mm2 + 2];
-              if (mm2 + 3 < i) a1 -= r4.w * x[mm2 + 3];
-            }
-            x[i] = a0 + a1;
-          }
-          // C layout: lane (q, r) holds rows 4q..4q+3 of column r = its own column
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            Tw[v] = lq == 0 ? x[v] : (lq == 1 ? x[4 + v] : (lq == 2 ? x[8 + v] : x[12 + v]));
-          if (l < 16) {
-            // T_ww^T row cc = column cc of T_ww, hi and lo, for the other waves
-            bf16_t* dh = sTdT + (16 * bi + cc) * LDD;
-            bf16_t* dl = dh + TD_LO;
-#pragma unroll
-            for (int h8 = 0; h8 < 2; ++h8) {
-              float hv[8];
-#pragma unroll
-              for (int e = 0; e < 8; ++e) hv[e] = x[8 * h8 + e];
-              *(u32x4*)(dh + 8 * h8) = pack8(hv);
-              *(u32x4*)(dl + 8 * h8) = pack8_lo(hv);
-            }
-          }
-          const int tw = kRecT + 2 * tile_index(bi, bi) * kTileBytes;
-          put_tile(rec, tw, to_afrag(scr, Tw, false));
-          put_tile(rec, tw + kTileBytes, to_afrag(scr, Tw, true));
-        } else {
-          store_ct_split(sLoT, sLoT + LO_LO, LDT, 16 * bi, 16 * bj, val);
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int i = 16 * bi + 4 * lq + v;
-          const float dec = __builtin_amdgcn_exp2f(fminf(gi[v] - Gm, 0.f));
-          val[v] = p.scale * acc[v] * dec * (float)(i >= m);
-        }
-        const int tix = tile_index(bi, bj);
-        put_tile(rec, kRecP + tix * kTileBytes, to_afrag(scr, val, false));
-        if constexpr (IS) put_tile(rec, kRecPL + tix * kTileBytes, to_afrag(scr, val, true));
+      for (int s = 0; s < DK / 32; ++s) {
+        u32x4 ah, al, bh, bl;
+        frag2<IS>(sK, K_LO, LDK, 16 * bj, 32 * s, ah, al);
+        frag2<IS>(qk ? sQ : sK, K_LO, LDK, 16 * bi, 32 * s, bh, bl);
+        tacc[ti] = mm<IS, IS>(tacc[ti], ah, al, bh, bl);
       }
     }
-    __syncthreads();  // L^T blocks and the diagonal inverses of all waves are in LDS
 
-    // block column j = wave: T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj, i = j+1..3
-    {
-      const int j = wave;
-      u32x2 Th[4], Tl[4];  // B operands of the column's finished blocks T_kj
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        Th[k] = pack_hi4(Tw);
-        Tl[k] = pack_lo4(Tw);
-      }
-#pragma unroll
-      for (int i = 1; i < 4; ++i) {
-        if (i <= j) continue;  // uniform
-        f32x4 X = zero4();
-#pragma unroll
-        for (int k = 0; k < i; ++k) {
-          if (k < j) continue;
-          const u32x2 ah = rows4_tr(sLoT, LDT, 16 * k, 16 * i);
-          const u32x2 al = rows4_tr(sLoT + LO_LO, LDT, 16 * k, 16 * i);
-          X = mm3k16(X, ah, al, Th[k], Tl[k]);
+    float* gw = sGw + wave * 2 * C;  // this wave's G log2(e) [0, C) and beta [C, 2C)
+    const size_t rec_stride = (size_t)rec_bytes(MODE);
+
+    for (int gg = 0; gg < gqa; ++gg) {
+      const int h = hk * gqa + gg;
+      unsigned char* rec = p.rec + ((size_t)ci * p.Hv + h) * rec_stride;
+
+      // gates of value head h, one token per lane; every wave scans its own copy
+      {
+        float g = 0.f, bt = 0.f;
+        if (gg < kGatePf) {
+          g = sGin[gg * 2 * C + l];
+          bt = sGin[gg * 2 * C + C + l];
+        } else if (l < nvalid) {
+          const long long idx = (t0 + l) * p.Hv + h;
+          if constexpr (MODE == MODE_LAYER) {
+            g = bf2f(((const bf16_t*)p.a)[idx]);
+            bt = bf2f(((const bf16_t*)p.b)[idx]);
+          } else {
+            g = p.g[idx];
+            bt = p.beta[idx];
+          }
         }
-        // the A operand T_ii is negated (a sign flip is exact in bf16)
-        const u32x2 th = rows4_tr(sTdT, LDD, 16 * i, 0) ^ 0x80008000u;
-        const u32x2 tl = rows4_tr(sTdT + TD_LO, LDD, 16 * i, 0) ^ 0x80008000u;
-        const f32x4 Tij = mm3k16(zero4(), th, tl, pack_hi4(X), pack_lo4(X));
-        Th[i] = pack_hi4(Tij);
-        Tl[i] = pack_lo4(Tij);
-        const int off = kRecT + 2 * tile_index(i, j) * kTileBytes;
-        put_tile(rec, off, to_afrag(scr, Tij, false));
-        put_tile(rec, off + kTileBytes, to_afrag(scr, Tij, true));
+        if constexpr (MODE == MODE_LAYER) {
+          // deltanet.py:248-250: beta in bf16, g in fp32 (padded tokens: both 0)
+          const float keep = (float)(l < nvalid);
+          g = -expf(p.A_log[h]) * softplusf_(g + p.dt_bias[h]) * keep;
+          bt = round_bf(sigmoidf_(bt)) * keep;
+        }
+        const float G = wave_scan_dpp(g);
+        const float Gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 63));
+        const float eg = __expf(G);
+        gw[l] = G * 1.4426950408889634f;
+        gw[C + l] = bt;
+        if (wave == 0) {
+          float* rg = (float*)(rec + kRecG);
+          rg[kGateBeta * C + l] = bt;
+          rg[kGateBE * C + l] = bt * eg;
+          rg[kGateEG * C + l] = eg;
+          rg[kGateEL * C + l] = __expf(Gl - G);
+        }
+        wave_lds_fence();
       }
+      // gate the wave's Gram tiles into L (strictly lower) and P (lower) blocks; lane
+      // (q, r) holds row i = 16 bi + r, columns m = 16 bj + 4q + v
+      f32x4 Tw = zero4();  // this wave's diagonal inverse T_ww, C layout
+  #pragma unroll
+      for (int ti = 0; ti < 5; ++ti) {
+        const f32x4 acc = tacc[ti];
+        const int code = tile_code(wave + 4 * ti);
+        const bool qk = ti >= 3 || (ti == 2 && wave >= 2);
+        const int bi = (code >> 2) & 3, bj = code & 3;
+        const int i = 16 * bi + lr;
+        const float Gi = gw[i];
+        const float4 Gm4 = *(const float4*)(gw + 16 * bj + 4 * lq);
+        const float Gm[4] = {Gm4.x, Gm4.y, Gm4.z, Gm4.w};
+        f32x4 val;
+        if (!qk) {
+          const float bt = gw[C + i];
+          // branch-free: the exponent is clamped to <= 0 (masked entries would
+          // overflow) and the strictly-lower mask multiplies the result
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int m = 16 * bj + 4 * lq + v;
+            val[v] = bt * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i > m);
+          }
+          if (ti == 0) {
+            // the diagonal block: T_ww = (I + L_ww)^-1 by forward substitution, one
+            // column per lane (lanes 16..63 repeat the columns of lanes 0..15)
+            *(float4*)(sLd + i * LDD + 4 * lq) = float4{val[0], val[1], val[2], val[3]};
+            wave_lds_fence();
+            const int cc = l & 15;
+            float x[16];
+  #pragma unroll
+            for (int ii = 0; ii < 16; ++ii) {
+              const float* row = sLd + (16 * bi + ii) * LDD;
+              float a0 = (ii == cc) ? 1.f : 0.f, a1 = 0.f;
+  #pragma unroll
+              for (int mm2 = 0; mm2 < ii; mm2 += 4) {
+                const float4 r4 = *(const float4*)(row + mm2);
+                a0 -= r4.x * x[mm2];
+                if (mm2 + 1 < ii) a1 -= r4.y * x[mm2 + 1];
+                if (mm2 + 2 < ii) a0 -= r4.z * x[mm2 + 2];
+                if (mm2 + 3 < ii) a1 -= r4.w * x[mm2 + 3];
+              }
+              x[ii] = a0 + a1;
+            }
+            // C layout: lane (q, r) holds rows 4q..4q+3 of column r = its own column
+  #pragma unroll
+            for (int v = 0; v < 4; ++v)
+              Tw[v] = lq == 0 ? x[v] : (lq == 1 ? x[4 + v] : (lq == 2 ? x[8 + v] : x[12 + v]));
+            if (l < 16) {
+              // T_ww^T row cc = column cc of T_ww, hi and lo, for the other waves
+              bf16_t* dh = sTdT + (16 * bi + cc) * LDD;
+              bf16_t* dl = dh + TD_LO;
+  #pragma unroll
+              for (int h8 = 0; h8 < 2; ++h8) {
+                float hv[8];
+  #pragma unroll
+                for (int e = 0; e < 8; ++e) hv[e] = x[8 * h8 + e];
+                *(u32x4*)(dh + 8 * h8) = pack8(hv);
+                *(u32x4*)(dl + 8 * h8) = pack8_lo(hv);
+              }
+            }
+            wave_lds_fence();
+            const int tw = kRecT + 2 * tile_index(bi, bi) * kTileBytes;
+            put_tile(rec, tw, rows4_tr(sTdT, LDD, 16 * bi, 0));
+            put_tile(rec, tw + kTileBytes, rows4_tr(sTdT + TD_LO, LDD, 16 * bi, 0));
+          } else {
+            u32x2* d = sLf + 2 * 64 * tile_index(bi, bj) + l;
+            d[0] = pack_hi4(val);
+            d[64] = pack_lo4(val);
+          }
+        } else {
+          const float sc = p.scale;
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int m = 16 * bj + 4 * lq + v;
+            val[v] = sc * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i >= m);
+          }
+          const int tix = tile_index(bi, bj);
+          put_tile(rec, kRecP + tix * kTileBytes, pack_hi4(val));
+          if constexpr (IS) put_tile(rec, kRecPL + tix * kTileBytes, pack_lo4(val));
+        }
+      }
+      __syncthreads();  // L blocks and the diagonal inverses of all waves are in LDS
+
+      // block column j = wave: T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj, i = j+1..3.
+      // X is an MFMA result in C layout: the B operand here, and read the other way the
+      // A operand of X^T, so T_ij^T = -X^T T_ii^T (the record's A fragment of T_ij)
+      // comes from the same operands with the roles swapped.
+      {
+        const int j = wave;
+        u32x2 Th[4], Tl[4];  // B operands (C layout) of the column's finished blocks T_kj
+  #pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          Th[k] = pack_hi4(Tw);
+          Tl[k] = pack_lo4(Tw);
+        }
+  #pragma unroll
+        for (int i = 1; i < 4; ++i) {
+          if (i <= j) continue;  // uniform
+          f32x4 X = zero4();
+  #pragma unroll
+          for (int k = 0; k < i; ++k) {
+            if (k < j) continue;
+            const u32x2* f = sLf + 2 * 64 * tile_index(i, k) + l;
+            X = mm3k16(X, f[0], f[64], Th[k], Tl[k]);
+          }
+          // the T_ii fragment is negated (a sign flip is exact in bf16)
+          const u32x2 th = rows4_tr(sTdT, LDD, 16 * i, 0) ^ 0x80008000u;
+          const u32x2 tl = rows4_tr(sTdT + TD_LO, LDD, 16 * i, 0) ^ 0x80008000u;
+          const u32x2 xh = pack_hi4(X), xl = pack_lo4(X);
+          const f32x4 Tij = mm3k16(zero4(), th, tl, xh, xl);
+          const f32x4 TijT = mm3k16(zero4(), xh, xl, th, tl);
+          Th[i] = pack_hi4(Tij);
+          Tl[i] = pack_lo4(Tij);
+          const int off = kRecT + 2 * tile_index(i, j) * kTileBytes;
+          put_tile(rec, off, pack_hi4(TijT));
+          put_tile(rec, off + kTileBytes, pack_lo4(TijT));
+        }
+      }
+      __syncthreads();  // sLf / sTdT are rewritten for the next value head
     }
-    __syncthreads();  // sLoT / sTdT are rewritten for the next value head
   }
+}
+
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
 }
 
 template <int DK, int MODE>
 hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
-  const unsigned grid = (unsigned)p.n_rec * (unsigned)p.Hk;
-  if (grid == 0) return hipSuccess;
+  // persistent (core modes): two workgroups per compute unit walk the tasks, each
+  // prefetching its next task while it computes the current one
+  const long long tasks = (long long)p.n_rec * p.Hk;
+  if (tasks == 0) return hipSuccess;
+  const long long cap = prep_persistent<MODE>() ? 2LL * device_cus() : tasks;
+  const unsigned grid = (unsigned)(tasks < cap ? tasks : cap);
   hipLaunchKernelGGL((prep_kernel<DK, MODE>), dim3(grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
 }
