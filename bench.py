@@ -9,8 +9,9 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
            A "step" is one omx_gdn_prefill call over the whole batch.
   decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
-kernel, timed at the core-function boundary (chunk_gated_delta_rule on the same
-shapes), and carries the decode step's HBM roofline as "decode".  Only one GPU is
+rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
+shapes: the chunk-parallel preparation kernel and the state scan), and carries the
+decode step's HBM roofline as "decode".  Only one GPU is
 used: --gpus above 1 exits with a message.
 
 Kernel durations come from HIP events recorded on the stream the kernels run on
@@ -167,7 +168,8 @@ def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
         "step_event_ms": ms_step, "core_kernel_ms": ms_core,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
-                     "algorithmic_flops": flops},
+                     "algorithmic_flops": flops,
+                     "kernels": "prep_kernel + scan_kernel (the two launches of one call)"},
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_prefill_baseline()

@@ -77,7 +77,7 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
  * (N = number of sequences).  It holds the per-(chunk, value head) records of the
  * chunk-parallel preparation (the inverse T = (I + L)^-1 and P of each chunk,
  * deltanet.py:100-113, 130-131, and the chunk's gate vectors), the normalised
- * q and k, and the chunk offsets of packed sequences.  Pass it 256-byte aligned.
+ * q and k, and the chunk offsets of packed sequences.  Pass it 16-byte aligned.
  */
 size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
                                         int64_t dk, int64_t dv, int64_t N, int in_dtype);
@@ -112,7 +112,7 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Bytes of device workspace omx_gdn_prefill needs (256-byte aligned): the chunk
+ * Bytes of device workspace omx_gdn_prefill needs (16-byte aligned): the chunk
  * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v, and
  * the unnormalised bf16 o with partial sums of o^2 that the gated-norm epilogue
  * combines.

@@ -36,9 +36,16 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libomx_gdn.so)")
 
 
+# MFMA-heavy sources: keep MFMA accumulators in VGPRs, so the VALU work on them
+# (scaling, packing to bf16) needs no AGPR<->VGPR copies
+MFMA_VGPR_SOURCES = {"gdn_chunk.hip", "gdn_prep.hip"}
+MFMA_VGPR_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *COMMON, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    extra = MFMA_VGPR_FLAGS if os.path.basename(src) in MFMA_VGPR_SOURCES else []
+    cmd = [hipcc(), *COMMON, *DEVICE_FLAGS, *extra, "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [hipcc(), *COMMON, "-x", "hip", *DEVICE_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -242,7 +242,7 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   REQUIRE(workspace_bytes >= ws.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
           fn, workspace_bytes, ws.total);
   if (N == 0 || (B * T == 0 && !final_state)) return ok();
-  REQUIRE(workspace && aligned(workspace, 256), "%s: workspace must be non-NULL and 256-byte aligned",
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
           fn);
   REQUIRE(o || B * T == 0, "%s: o is NULL", fn);
   if (B * T > 0) REQUIRE(q && k && v && g && beta, "%s: a required pointer is NULL", fn);
@@ -301,7 +301,7 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   if (tokens > 0)
     REQUIRE(mixed_qkv && z && a && b && out, "%s: an activation pointer is NULL", fn);
   REQUIRE(conv_w && A_log && dt_bias && norm_w, "%s: a parameter pointer is NULL", fn);
-  REQUIRE(workspace && aligned(workspace, 256), "%s: workspace must be non-NULL and 256-byte aligned",
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
           fn);
   REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 16) && aligned(out, 16)),
           "%s: mixed_qkv, z and out must be 16-byte aligned", fn);

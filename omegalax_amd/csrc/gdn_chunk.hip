@@ -79,17 +79,38 @@ struct Prefetch {
   u32x4 rec[Q_::NI_R];
 };
 
-template <int DK, int MODE>
+// Loads of one chunk, in four parts (PART = 0..3, or -1 for all) so that a chunk's
+// prefetch can be spread over the previous chunk's compute phases: the four
+// wavefronts of a CU issuing all their loads at once would queue them behind
+// each other in the CU's memory pipeline.  Parts: record, v rows, k rows, q rows.
+template <int DK, int MODE, int PART = -1>
 __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE>& pf,
                                          long long t0, int nvalid, const unsigned char* rec,
                                          int hk, int h, int col0) {
   using Q_ = Cfg<DK, MODE>;
   constexpr bool F32 = MODE == MODE_F32;
   const int tid = threadIdx.x;
+  if constexpr (PART == -1 || PART == 0) {
+#pragma unroll
+    for (int k = 0; k < Q_::NI_R; ++k) {
+      const int it = tid + k * NT;
+      if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) pf.rec[k] = ((const u32x4*)rec)[it];
+    }
+  }
+  if constexpr (PART == -1 || PART == 1) {
+#pragma unroll
+    for (int k = 0; k < Q_::NI_V; ++k) {
+      const int it = tid + k * NT;
+      const int r = it / (BV / 8), seg = it % (BV / 8);
+      const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
+      load_raw<F32>(p.vs, tok * p.vs_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < Q_::NI_KQ; ++k) {
     constexpr int PER = C * Q_::SEGS;
-    const int which = (k * NT) / PER;  // 0 = k, 1 = q
+    const int which = (k * NT) / PER;  // 0 = k (part 2), 1 = q (part 3); folded when unrolled
+    if (PART != -1 && PART != 2 + which) continue;
     const int rem = (k * NT) % PER + tid;
     const int r = rem / Q_::SEGS, seg = rem % Q_::SEGS;
     // rows past the sequence end load the last valid row (in bounds); staging zeroes
@@ -97,18 +118,6 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
     const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
     load_raw<F32>(which == 0 ? p.ks : p.qs,
                   tok * (which == 0 ? p.ks_ld : p.qs_ld) + (long long)hk * DK + seg * 8, pf.kq[k]);
-  }
-#pragma unroll
-  for (int k = 0; k < Q_::NI_V; ++k) {
-    const int it = tid + k * NT;
-    const int r = it / (BV / 8), seg = it % (BV / 8);
-    const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
-    load_raw<F32>(p.vs, tok * p.vs_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
-  }
-#pragma unroll
-  for (int k = 0; k < Q_::NI_R; ++k) {
-    const int it = tid + k * NT;
-    if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) pf.rec[k] = ((const u32x4*)rec)[it];
   }
 }
 
@@ -190,6 +199,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
     // ------------------------------------------------------------ stage the chunk
+    const bool full = nvalid == C;  // uniform: only a sequence's last chunk has padded rows
 #pragma unroll
     for (int k = 0; k < Q_::NI_KQ; ++k) {
       constexpr int PER = C * SEGS;
@@ -205,6 +215,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         for (int e = 0; e < 8; ++e) x[e] *= keep;
         *(u32x4*)dst = pack8(x);
         *(u32x4*)(dst + K_LO) = pack8_lo(x);
+      } else if (full) {
+        *(u32x4*)dst = pf.kq[k][0];
       } else {
         const unsigned keep = r < nvalid ? 0xffffffffu : 0u;  // padded rows are zero
         *(u32x4*)dst = pf.kq[k][0] & keep;
@@ -223,6 +235,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         for (int e = 0; e < 8; ++e) x[e] *= keep;
         *(u32x4*)dst = pack8(x);
         *(u32x4*)(dst + V_LO) = pack8_lo(x);
+      } else if (full) {
+        *(u32x4*)dst = pf.v[k][0];
       } else {
         const unsigned keep = r < nvalid ? 0xffffffffu : 0u;
         *(u32x4*)dst = pf.v[k][0] & keep;
@@ -243,51 +257,82 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
 
     // ------------------------------------------------------------ K S, Q S, right-hand side
+    // S^T goes to the wave's scratch as the B operand of K S and Q S.  Every operand
+    // that does not depend on S is read from LDS in one batch while it lands, so
+    // the products below run back to back on registers.
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {
       if constexpr (IS) store_ct_split(wS, wS + WS_LO, LDK, 16 * t, 0, S[t]);
       else store_ct_bf16(wS, LDK, 16 * t, 0, S[t]);
     }
-    wave_lds_fence();
-    f32x4 R[4], QS[4];
+    constexpr int NSK = DK / 32;
+    u32x4 kh[4][NSK], kl[4][NSK], qh[4][NSK], ql[4][NSK];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int s2 = 0; s2 < NSK; ++s2) {
+        frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s2, kh[i][s2], kl[i][s2]);
+        frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s2, qh[i][s2], ql[i][s2]);
+      }
+    float vv[4][4];  // V at rows 16i + 4lq + v, column 16w + lr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 ks = zero4();
-      QS[i] = zero4();
-#pragma unroll
-      for (int s = 0; s < DK / 32; ++s) {
-        u32x4 bh, bl, ah, al;
-        frag2<IS>(wS, WS_LO, LDK, 0, 32 * s, bh, bl);
-        frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s, ah, al);
-        ks = mm<IS, IS>(ks, ah, al, bh, bl);
-        frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s, ah, al);
-        QS[i] = mm<IS, IS>(QS[i], ah, al, bh, bl);
-      }
-      // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
-      const int r0 = 16 * i + 4 * lq;
       const u32x2 vw = rows4_tr(sV, LDT, 16 * i, 16 * wave);
-      float vv[4] = {__uint_as_float(vw[0] << 16), __uint_as_float(vw[0] & 0xffff0000u),
-                     __uint_as_float(vw[1] << 16), __uint_as_float(vw[1] & 0xffff0000u)};
+      vv[i][0] = __uint_as_float(vw[0] << 16);
+      vv[i][1] = __uint_as_float(vw[0] & 0xffff0000u);
+      vv[i][2] = __uint_as_float(vw[1] << 16);
+      vv[i][3] = __uint_as_float(vw[1] & 0xffff0000u);
       if constexpr (IS) {
         const u32x2 vl = rows4_tr(sV + V_LO, LDT, 16 * i, 16 * wave);
-        vv[0] += __uint_as_float(vl[0] << 16);
-        vv[1] += __uint_as_float(vl[0] & 0xffff0000u);
-        vv[2] += __uint_as_float(vl[1] << 16);
-        vv[3] += __uint_as_float(vl[1] & 0xffff0000u);
+        vv[i][0] += __uint_as_float(vl[0] << 16);
+        vv[i][1] += __uint_as_float(vl[0] & 0xffff0000u);
+        vv[i][2] += __uint_as_float(vl[1] << 16);
+        vv[i][3] += __uint_as_float(vl[1] & 0xffff0000u);
       }
+    }
+    wave_lds_fence();
+    u32x4 sh[NSK], sl[NSK];
+#pragma unroll
+    for (int s2 = 0; s2 < NSK; ++s2) frag2<IS>(wS, WS_LO, LDK, 0, 32 * s2, sh[s2], sl[s2]);
+    f32x4 KS[4], QS[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      KS[i] = zero4();
+      QS[i] = zero4();
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < NSK; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {  // eight independent accumulation chains
+        KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
+        QS[i] = mm<IS, IS>(QS[i], qh[i][s2], ql[i][s2], sh[s2], sl[s2]);
+      }
+    // T fragments for V_new = T R (read while the products run)
+    u32x2 th[10], tl[10];
+#pragma unroll
+    for (int x = 0; x < 10; ++x) {
+      const unsigned char* tp = sRec + kRecT + 2 * x * kTileBytes + 8 * l;
+      th[x] = *(const u32x2*)tp;
+      tl[x] = *(const u32x2*)(tp + kTileBytes);
+    }
+    // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
+    f32x4 R[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r0 = 16 * i + 4 * lq;
       const float4 bt = *(const float4*)(sBeta + r0);
       const float4 be = *(const float4*)(sBE + r0);
-      R[i][0] = bt.x * vv[0] - be.x * ks[0];
-      R[i][1] = bt.y * vv[1] - be.y * ks[1];
-      R[i][2] = bt.z * vv[2] - be.z * ks[2];
-      R[i][3] = bt.w * vv[3] - be.w * ks[3];
+      R[i][0] = bt.x * vv[i][0] - be.x * KS[i][0];
+      R[i][1] = bt.y * vv[i][1] - be.y * KS[i][1];
+      R[i][2] = bt.z * vv[i][2] - be.z * KS[i][2];
+      R[i][3] = bt.w * vv[i][3] - be.w * KS[i][3];
     }
 
     // ------------------------------------------------------------ V_new = T R
     // A C-layout tile (lane (q, r) holds rows 4q..4q+3 of column r) is exactly the
     // B operand layout of the 16x16x16 MFMA, so R feeds the products from
-    // registers; T comes as ready A-operand fragments.  The four row blocks are
-    // independent chains.
+    // registers; T comes as ready A-operand fragments.  The hi*hi, hi*lo and
+    // lo*hi parts accumulate separately: twelve independent chains.
     u32x2 Rh[4], Rl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -298,16 +343,34 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     u32x2 Uh[4], Ul[4];  // bf16 hi/lo of V_new blocks as B operands
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 acc = zero4();
+      f32x4 a0 = zero4(), a1 = zero4(), a2 = zero4();
 #pragma unroll
       for (int kb = 0; kb <= i; ++kb) {
-        const unsigned char* tp = sRec + kRecT + 2 * tile_index(i, kb) * kTileBytes + 8 * l;
-        acc = mm3k16(acc, *(const u32x2*)tp, *(const u32x2*)(tp + kTileBytes), Rh[kb], Rl[kb]);
+        const int x = tile_index(i, kb);
+        a0 = mma16k16(th[x], Rh[kb], a0);
+        a1 = mma16k16(th[x], Rl[kb], a1);
+        a2 = mma16k16(tl[x], Rh[kb], a2);
       }
-      U[i] = acc;
-      Uh[i] = pack_hi4(acc);
-      Ul[i] = pack_lo4(acc);
+      U[i] = a0 + a1 + a2;
+      Uh[i] = pack_hi4(U[i]);
+      Ul[i] = pack_lo4(U[i]);
     }
+    // P fragments and the K^T fragments of the state update (read while V_new forms)
+    u32x2 ph[10], pl[10];
+#pragma unroll
+    for (int x = 0; x < 10; ++x) {
+      ph[x] = *(const u32x2*)(sRec + kRecP + x * kTileBytes + 8 * l);
+      if constexpr (OS) pl[x] = *(const u32x2*)(sRec + kRecPL + x * kTileBytes + 8 * l);
+      else pl[x] = ph[x];
+    }
+    u32x4 kth[DK / 16][2], ktl[DK / 16][2];
+#pragma unroll
+    for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        kth[t][s2] = frag_tr(sK, LDK, 32 * s2, 16 * t);
+        ktl[t][s2] = IS ? frag_tr(sK + K_LO, LDK, 32 * s2, 16 * t) : kth[t][s2];
+      }
     // Vt = diag(e^{G_last - G}) V_new for the state update
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -318,22 +381,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
 
     // ------------------------------------------------------------ O = scale e^G (Q S) + P V_new
-    f32x4 OUT[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4& o = OUT[i];
+      f32x4 o;
       const float4 eg = *(const float4*)(sEG + 16 * i + 4 * lq);
       o[0] = p.scale * eg.x * QS[i][0]; o[1] = p.scale * eg.y * QS[i][1];
       o[2] = p.scale * eg.z * QS[i][2]; o[3] = p.scale * eg.w * QS[i][3];
 #pragma unroll
       for (int jb = 0; jb <= i; ++jb) {  // P is lower triangular
-        const int tix = tile_index(i, jb);
-        const u32x2 ah = *(const u32x2*)(sRec + kRecP + tix * kTileBytes + 8 * l);
-        o = mma16k16(ah, Uh[jb], o);
+        const int x = tile_index(i, jb);
+        o = mma16k16(ph[x], Uh[jb], o);
         if constexpr (OS) {
-          const u32x2 al = *(const u32x2*)(sRec + kRecPL + tix * kTileBytes + 8 * l);
-          o = mma16k16(ah, Ul[jb], o);
-          o = mma16k16(al, Uh[jb], o);
+          o = mma16k16(ph[x], Ul[jb], o);
+          o = mma16k16(pl[x], Uh[jb], o);
         }
       }
       if constexpr (MODE != MODE_LAYER) {
@@ -367,21 +427,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       }
     }
 
+
     // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
     wave_lds_fence();  // Vt^T stores above are visible to the wave's fragment loads
+    u32x4 vth[2], vtl[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) frag2<true>(wVt, W_LO, LDT, 0, 32 * s2, vth[s2], vtl[s2]);
     const float gl = sEG[C - 1];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) S[t][v] *= gl;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        u32x4 ah, al, bh, bl;
-        ah = frag_tr(sK, LDK, 32 * s, 16 * t);
-        al = IS ? frag_tr(sK + K_LO, LDK, 32 * s, 16 * t) : ah;
-        frag2<true>(wVt, W_LO, LDT, 0, 32 * s, bh, bl);
-        S[t] = mm<IS, true>(S[t], ah, al, bh, bl);
-      }
+      for (int s2 = 0; s2 < 2; ++s2) S[t] = mm<IS, true>(S[t], kth[t][s2], ktl[t][s2], vth[s2], vtl[s2]);
     }
   }
 

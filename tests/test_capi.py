@@ -89,3 +89,53 @@ def test_python_api_rejects_cpu_tensors():
     with pytest.raises(ValueError, match="GPU"):
         recurrent_gated_delta_rule_step(q, q, torch.zeros(1, 1, 16), torch.zeros(1, 1),
                                         torch.zeros(1, 1), torch.zeros(1, 1, 16, 16))
+
+
+def _ws_size(B=2, T=100, Hk=2, Hv=4, dk=128, dv=128, N=2, dt=_lib.BF16):
+    return _lib.lib().omx_gdn_chunk_fwd_workspace_size(B, T, Hk, Hv, dk, dv, N, dt)
+
+
+def test_chunk_workspace_size_covers_records_and_normalised_qk():
+    # records: (ceil(B*T/64) + N) slots x Hv x 16 KiB (bf16) or 21 KiB (fp32), plus q/k
+    bf, f32 = _ws_size(dt=_lib.BF16), _ws_size(dt=_lib.F32)
+    slots = (2 * 100 + 63) // 64 + 2
+    assert bf >= slots * 4 * 16384 + 2 * 200 * 2 * 128 * 2
+    assert f32 >= slots * 4 * 21504 + 2 * 200 * 2 * 128 * 4
+    assert f32 > bf
+    assert _ws_size(T=1000) > _ws_size(T=100)
+    prefill = _lib.lib().omx_gdn_prefill_workspace_size(2, 100, 2, 4, 128, 128, 2)
+    assert prefill > bf  # adds conv(v), bf16 o and the norm's partial sums
+
+
+def _chunk(ws, ws_bytes, **over):
+    a = dict(q=16, k=16, v=16, dt=_lib.BF16, g=16, beta=16, s0=None, cu=None, N=2, o=16, fs=None,
+             B=2, T=100, Hk=2, Hv=4, dk=128, dv=128, C=64, scale=0.088, norm=1, ws=ws,
+             ws_bytes=ws_bytes, stream=None)
+    a.update(over)
+    L = _lib.lib()
+    rc = L.omx_gdn_chunk_fwd(*a.values())
+    return rc, L.omx_gdn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(ws_bytes=1024), "workspace"),
+    (dict(ws=24), "aligned"),
+    (dict(ws=None), "workspace"),
+    (dict(C=32), "chunk_size"),
+    (dict(dt=5), "in_dtype"),
+    (dict(N=3), "N must equal B"),
+])
+def test_chunk_fwd_rejects_bad_arguments(over, msg):
+    args = dict(ws=256, ws_bytes=_ws_size())
+    args.update(over)
+    rc, err = _chunk(args.pop("ws"), args.pop("ws_bytes"), **args)
+    assert rc == _lib.EINVAL
+    assert msg in err
+
+
+def test_prefill_rejects_small_workspace():
+    L = _lib.lib()
+    need = L.omx_gdn_prefill_workspace_size(2, 100, 2, 4, 128, 128, 2)
+    rc = L.omx_gdn_prefill(16, 16, 16, 16, 16, 16, 16, 16, 1e-6, None, 2, None, None, None, None, 16,
+                           2, 100, 2, 4, 128, 128, 4, 64, 256, need - 1, None)
+    assert rc == _lib.EINVAL and "workspace" in L.omx_gdn_last_error().decode()
