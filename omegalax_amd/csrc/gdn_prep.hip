@@ -128,7 +128,7 @@ __device__ __forceinline__ void conv_compute(const u32x4* raw, const float (*wt)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float acc = wt[e][0] * x0[e] + wt[e][1] * x1[e] + wt[e][2] * x2[e] + wt[e][3] * x3[e];
-      y[e] = round_bf(siluf_(round_bf(acc))) * keep;
+      y[e] = round_bf(silu_fast(round_bf(acc))) * keep;
       x3[e] = x2[e];
       x2[e] = x1[e];
       x1[e] = x0[e];
