@@ -91,8 +91,8 @@ __device__ __forceinline__ void unpack8(const u32x4* w, float* x) {
   }
 }
 
-template <bool F32>
-__device__ __forceinline__ void load_raw(const void* base, long long elem, u32x4* w) {
+template <bool F32, class I>
+__device__ __forceinline__ void load_raw(const void* base, I elem, u32x4* w) {
   if constexpr (F32) {
     const u32x4* p = (const u32x4*)((const float*)base + elem);
     w[0] = p[0];

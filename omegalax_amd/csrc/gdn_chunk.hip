@@ -62,8 +62,15 @@ struct Cfg {
   static constexpr int WS_S = NS * 16 * LDK * 2;
   static constexpr int WS_U = 2 * 16 * LDT * 2;
   static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
-  static constexpr int TOTAL =
-      2 * NS * C * LDK * 2 + NS * C * LDT * 2 + REC + NWC * WS;
+  // bf16 rows with dk = 128 are loaded straight from global memory into one of two
+  // LDS buffers (no register staging): unpadded rows with XOR-swizzled 16-byte
+  // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
+  // into padded rows.
+  static constexpr bool DIRECT = MODE != MODE_F32 && DK == 128;
+  static constexpr int NBUF = DIRECT ? 2 : 1;
+  static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
+  static constexpr int SZV = DIRECT ? C * BV : NS * C * LDT;  // elements of a V buffer
+  static constexpr int TOTAL = NBUF * (2 * SZK * 2 + SZV * 2 + REC) + NWC * WS;
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
   static_assert(NI_KQ * NT == 2 * C * SEGS && (C * SEGS) % NT == 0, "item split");
@@ -79,45 +86,127 @@ struct Prefetch {
   u32x4 rec[Q_::NI_R];
 };
 
-// Loads of one chunk, in four parts (PART = 0..3, or -1 for all) so that a chunk's
-// prefetch can be spread over the previous chunk's compute phases: the four
-// wavefronts of a CU issuing all their loads at once would queue them behind
-// each other in the CU's memory pipeline.  Parts: record, v rows, k rows, q rows.
-template <int DK, int MODE, int PART = -1>
+// Loads of one chunk's k, q, v rows and record into registers.  Addresses are a
+// chunk-uniform base (scalar registers) plus a per-thread 32-bit offset that does not
+// change from chunk to chunk; only a sequence's last, partial chunk clamps its rows
+// (rows past the end load the last valid row, in bounds, and staging zeroes them).
+template <int DK, int MODE>
 __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE>& pf,
                                          long long t0, int nvalid, const unsigned char* rec,
                                          int hk, int h, int col0) {
   using Q_ = Cfg<DK, MODE>;
   constexpr bool F32 = MODE == MODE_F32;
+  using In = typename std::conditional<F32, float, bf16_t>::type;
   const int tid = threadIdx.x;
-  if constexpr (PART == -1 || PART == 0) {
 #pragma unroll
-    for (int k = 0; k < Q_::NI_R; ++k) {
-      const int it = tid + k * NT;
-      if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) pf.rec[k] = ((const u32x4*)rec)[it];
-    }
+  for (int k = 0; k < Q_::NI_R; ++k) {
+    const int it = tid + k * NT;
+    if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) pf.rec[k] = ((const u32x4*)rec)[it];
   }
-  if constexpr (PART == -1 || PART == 1) {
+  const unsigned ksl = (unsigned)p.ks_ld, qsl = (unsigned)p.qs_ld, vsl = (unsigned)p.vs_ld;
+  const In* kb = (const In*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
+  const In* qb = (const In*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
+  const In* vb = (const In*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
+  const bool full = nvalid == C;
 #pragma unroll
-    for (int k = 0; k < Q_::NI_V; ++k) {
-      const int it = tid + k * NT;
-      const int r = it / (BV / 8), seg = it % (BV / 8);
-      const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
-      load_raw<F32>(p.vs, tok * p.vs_ld + (long long)h * p.DV + col0 + seg * 8, pf.v[k]);
-    }
+  for (int k = 0; k < Q_::NI_V; ++k) {
+    const int it = tid + k * NT;
+    const int r = it / (BV / 8), seg = it % (BV / 8);
+    const unsigned rr = full ? r : (r < nvalid ? r : nvalid - 1);
+    load_raw<F32>(vb, rr * vsl + seg * 8u, pf.v[k]);
   }
 #pragma unroll
   for (int k = 0; k < Q_::NI_KQ; ++k) {
     constexpr int PER = C * Q_::SEGS;
-    const int which = (k * NT) / PER;  // 0 = k (part 2), 1 = q (part 3); folded when unrolled
-    if (PART != -1 && PART != 2 + which) continue;
+    const int which = (k * NT) / PER;  // 0 = k, 1 = q (folded when unrolled)
     const int rem = (k * NT) % PER + tid;
     const int r = rem / Q_::SEGS, seg = rem % Q_::SEGS;
-    // rows past the sequence end load the last valid row (in bounds); staging zeroes
-    // them, so the loaded registers are not touched until the data is needed
-    const long long tok = t0 + (r < nvalid ? r : nvalid - 1);
-    load_raw<F32>(which == 0 ? p.ks : p.qs,
-                  tok * (which == 0 ? p.ks_ld : p.qs_ld) + (long long)hk * DK + seg * 8, pf.kq[k]);
+    const unsigned rr = full ? r : (r < nvalid ? r : nvalid - 1);
+    if (which == 0) load_raw<F32>(kb, rr * ksl + seg * 8u, pf.kq[k]);
+    else load_raw<F32>(qb, rr * qsl + seg * 8u, pf.kq[k]);
+  }
+}
+
+// Swizzled layouts of the direct-loaded rows.  A K or Q row (dk = 128) is 16
+// segments of 8 bf16; logical segment g of row r sits at physical segment
+// g ^ swz_k(r).  swz_k is a bijection on 0..15, so the 16 rows of a 16-byte MFMA
+// fragment read hit 16 different segments (all 64 banks), and swz_k(r) >> 1 is
+// distinct over the rows {0..3, 8..11} that one pass of the transposed 8-byte read
+// covers, so its 8 rows x 32 bytes also spread over all banks.  A V row (64 columns)
+// is 8 segments; swz_v(r) = r & 6 makes the 8 rows x 32 bytes of a transposed read
+// pass conflict-free the same way.
+__device__ __forceinline__ int swz_k(int r) {
+  return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8);
+}
+__device__ __forceinline__ int swz_v(int r) { return r & 6; }
+
+// element offset of (row, col) in a swizzled buffer with 8-element segments
+template <int ROWLEN>
+__device__ __forceinline__ int swz_off(int row, int col) {
+  const int g = col >> 3;
+  const int sw = ROWLEN == 128 ? swz_k(row & 15) : swz_v(row);
+  return row * ROWLEN + ((g ^ sw) << 3) + (col & 7);
+}
+
+// 16x32 MFMA fragment (rows row0 + lane%16, elements k0 + 8 (lane/16) .. +7)
+__device__ __forceinline__ u32x4 swz_frag(const bf16_t* base, int row0, int k0) {
+  const int l = lane_id();
+  return *(const u32x4*)(base + swz_off<128>(row0 + (l & 15), k0 + 8 * (l >> 4)));
+}
+// transposed 16x32 fragment: rows k0 + 8q .. +7 of column col0 + r (as frag_tr)
+__device__ __forceinline__ u32x4 swz_frag_tr(const bf16_t* base, int k0, int col0) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  const int row = k0 + 8 * q + (s >> 2), col = col0 + 4 * (s & 3);
+  const u32x2 a = ds_read_tr(base + swz_off<128>(row, col));
+  const u32x2 b = ds_read_tr(base + swz_off<128>(row + 4, col));
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+// four consecutive rows row0 + 4q .. +3 of column col0 + r of a V buffer (as rows4_tr)
+__device__ __forceinline__ u32x2 swz_rows4_v(const bf16_t* base, int row0, int col0) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  return ds_read_tr(base + swz_off<BV>(row0 + 4 * q + (s >> 2), col0 + 4 * (s & 3)));
+}
+
+// Issue the loads of one chunk straight into an LDS buffer (global_load_lds_dwordx4:
+// lane i of an instruction writes 16 bytes at the buffer offset + 16 i).  Per wave: 4
+// instructions of K rows, 4 of Q, 2 of V and 4 of the record, each covering 1 KiB of
+// the buffer.  Rows past the sequence end repeat the last valid row: every product
+// they enter is multiplied by their zero beta, so they need no clearing.
+template <int DK, int MODE>
+__device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0, int nvalid,
+                                             const unsigned char* rec, int hk, int h, int col0,
+                                             bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
+  typedef __attribute__((address_space(3))) void lds_void;
+  typedef __attribute__((address_space(1))) void glob_void;
+  const int l = lane_id(), w = threadIdx.x >> 6;
+  const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
+  const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
+  const bf16_t* vb = (const bf16_t*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int mi = 4 * w + m;               // rows 4 mi .. 4 mi + 3
+    const int row = 4 * mi + (l >> 4);
+    const int rr = row < nvalid ? row : nvalid - 1;
+    const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));  // logical segment
+    const unsigned ko = (unsigned)rr * (unsigned)p.ks_ld + 8u * g;
+    const unsigned qo = (unsigned)rr * (unsigned)p.qs_ld + 8u * g;
+    __builtin_amdgcn_global_load_lds((glob_void*)(kb + ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((glob_void*)(qb + qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+  }
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const int mi = 2 * w + m;               // rows 8 mi .. 8 mi + 7
+    const int row = 8 * mi + (l >> 3);
+    const int rr = row < nvalid ? row : nvalid - 1;
+    const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
+    const unsigned vo = (unsigned)rr * (unsigned)p.vs_ld + 8u * g;
+    __builtin_amdgcn_global_load_lds((glob_void*)(vb + vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int mi = 4 * w + m;
+    __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
+                                     (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
   }
 }
 
@@ -131,16 +220,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   constexpr bool F32 = MODE == MODE_F32;
   // Each buffer is its own __shared__ object, so the compiler can tell their
   // accesses apart and overlap loads of one with stores to another.
-  __shared__ __align__(16) bf16_t sK[Q_::NS * C * LDK];
-  __shared__ __align__(16) bf16_t sQ[Q_::NS * C * LDK];
-  __shared__ __align__(16) bf16_t sV[Q_::NS * C * LDT];
-  __shared__ __align__(16) unsigned char sRec[Q_::REC];     // the chunk's record
-  __shared__ __align__(16) bf16_t sWS[NWC * Q_::WS / 2];    // per-wave scratch
-  const float* sGate = (const float*)(sRec + kRecG);
-  const float* sBeta = sGate + kGateBeta * C;  // beta
-  const float* sBE = sGate + kGateBE * C;      // beta e^G
-  const float* sEG = sGate + kGateEG * C;      // e^G
-  const float* sEL = sGate + kGateEL * C;      // e^{G_last - G}
+  constexpr bool DIRECT = Q_::DIRECT;
+  // Buffer 0 and, with direct loads, buffer 1 are separate objects, and the chunk loop
+  // below is unrolled by two so that every access names its buffer statically: the
+  // compiler can then tell that the next chunk's loads into one buffer do not touch
+  // the other, and does not wait for them before this chunk's LDS reads.
+  __shared__ __align__(16) bf16_t sK0[Q_::SZK], sK1[DIRECT ? Q_::SZK : 8];
+  __shared__ __align__(16) bf16_t sQ0[Q_::SZK], sQ1[DIRECT ? Q_::SZK : 8];
+  __shared__ __align__(16) bf16_t sV0[Q_::SZV], sV1[DIRECT ? Q_::SZV : 8];
+  __shared__ __align__(16) unsigned char sRec0[Q_::REC], sRec1[DIRECT ? Q_::REC : 16];
+  __shared__ __align__(16) bf16_t sWS[NWC * Q_::WS / 2];  // per-wave scratch
   constexpr int K_LO = C * LDK, V_LO = C * LDT;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -189,13 +278,42 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   bf16_t* wVt = wscr;                 // Vt^T [16][LDT] hi, then lo
   constexpr int WS_LO = 16 * LDK, W_LO = 16 * LDT;
 
-  Prefetch<DK, MODE> pf;
-  if (nchunks > 0)
-    prefetch<DK, MODE>(p, pf, s0, (int)((s1 - s0) < C ? (s1 - s0) : C), rec_of(0), hk, h, col0);
+  // output addressing: row stride and the lane's constant offset within a chunk
+  const int nparts = nb * NWC;                       // partial sums of o^2 per row (layer)
+  const int o_rs = p.Hv * DV, s_rs = p.Hv * nparts;  // row strides of o and of the sums
+  // unsigned: a uniform 64-bit base plus a zero-extended 32-bit lane offset is one
+  // scalar-base memory instruction with no per-lane 64-bit address arithmetic
+  const unsigned o_lane = 4u * lq * o_rs + 16u * wave + lr, s_lane = 4u * lq * s_rs;
 
-  for (int j = 0; j < nchunks; ++j) {
+  Prefetch<DK, MODE> pf;
+  if (nchunks > 0) {
+    const int nv0 = (int)((s1 - s0) < C ? (s1 - s0) : C);
+    if constexpr (DIRECT) stage_direct<DK, MODE>(p, s0, nv0, rec_of(0), hk, h, col0, sK0, sQ0, sV0, sRec0);
+    else prefetch<DK, MODE>(p, pf, s0, nv0, rec_of(0), hk, h, col0);
+  }
+
+  // one chunk: reads buffer (sK, sQ, sV, sRec); with direct loads, issues chunk j+1's
+  // loads into buffer (nK, nQ, nV, nRec)
+  auto run_chunk = [&](const int j, bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec,
+                       bf16_t* nK, bf16_t* nQ, bf16_t* nV, unsigned char* nRec) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
+    const float* sGate = (const float*)(sRec + kRecG);
+    const float* sBeta = sGate + kGateBeta * C;  // beta
+    const float* sBE = sGate + kGateBE * C;      // beta e^G
+    const float* sEG = sGate + kGateEG * C;      // e^G
+    const float* sEL = sGate + kGateEL * C;      // e^{G_last - G}
+    if constexpr (DIRECT) {
+      // this wave's loads of chunk j have landed; after the barrier every wave's have,
+      // and chunk j-1, the last reader of the other buffer, is finished everywhere
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __syncthreads();
+      if (j + 1 < nchunks) {
+        const long long tn = t0 + C;
+        stage_direct<DK, MODE>(p, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), rec_of(j + 1), hk, h,
+                               col0, nK, nQ, nV, nRec);
+      }
+    } else {
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
     // ------------------------------------------------------------ stage the chunk
@@ -255,6 +373,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       prefetch<DK, MODE>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), rec_of(j + 1), hk, h,
                          col0);
     }
+    }
 
     // ------------------------------------------------------------ K S, Q S, right-hand side
     // S^T goes to the wave's scratch as the B operand of K S and Q S.  Every operand
@@ -271,13 +390,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int s2 = 0; s2 < NSK; ++s2) {
-        frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s2, kh[i][s2], kl[i][s2]);
-        frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s2, qh[i][s2], ql[i][s2]);
+        if constexpr (DIRECT) {
+          kh[i][s2] = kl[i][s2] = swz_frag(sK, 16 * i, 32 * s2);
+          qh[i][s2] = ql[i][s2] = swz_frag(sQ, 16 * i, 32 * s2);
+        } else {
+          frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s2, kh[i][s2], kl[i][s2]);
+          frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s2, qh[i][s2], ql[i][s2]);
+        }
       }
     float vv[4][4];  // V at rows 16i + 4lq + v, column 16w + lr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x2 vw = rows4_tr(sV, LDT, 16 * i, 16 * wave);
+      const u32x2 vw = DIRECT ? swz_rows4_v(sV, 16 * i, 16 * wave) : rows4_tr(sV, LDT, 16 * i, 16 * wave);
       vv[i][0] = __uint_as_float(vw[0] << 16);
       vv[i][1] = __uint_as_float(vw[0] & 0xffff0000u);
       vv[i][2] = __uint_as_float(vw[1] << 16);
@@ -368,7 +492,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        kth[t][s2] = frag_tr(sK, LDK, 32 * s2, 16 * t);
+        kth[t][s2] = DIRECT ? swz_frag_tr(sK, 32 * s2, 16 * t) : frag_tr(sK, LDK, 32 * s2, 16 * t);
         ktl[t][s2] = IS ? frag_tr(sK + K_LO, LDK, 32 * s2, 16 * t) : kth[t][s2];
       }
     // Vt = diag(e^{G_last - G}) V_new for the state update
@@ -396,32 +520,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
           o = mma16k16(pl[x], Uh[jb], o);
         }
       }
+      // row 16i + 4lq + v of the chunk: chunk base + (16i + v) rows (uniform) + the
+      // lane's constant offset
       if constexpr (MODE != MODE_LAYER) {
-        float* orow = p.o + (t0 * p.Hv + h) * (long long)DV + col0 + 16 * wave + lr;
-        const long long rs = (long long)p.Hv * DV;  // row stride of o
+        float* ochunk = p.o + (t0 * p.Hv + h) * (long long)DV + col0;
         if (nvalid == C) {  // uniform: every row of a full chunk is stored
 #pragma unroll
-          for (int v = 0; v < 4; ++v) orow[(16 * i + 4 * lq + v) * rs] = o[v];
+          for (int v = 0; v < 4; ++v) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = o[v];
         } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = 16 * i + 4 * lq + v;
-            if (r < nvalid) orow[r * rs] = o[v];
-          }
+          for (int v = 0; v < 4; ++v)
+            if (16 * i + 4 * lq + v < nvalid) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = o[v];
         }
       } else {
         // unnormalised o in bf16 and this wave's share of sum(o^2) over its 16
         // columns; the epilogue kernel adds the shares and applies the norm
-        const int col = col0 + 16 * wave + lr;
-        const int nparts = nb * NWC;
+        bf16_t* ochunk = (bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0;
+        float* schunk = p.ss_part + (t0 * p.Hv + h) * (long long)nparts + blk * NWC + wave;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float ss = group_sum_dpp<16>(o[v] * o[v]);
-          const int r = 16 * i + 4 * lq + v;
-          if (r < nvalid) {
-            const size_t row = (size_t)(t0 + r) * p.Hv + h;
-            ((bf16_t*)p.o_part)[row * DV + col] = f2bf(o[v]);
-            if (lr == 0) p.ss_part[row * nparts + blk * NWC + wave] = ss;
+          if (16 * i + 4 * lq + v < nvalid) {
+            (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
+            if (lr == 0) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss;
           }
         }
       }
@@ -441,6 +562,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) S[t] = mm<IS, true>(S[t], kth[t][s2], ktl[t][s2], vth[s2], vtl[s2]);
     }
+  };
+
+  if constexpr (DIRECT) {
+    for (int j = 0; j < nchunks; j += 2) {
+      run_chunk(j, sK0, sQ0, sV0, sRec0, sK1, sQ1, sV1, sRec1);
+      if (j + 1 < nchunks) run_chunk(j + 1, sK1, sQ1, sV1, sRec1, sK0, sQ0, sV0, sRec0);
+    }
+  } else {
+    for (int j = 0; j < nchunks; ++j) run_chunk(j, sK0, sQ0, sV0, sRec0, sK0, sQ0, sV0, sRec0);
   }
 
   if (p.final_state) {
