@@ -58,10 +58,8 @@ struct Cfg {
   static constexpr int REC = rec_bytes(MODE);
   static constexpr int NREC16 = REC / 16;
   static constexpr int NI_R = (NREC16 + NT - 1) / NT;
-  // per-wave scratch: S^T (K S, Q S), then Vt^T (hi, lo)
-  static constexpr int WS_S = NS * 16 * LDK * 2;
-  static constexpr int WS_U = 2 * 16 * LDT * 2;
-  static constexpr int WS = WS_S > WS_U ? WS_S : WS_U;
+  // per-wave scratch: S^T, the B operand of K S and Q S
+  static constexpr int WS = NS * 16 * LDK * 2;
   // bf16 rows with dk = 128 are loaded straight from global memory into one of two
   // LDS buffers (no register staging): unpadded rows with XOR-swizzled 16-byte
   // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
@@ -131,13 +129,11 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
 // segments of 8 bf16; logical segment g of row r sits at physical segment
 // g ^ swz_k(r).  swz_k is a bijection on 0..15, so the 16 rows of a 16-byte MFMA
 // fragment read hit 16 different segments (all 64 banks), and swz_k(r) >> 1 is
-// distinct over the rows {0..3, 8..11} that one pass of the transposed 8-byte read
-// covers, so its 8 rows x 32 bytes also spread over all banks.  A V row (64 columns)
-// is 8 segments; swz_v(r) = r & 6 makes the 8 rows x 32 bytes of a transposed read
-// pass conflict-free the same way.
-__device__ __forceinline__ int swz_k(int r) {
-  return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8);
-}
+// distinct over rows 0..7 and over rows 8..15, the rows one pass of the transposed
+// 8-byte read (4 consecutive rows per 16 lanes) covers, so its 8 rows x 32 bytes
+// also spread over all banks.  A V row (64 columns) is 8 segments; swz_v(r) = r & 6
+// makes the 8 rows x 32 bytes of a transposed read pass conflict-free the same way.
+__device__ __forceinline__ int swz_k(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_v(int r) { return r & 6; }
 
 // element offset of (row, col) in a swizzled buffer with 8-element segments
@@ -153,13 +149,10 @@ __device__ __forceinline__ u32x4 swz_frag(const bf16_t* base, int row0, int k0) 
   const int l = lane_id();
   return *(const u32x4*)(base + swz_off<128>(row0 + (l & 15), k0 + 8 * (l >> 4)));
 }
-// transposed 16x32 fragment: rows k0 + 8q .. +7 of column col0 + r (as frag_tr)
-__device__ __forceinline__ u32x4 swz_frag_tr(const bf16_t* base, int k0, int col0) {
+// four consecutive rows row0 + 4q .. +3 of column col0 + r of a K buffer (as rows4_tr)
+__device__ __forceinline__ u32x2 swz_rows4_k(const bf16_t* base, int row0, int col0) {
   const int l = lane_id(), q = l >> 4, s = l & 15;
-  const int row = k0 + 8 * q + (s >> 2), col = col0 + 4 * (s & 3);
-  const u32x2 a = ds_read_tr(base + swz_off<128>(row, col));
-  const u32x2 b = ds_read_tr(base + swz_off<128>(row + 4, col));
-  return u32x4{a[0], a[1], b[0], b[1]};
+  return ds_read_tr(base + swz_off<128>(row0 + 4 * q + (s >> 2), col0 + 4 * (s & 3)));
 }
 // four consecutive rows row0 + 4q .. +3 of column col0 + r of a V buffer (as rows4_tr)
 __device__ __forceinline__ u32x2 swz_rows4_v(const bf16_t* base, int row0, int col0) {
@@ -273,10 +266,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int t = 0; t < DK / 16; ++t) S[t] = zero4();
   }
 
-  bf16_t* wscr = sWS + wave * (Q_::WS / 2);
-  bf16_t* wS = wscr;                  // S^T [16][LDK] (hi, lo)
-  bf16_t* wVt = wscr;                 // Vt^T [16][LDT] hi, then lo
-  constexpr int WS_LO = 16 * LDK, W_LO = 16 * LDT;
+  bf16_t* wS = sWS + wave * (Q_::WS / 2);  // S^T [16][LDK] (hi, lo)
+  constexpr int WS_LO = 16 * LDK;
 
   // output addressing: row stride and the lane's constant offset within a chunk
   const int nparts = nb * NWC;                       // partial sums of o^2 per row (layer)
@@ -487,21 +478,26 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       if constexpr (OS) pl[x] = *(const u32x2*)(sRec + kRecPL + x * kTileBytes + 8 * l);
       else pl[x] = ph[x];
     }
-    u32x4 kth[DK / 16][2], ktl[DK / 16][2];
+    // K^T blocks of the state update as 16x16x16 A operands: lane (q, r) holds
+    // K[16kb + 4q .. +3][16t + r], four token rows of one dk column
+    u32x2 kth[DK / 16][4], ktl[DK / 16][4];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        kth[t][s2] = DIRECT ? swz_frag_tr(sK, 32 * s2, 16 * t) : frag_tr(sK, LDK, 32 * s2, 16 * t);
-        ktl[t][s2] = IS ? frag_tr(sK + K_LO, LDK, 32 * s2, 16 * t) : kth[t][s2];
+      for (int kb = 0; kb < 4; ++kb) {
+        kth[t][kb] = DIRECT ? swz_rows4_k(sK, 16 * kb, 16 * t) : rows4_tr(sK, LDK, 16 * kb, 16 * t);
+        ktl[t][kb] = IS ? rows4_tr(sK + K_LO, LDK, 16 * kb, 16 * t) : kth[t][kb];
       }
-    // Vt = diag(e^{G_last - G}) V_new for the state update
+    // Vt = diag(e^{G_last - G}) V_new: its C-layout blocks are the 16x16x16 B operands of
+    // the state update, so it stays in registers (hi and lo)
+    u32x2 vth[4], vtl[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 vt;
       const float4 el = *(const float4*)(sEL + 16 * i + 4 * lq);
       vt[0] = U[i][0] * el.x; vt[1] = U[i][1] * el.y; vt[2] = U[i][2] * el.z; vt[3] = U[i][3] * el.w;
-      store_ct_split(wVt, wVt + W_LO, LDT, 16 * i, 0, vt);
+      vth[i] = pack_hi4(vt);
+      vtl[i] = pack_lo4(vt);
     }
 
     // ------------------------------------------------------------ O = scale e^G (Q S) + P V_new
@@ -550,17 +546,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 
 
     // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
-    wave_lds_fence();  // Vt^T stores above are visible to the wave's fragment loads
-    u32x4 vth[2], vtl[2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) frag2<true>(wVt, W_LO, LDT, 0, 32 * s2, vth[s2], vtl[s2]);
     const float gl = sEG[C - 1];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) S[t][v] *= gl;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) S[t] = mm<IS, true>(S[t], kth[t][s2], ktl[t][s2], vth[s2], vtl[s2]);
+      for (int kb = 0; kb < 4; ++kb) {
+        S[t] = mma16k16(kth[t][kb], vth[kb], S[t]);
+        S[t] = mma16k16(kth[t][kb], vtl[kb], S[t]);
+        if constexpr (IS) S[t] = mma16k16(ktl[t][kb], vth[kb], S[t]);
+      }
     }
   };
 
