@@ -165,7 +165,9 @@ __device__ __forceinline__ u32x2 swz_rows4_v(const bf16_t* base, int row0, int c
 // instructions of K rows, 4 of Q, 2 of V and 4 of the record, each covering 1 KiB of
 // the buffer.  Rows past the sequence end repeat the last valid row: every product
 // they enter is multiplied by their zero beta, so they need no clearing.
-template <int DK, int MODE>
+// PART selects a part of the instructions (0: record, 1: v, 2: k, 3: q) or all (-1),
+// so that the issue can be spread over a chunk's phases.
+template <int DK, int MODE, int PART = -1>
 __device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0, int nvalid,
                                              const unsigned char* rec, int hk, int h, int col0,
                                              bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
@@ -175,31 +177,41 @@ __device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0,
   const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
   const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
   const bf16_t* vb = (const bf16_t*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
+  if constexpr (PART == -1 || PART == 0) {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int mi = 4 * w + m;               // rows 4 mi .. 4 mi + 3
-    const int row = 4 * mi + (l >> 4);
-    const int rr = row < nvalid ? row : nvalid - 1;
-    const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));  // logical segment
-    const unsigned ko = (unsigned)rr * (unsigned)p.ks_ld + 8u * g;
-    const unsigned qo = (unsigned)rr * (unsigned)p.qs_ld + 8u * g;
-    __builtin_amdgcn_global_load_lds((glob_void*)(kb + ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((glob_void*)(qb + qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+    for (int m = 0; m < 4; ++m) {
+      const int mi = 4 * w + m;
+      __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
+                                       (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+    }
   }
+  if constexpr (PART == -1 || PART == 1) {
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int mi = 2 * w + m;               // rows 8 mi .. 8 mi + 7
-    const int row = 8 * mi + (l >> 3);
-    const int rr = row < nvalid ? row : nvalid - 1;
-    const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
-    const unsigned vo = (unsigned)rr * (unsigned)p.vs_ld + 8u * g;
-    __builtin_amdgcn_global_load_lds((glob_void*)(vb + vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
+    for (int m = 0; m < 2; ++m) {
+      const int mi = 2 * w + m;               // rows 8 mi .. 8 mi + 7
+      const int row = 8 * mi + (l >> 3);
+      const int rr = row < nvalid ? row : nvalid - 1;
+      const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
+      const unsigned vo = (unsigned)rr * (unsigned)p.vs_ld + 8u * g;
+      __builtin_amdgcn_global_load_lds((glob_void*)(vb + vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
+    }
   }
+  if constexpr (PART == -1 || PART == 2 || PART == 3) {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int mi = 4 * w + m;
-    __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
-                                     (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+    for (int m = 0; m < 4; ++m) {
+      const int mi = 4 * w + m;               // rows 4 mi .. 4 mi + 3
+      const int row = 4 * mi + (l >> 4);
+      const int rr = row < nvalid ? row : nvalid - 1;
+      const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));  // logical segment
+      if constexpr (PART != 3) {
+        const unsigned ko = (unsigned)rr * (unsigned)p.ks_ld + 8u * g;
+        __builtin_amdgcn_global_load_lds((glob_void*)(kb + ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
+      }
+      if constexpr (PART != 2) {
+        const unsigned qo = (unsigned)rr * (unsigned)p.qs_ld + 8u * g;
+        __builtin_amdgcn_global_load_lds((glob_void*)(qb + qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+      }
+    }
   }
 }
 
@@ -289,6 +301,17 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
                        bf16_t* nK, bf16_t* nQ, bf16_t* nV, unsigned char* nRec) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
+    // the next chunk's loads go out in four parts spread over this chunk's phases, so
+    // the four wavefronts do not queue all their loads at once
+    const bool more = DIRECT && j + 1 < nchunks;
+    const long long tn = t0 + C;
+    const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
+    const unsigned char* recn = rec_of(more ? j + 1 : j);
+    auto stage_next = [&](auto part) {
+      if constexpr (DIRECT)
+        if (more)
+          stage_direct<DK, MODE, decltype(part)::value>(p, tn, nvn, recn, hk, h, col0, nK, nQ, nV, nRec);
+    };
     const float* sGate = (const float*)(sRec + kRecG);
     const float* sBeta = sGate + kGateBeta * C;  // beta
     const float* sBE = sGate + kGateBE * C;      // beta e^G
@@ -299,11 +322,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       // and chunk j-1, the last reader of the other buffer, is finished everywhere
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       __syncthreads();
-      if (j + 1 < nchunks) {
-        const long long tn = t0 + C;
-        stage_direct<DK, MODE>(p, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), rec_of(j + 1), hk, h,
-                               col0, nK, nQ, nV, nRec);
-      }
+      stage_next(std::integral_constant<int, 0>{});
     } else {
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
@@ -422,6 +441,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
         QS[i] = mm<IS, IS>(QS[i], qh[i][s2], ql[i][s2], sh[s2], sl[s2]);
       }
+    stage_next(std::integral_constant<int, 1>{});
     // T fragments for V_new = T R (read while the products run)
     u32x2 th[10], tl[10];
 #pragma unroll
@@ -470,6 +490,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       Uh[i] = pack_hi4(U[i]);
       Ul[i] = pack_lo4(U[i]);
     }
+    stage_next(std::integral_constant<int, 2>{});
     // P fragments and the K^T fragments of the state update (read while V_new forms)
     u32x2 ph[10], pl[10];
 #pragma unroll
@@ -544,6 +565,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       }
     }
 
+
+    stage_next(std::integral_constant<int, 3>{});
 
     // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
     const float gl = sEG[C - 1];
