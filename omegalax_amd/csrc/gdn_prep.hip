@@ -11,8 +11,9 @@
 //   * per value head: the gates (:248-250 on the layer path), G = cumsum(g)
 //     (:98), L = strict_lower(beta_i (k_i.k_j) e^{G_i-G_j}) (:100-108),
 //     T = (I + L)^-1 (:110-113), P = lower(scale (q_i.k_j) e^{G_i-G_j}) (:130-131).
-// T is formed by blocks: each wavefront inverts one 16x16 diagonal block by
-// forward substitution, then wavefront j runs down block column j,
+// T is formed by blocks: each wavefront inverts one 16x16 diagonal block by the
+// product (I + N)(I + N^2)(I + N^4)(I + N^8) with N = -L_ww, then wavefront j runs
+// down block column j,
 //     T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj,
 // on 16x16x16 MFMAs with hi+lo bf16 operands (fp32-accurate products).  The
 // outputs go to the per-(chunk, value head) record described in gdn_chunk.h.
@@ -30,7 +31,7 @@ namespace omx {
 
 namespace {
 
-constexpr int C = kC, NT = kNT, LDD = kLDD;
+constexpr int C = kC, NT = kNT;
 
 template <int DK, int MODE>
 struct PrepCfg {
@@ -59,6 +60,33 @@ constexpr unsigned long long kTilesLo = pack_tiles(0, 12), kTilesHi = pack_tiles
 
 __device__ __forceinline__ int tile_code(int t) {
   return t < 12 ? (int)((kTilesLo >> (5 * t)) & 31) : (int)((kTilesHi >> (5 * (t - 12))) & 31);
+}
+
+// A 16x16 block in both MFMA layouts: fc = C layout (lane (q, r) holds rows
+// 4q..4q+3 of column r), fa = A layout (lane (q, r) holds row r, columns 4q..4q+3),
+// with the bf16 hi/lo packs of each.
+struct Blk {
+  f32x4 fa, fc;
+  u32x2 ah, al, ch, cl;
+  __device__ __forceinline__ void set(f32x4 a, f32x4 c) {
+    fa = a;
+    fc = c;
+    ah = pack_hi4(a);
+    al = pack_lo4(a);
+    ch = pack_hi4(c);
+    cl = pack_lo4(c);
+  }
+};
+
+// X Y in both layouts: (X Y)_C from A(X) and C(Y); (X Y)_A = ((X Y)^T)_C = (Y^T X^T)_C,
+// whose A operand is Y^T (= C(Y) read as A) and B operand X^T (= A(X) read as B)
+__device__ __forceinline__ Blk blk_mul(const Blk& x, const Blk& y) {
+  Blk r;
+  r.set(mm3k16(zero4(), y.ch, y.cl, x.ah, x.al), mm3k16(zero4(), x.ah, x.al, y.ch, y.cl));
+  return r;
+}
+__device__ __forceinline__ f32x4 blk_mul_c(const Blk& x, const Blk& y) {
+  return mm3k16(zero4(), x.ah, x.al, y.ch, y.cl);
 }
 
 __device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
@@ -261,11 +289,10 @@ __global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
   __shared__ __align__(16) bf16_t sK[Q_::NS * C * LDK];   // K rows [token][dk] (hi, lo)
   __shared__ __align__(16) bf16_t sQ[Q_::NS * C * LDK];   // Q rows
   __shared__ __align__(16) u32x2 sLf[10 * 2 * 64];        // L blocks as A fragments (hi, lo)
-  __shared__ __align__(16) bf16_t sTdT[2 * C * LDD];      // diagonal inverses, transposed (hi, lo)
-  __shared__ __align__(16) float sLd[C * LDD];            // diagonal blocks of L (wave w: rows 16w..)
+  __shared__ __align__(16) u32x2 sTd[4 * 2 * 64];         // diagonal inverses as A fragments (hi, lo)
   __shared__ __align__(16) float sGw[4 * 2 * C];          // per wave: G log2(e), beta
   __shared__ __align__(16) float sGin[kGatePf * 2 * C];   // the task's prefetched gate inputs
-  constexpr int K_LO = C * LDK, TD_LO = C * LDD;
+  constexpr int K_LO = C * LDK;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -451,47 +478,53 @@ __global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
             val[v] = bt * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i > m);
           }
           if (ti == 0) {
-            // the diagonal block: T_ww = (I + L_ww)^-1 by forward substitution, one
-            // column per lane (lanes 16..63 repeat the columns of lanes 0..15)
-            *(float4*)(sLd + i * LDD + 4 * lq) = float4{val[0], val[1], val[2], val[3]};
-            wave_lds_fence();
-            const int cc = l & 15;
-            float x[16];
-  #pragma unroll
-            for (int ii = 0; ii < 16; ++ii) {
-              const float* row = sLd + (16 * bi + ii) * LDD;
-              float a0 = (ii == cc) ? 1.f : 0.f, a1 = 0.f;
-  #pragma unroll
-              for (int mm2 = 0; mm2 < ii; mm2 += 4) {
-                const float4 r4 = *(const float4*)(row + mm2);
-                a0 -= r4.x * x[mm2];
-                if (mm2 + 1 < ii) a1 -= r4.y * x[mm2 + 1];
-                if (mm2 + 2 < ii) a0 -= r4.z * x[mm2 + 2];
-                if (mm2 + 3 < ii) a1 -= r4.w * x[mm2 + 3];
-              }
-              x[ii] = a0 + a1;
-            }
-            // C layout: lane (q, r) holds rows 4q..4q+3 of column r = its own column
-  #pragma unroll
-            for (int v = 0; v < 4; ++v)
-              Tw[v] = lq == 0 ? x[v] : (lq == 1 ? x[4 + v] : (lq == 2 ? x[8 + v] : x[12 + v]));
-            if (l < 16) {
-              // T_ww^T row cc = column cc of T_ww, hi and lo, for the other waves
-              bf16_t* dh = sTdT + (16 * bi + cc) * LDD;
-              bf16_t* dl = dh + TD_LO;
-  #pragma unroll
-              for (int h8 = 0; h8 < 2; ++h8) {
-                float hv[8];
-  #pragma unroll
-                for (int e = 0; e < 8; ++e) hv[e] = x[8 * h8 + e];
-                *(u32x4*)(dh + 8 * h8) = pack8(hv);
-                *(u32x4*)(dl + 8 * h8) = pack8_lo(hv);
+            // The diagonal block.  With N = -L_ww (strictly lower, so N^16 = 0),
+            //   T_ww = (I + L_ww)^-1 = (I + N)(I + N^2)(I + N^4)(I + N^8),
+            // formed in registers on 16x16x16 MFMAs in split precision.  Each product
+            // is kept in two layouts: C (lane (q, r) holds rows 4q..4q+3 of column r,
+            // the B operand of the next product) and A (the transpose of that: the A
+            // operand), the A form computed as the transposed product (X Y)^T = Y^T X^T
+            // from the same packed operands.
+            Blk n1;
+            f32x4 nc;  // C layout of N: entry (16bi + 4lq + v, 16bi + lr); K K^T is symmetric
+            {
+              const int m2 = 16 * bi + lr;
+              const float Gm2 = gw[m2];
+              const float4 Gi4 = *(const float4*)(gw + 16 * bi + 4 * lq);
+              const float4 Bi4 = *(const float4*)(gw + C + 16 * bi + 4 * lq);
+              const float gi2[4] = {Gi4.x, Gi4.y, Gi4.z, Gi4.w}, bt2[4] = {Bi4.x, Bi4.y, Bi4.z, Bi4.w};
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int i2 = 16 * bi + 4 * lq + v;
+                nc[v] = -bt2[v] * acc[v] * __builtin_amdgcn_exp2f(fminf(gi2[v] - Gm2, 0.f)) *
+                        (float)(i2 > m2);
               }
             }
-            wave_lds_fence();
+            n1.set(-val, nc);
+            const Blk n2 = blk_mul(n1, n1), n4 = blk_mul(n2, n2);
+            const f32x4 n8c = blk_mul_c(n4, n4);
+            f32x4 eye;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) eye[v] = (float)(4 * lq + v == lr);
+            Blk x1, x2;
+            {
+              const Blk y = blk_mul(n1, n2);
+              x1.set(eye + n1.fa + n2.fa + y.fa, eye + n1.fc + n2.fc + y.fc);
+            }
+            {
+              const Blk z = blk_mul(x1, n4);
+              x2.set(x1.fa + z.fa, x1.fc + z.fc);
+            }
+            const u32x2 n8h = pack_hi4(n8c), n8l = pack_lo4(n8c);
+            const f32x4 Tc = x2.fc + mm3k16(zero4(), x2.ah, x2.al, n8h, n8l);
+            const f32x4 Ta = x2.fa + mm3k16(zero4(), n8h, n8l, x2.ah, x2.al);
+            Tw = Tc;
+            const u32x2 th = pack_hi4(Ta), tl = pack_lo4(Ta);
+            sTd[(2 * bi) * 64 + l] = th;  // A fragments of T_ww for the other waves
+            sTd[(2 * bi + 1) * 64 + l] = tl;
             const int tw = kRecT + 2 * tile_index(bi, bi) * kTileBytes;
-            put_tile(rec, tw, rows4_tr(sTdT, LDD, 16 * bi, 0));
-            put_tile(rec, tw + kTileBytes, rows4_tr(sTdT + TD_LO, LDD, 16 * bi, 0));
+            put_tile(rec, tw, th);
+            put_tile(rec, tw + kTileBytes, tl);
           } else {
             u32x2* d = sLf + 2 * 64 * tile_index(bi, bj) + l;
             d[0] = pack_hi4(val);
@@ -534,8 +567,8 @@ __global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
             X = mm3k16(X, f[0], f[64], Th[k], Tl[k]);
           }
           // the T_ii fragment is negated (a sign flip is exact in bf16)
-          const u32x2 th = rows4_tr(sTdT, LDD, 16 * i, 0) ^ 0x80008000u;
-          const u32x2 tl = rows4_tr(sTdT + TD_LO, LDD, 16 * i, 0) ^ 0x80008000u;
+          const u32x2 th = sTd[(2 * i) * 64 + l] ^ 0x80008000u;
+          const u32x2 tl = sTd[(2 * i + 1) * 64 + l] ^ 0x80008000u;
           const u32x2 xh = pack_hi4(X), xl = pack_lo4(X);
           const f32x4 Tij = mm3k16(zero4(), th, tl, xh, xl);
           const f32x4 TijT = mm3k16(zero4(), xh, xl, th, tl);
@@ -546,7 +579,7 @@ __global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
           put_tile(rec, off + kTileBytes, pack_lo4(TijT));
         }
       }
-      __syncthreads();  // sLf / sTdT are rewritten for the next value head
+      __syncthreads();  // sLf / sTd are rewritten for the next value head
     }
   }
 }
