@@ -554,12 +554,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         // columns; the epilogue kernel adds the shares and applies the norm
         bf16_t* ochunk = (bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0;
         float* schunk = p.ss_part + (t0 * p.Hv + h) * (long long)nparts + blk * NWC + wave;
+        float ss[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float ss = group_sum_dpp<16>(o[v] * o[v]);
-          if (16 * i + 4 * lq + v < nvalid) {
-            (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
-            if (lr == 0) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss;
+        for (int v = 0; v < 4; ++v) ss[v] = group_sum_dpp<16>(o[v] * o[v]);
+        if (nvalid == C) {  // uniform: every row of a full chunk is stored
+#pragma unroll
+          for (int v = 0; v < 4; ++v) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
+          if (lr == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss[v];
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            if (16 * i + 4 * lq + v < nvalid) {
+              (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
+              if (lr == 0) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss[v];
+            }
           }
         }
       }
