@@ -93,7 +93,7 @@ size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_
  *   mixed_qkv     [B, T, conv_dim] bf16  (in_proj_qkv output, token-major)
  *   z             [B, T, Hv, dv] bf16
  *   a, b          [B, T, Hv] bf16
- *   conv_w        [conv_dim, K] f32 (cast to bf16 as at deltanet.py:243)
+ *   conv_w        [conv_dim, K] f32, 16-byte aligned (cast to bf16 as at deltanet.py:243)
  *   A_log, dt_bias [Hv] f32;  norm_w [dv] f32 (16-byte aligned);  eps (rms_norm_eps)
  *   cu_seqlens    as for omx_gdn_chunk_fwd (conv history also restarts per sequence)
  *   initial_state / final_state  [N, Hv, dk, dv] f32 or NULL

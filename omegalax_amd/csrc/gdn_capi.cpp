@@ -305,7 +305,8 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
           fn);
   REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(z, 16) && aligned(out, 16)),
           "%s: mixed_qkv, z and out must be 16-byte aligned", fn);
-  REQUIRE(aligned(norm_w, 16), "%s: norm_w must be 16-byte aligned", fn);
+  REQUIRE(aligned(norm_w, 16) && aligned(conv_w, 16), "%s: norm_w and conv_w must be 16-byte aligned",
+          fn);
   omx::ChunkParams p{};
   p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b;
   p.conv_w = conv_w; p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w;

@@ -97,6 +97,17 @@ __device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
 // wt[e][d] multiplies the input d tokens back (tap K-1-d); taps beyond K are 0
 __device__ __forceinline__ void load_conv_w(const ChunkParams& p, int ch0, float (*wt)[4]) {
   const int K = p.conv_k;
+  if (K == 4) {  // uniform: each channel's taps are one 16-byte row
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float4 w = *(const float4*)(p.conv_w + (size_t)(ch0 + e) * 4);
+      wt[e][0] = round_bf(w.w);
+      wt[e][1] = round_bf(w.z);
+      wt[e][2] = round_bf(w.y);
+      wt[e][3] = round_bf(w.x);
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float* w = p.conv_w + (size_t)(ch0 + e) * K;
@@ -281,8 +292,13 @@ __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTa
   }
 }
 
+// Workgroups per CU the register budget is set for: the layer mode's single task per
+// workgroup waits on its conv inputs, so more resident workgroups hide that latency.
+template <int MODE>
+constexpr int prep_min_blocks() { return MODE == MODE_LAYER ? 3 : 2; }
+
 template <int DK, int MODE>
-__global__ __launch_bounds__(NT) void prep_kernel(ChunkParams p) {
+__global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, F32 = MODE == MODE_F32;
