@@ -620,7 +620,7 @@ hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
   // prefetching its next task while it computes the current one
   const long long tasks = (long long)p.n_rec * p.Hk;
   if (tasks == 0) return hipSuccess;
-  const long long cap = prep_persistent<MODE>() ? 2LL * device_cus() : tasks;
+  const long long cap = prep_persistent<MODE>() ? (long long)prep_min_blocks<MODE>() * device_cus() : tasks;
   const unsigned grid = (unsigned)(tasks < cap ? tasks : cap);
   hipLaunchKernelGGL((prep_kernel<DK, MODE>), dim3(grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
