@@ -1,13 +1,16 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X GatedDeltaNet path on one GPU; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|core]
 
 Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   prefill  config C1: GDN layer prefill from projection outputs (mixed_qkv, z, a, b)
            to the gated-norm output, B=4 T=4096 Hk=16 Hv=32 d=128 (headline).
            A "step" is one omx_gdn_prefill call over the whole batch.
   decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
+  core     one chunk_gated_delta_rule call at --batch/--seq-len/--k-heads/--v-heads
+           (C1 by default; C4 is --batch 1 --seq-len 65536 --v-heads 64).
+  copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
 rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
 shapes: the chunk-parallel preparation kernel and the state scan), and carries the
@@ -101,7 +104,8 @@ def bench_decode(B, steps, warmup, cpu_baseline):
         "batch": B, "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
         "tokens_per_s": B * steps / wall,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": gbs / PEAK_HBM_GBS, "traffic": None,
+                     "frac": gbs / PEAK_HBM_GBS,
+                     "traffic": MEASURED_TRAFFIC.get(("decode", B, Hk, Hv, d)),
                      "algorithmic_bytes": nbytes},
     }
     if cpu_baseline:
@@ -128,11 +132,61 @@ def cpu_decode_baseline(B=8, budget_s=10.0):
             "sample": f"{n} decode steps of the numpy fp64 oracle at B={B}, C2 head layout"}
 
 
+# ----------------------------------------------------------------------------- core call
+
+# HBM bytes per call from two rocprofv3 --pmc runs (FETCH_SIZE x 2.0 and WRITE_SIZE x 1.0,
+# scaled by a plain copy kernel's counters), for the shapes they were taken on; summaries
+# and commands in profiles/prefill_c1.md and profiles/decode_step_c2_b64.md.
+MEASURED_TRAFFIC = {
+    ("core", 4, 4096, 16, 32, 128): 1_079_644_160,  # prep 133 MiB + 256, scan 384 + 256
+    ("decode", 64, 16, 32, 128): 277_401_702,       # state read + written once
+}
+
+
+def bench_core(B, T, Hk, Hv, d, steps, warmup, arrs=None):
+    """One chunk_gated_delta_rule call (bf16 q/k/v, fp32 gates) over [B, T]: the
+    chunk-parallel preparation kernel and the state scan, HIP-event timed."""
+    import torch
+    from omegalax_amd import chunk_gated_delta_rule, workloads as W
+    rng = np.random.default_rng(7)
+
+    def act(*shape):
+        x = W.round_bf16(rng.standard_normal(shape, dtype=np.float32))
+        return torch.from_numpy(x).cuda().bfloat16()
+
+    q, k, v = act(B, T, Hk, d), act(B, T, Hk, d), act(B, T, Hv, d)
+    if arrs is None:
+        arrs = W.layer_inputs(B, T, Hk, Hv, d, d) if B * T <= 16384 else None
+    if arrs is not None:
+        g32, beta32 = W.gates_f32(arrs["a"], arrs["b"], arrs["A_log"], arrs["dt_bias"])
+    else:
+        g32 = -0.1 * rng.random((B, T, Hv), dtype=np.float32)
+        beta32 = rng.random((B, T, Hv), dtype=np.float32)
+    g = torch.from_numpy(g32).cuda()
+    beta = torch.from_numpy(beta32).cuda()
+
+    def core():
+        chunk_gated_delta_rule(q, k, v, g, beta, C)
+
+    _say(f"core: B={B} T={T} Hk={Hk} Hv={Hv} timing {steps} launches")
+    wall, ms = time_launches(core, steps, warmup)
+    flops = prefill_flops_per_token_head(d, d) * B * T * Hv
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                     "traffic": MEASURED_TRAFFIC.get(("core", B, T, Hk, Hv, d)),
+                     "algorithmic_flops": flops,
+                     "kernels": "prep_kernel + scan_kernel (the two launches of one call)"},
+    }
+
+
 # ----------------------------------------------------------------------------- prefill (C1)
 
 def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
     import torch
-    from omegalax_amd import chunk_gated_delta_rule, gdn_prefill, workloads as W
+    from omegalax_amd import gdn_prefill, workloads as W
     Hk, Hv, d = 16, 32, 128
     _say(f"prefill: B={B} T={T} generating inputs")
     arrs = W.layer_inputs(B, T, Hk, Hv, d, d)
@@ -146,30 +200,13 @@ def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
     _say(f"prefill: timing {steps} layer steps")
     wall, ms_step = time_launches(step, steps, warmup)
     tokens = B * T
-    flops = prefill_flops_per_token_head(d, d) * tokens * Hv
 
-    # the dominant kernel, the chunked scan, at the core-function boundary on the same shapes
-    rng = np.random.default_rng(7)
-    q = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hk, d), dtype=np.float32))).cuda().bfloat16()
-    k = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hk, d), dtype=np.float32))).cuda().bfloat16()
-    v = torch.from_numpy(W.round_bf16(rng.standard_normal((B, T, Hv, d), dtype=np.float32))).cuda().bfloat16()
-    g32, beta32 = W.gates_f32(arrs["a"], arrs["b"], arrs["A_log"], arrs["dt_bias"])
-    g = torch.from_numpy(g32).cuda()
-    beta = torch.from_numpy(beta32).cuda()
-
-    def core():
-        chunk_gated_delta_rule(q, k, v, g, beta, 64)
-
-    _say(f"prefill: timing {steps} core-kernel launches")
-    _, ms_core = time_launches(core, steps, warmup)
-    tf = flops / (ms_core * 1e-3) / 1e12
+    # the dominant kernels, prep + scan, at the core-function boundary on the same shapes
+    core = bench_core(B, T, Hk, Hv, d, steps, warmup, arrs)
     res = {
         "tokens_per_s": tokens * steps / wall, "ms_per_step": wall / steps * 1e3,
-        "step_event_ms": ms_step, "core_kernel_ms": ms_core,
-        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
-                     "algorithmic_flops": flops,
-                     "kernels": "prep_kernel + scan_kernel (the two launches of one call)"},
+        "step_event_ms": ms_step, "core_kernel_ms": core["kernel_ms"],
+        "roofline": core["roofline"],
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_prefill_baseline()
@@ -200,8 +237,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode"], default="prefill")
+    ap.add_argument("--workload", choices=["prefill", "decode", "core", "copy"],
+                    default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
+    ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
+    ap.add_argument("--seq-len", type=int, default=4096, help="core workload: tokens each")
+    ap.add_argument("--k-heads", type=int, default=16, help="core workload")
+    ap.add_argument("--v-heads", type=int, default=32, help="core workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -214,6 +256,34 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     cpu = not args.no_cpu_baseline
+    if args.workload == "copy":
+        # calibration of the FETCH_SIZE / WRITE_SIZE counters: a plain 256 MiB device copy
+        src = torch.empty(1 << 26, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        wall, ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup)
+        gbs = 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
+        print(json.dumps({"metric": "device copy GB/s (counter calibration)", "value": gbs,
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+                          "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                          "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": "256 MiB read + 256 MiB written"}}), flush=True)
+        return 0
+    if args.workload == "core":
+        B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads
+        core = bench_core(B, T, Hk, Hv, 128, args.steps, args.warmup)
+        line = {
+            "metric": "chunk_gated_delta_rule TFLOP/s (bf16 MFMA roofline)",
+            "value": core["roofline"]["achieved"], "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": core["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) activations, random-init params)",
+            "config": {"workload": f"chunk_gated_delta_rule B={B} T={T} Hk={Hk} Hv={Hv} d=128",
+                       "chunk": C},
+            "roofline": core["roofline"], "kernel_ms": core["kernel_ms"],
+        }
+        print(json.dumps(line), flush=True)
+        return 0
     if args.workload == "decode":
         dec = bench_decode(args.decode_batch, args.steps, args.warmup, cpu)
         line = {
