@@ -8,10 +8,14 @@
 //   P = lower(scale (q_i . k_j) e^{G_i - G_j}) (deltanet.py:130-131), bf16 (hi + lo
 //       for fp32 inputs), as A-operand fragments;
 //   the gate vectors beta, beta e^G, e^G and e^{G_last - G} (fp32).
-// A 16x16 tile (bi, bj) of a 64x64 lower-triangular matrix M is stored as the
-// 16x16x16 MFMA A operand: lane (q, r) = (lane / 16, lane % 16) holds
-// M[16 bi + r][16 bj + 4q .. 4q + 3] as four bf16 in one 8-byte word; tile
-// index bi (bi + 1) / 2 + bj, 512 bytes per tile, lanes in order.
+// The 64x64 lower-triangular T and P are stored as 16x32 A operands of the
+// 16x16x32 MFMA whose contraction runs over two 16-token blocks 2p, 2p+1: for
+// row block i and block pair p <= i/2, lane (q, r) = (lane / 16, lane % 16)
+// holds 16 bytes, M[16i + r][32p + 4q .. +3] then M[16i + r][32p + 16 + 4q .. +3]
+// (the 16x16 tiles (i, 2p) and (i, 2p+1), each in the 16x16x16 A layout).  The
+// contraction order matches a B operand built from two C-layout tiles of the
+// right-hand side.  The upper tiles (0, 1) and (2, 3) that complete the pairs of
+// row blocks 0 and 2 are stored as zeros.  Six pairs, 1 KiB each, lanes in order.
 #pragma once
 
 #include "gdn_common.h"
@@ -27,18 +31,31 @@ constexpr int kLDD = 16 + 4;   // row stride of 16-wide LDS arrays
 constexpr int MODE_BF16 = kModeBF16, MODE_F32 = kModeF32, MODE_LAYER = kModeLayer;
 
 // record layout (bytes)
-constexpr int kTileBytes = 64 * 8;           // one A-operand tile, all lanes
-constexpr int kRecT = 0;                     // 10 tiles x {hi, lo}
-constexpr int kRecP = kRecT + 20 * kTileBytes;  // 10 tiles (hi)
-constexpr int kRecG = kRecP + 10 * kTileBytes;  // 4 x 64 fp32 gate vectors
-constexpr int kRecPL = kRecG + 4 * kC * 4;      // fp32 inputs: 10 tiles of P lo parts
-constexpr int kRecBytesBF16 = kRecPL;           // 16384
-constexpr int kRecBytesF32 = kRecPL + 10 * kTileBytes;  // 21504
+constexpr int kPairBytes = 64 * 16;            // one 16x32 A operand, all lanes
+constexpr int kNPairs = 6;                     // (i, p): (0,0) (1,0) (2,0) (2,1) (3,0) (3,1)
+constexpr int kRecT = 0;                       // 6 pairs x {hi, lo}
+constexpr int kRecP = kRecT + 2 * kNPairs * kPairBytes;  // 6 pairs (hi)
+constexpr int kRecG = kRecP + kNPairs * kPairBytes;      // 4 x 64 fp32 gate vectors
+constexpr int kRecPL = kRecG + 4 * kC * 4;               // fp32 inputs: P lo parts
+constexpr int kRecBytesBF16 = kRecPL;                    // 19456
+constexpr int kRecBytesF32 = kRecPL + kNPairs * kPairBytes;  // 25600
 constexpr int kGateBeta = 0, kGateBE = 1, kGateEG = 2, kGateEL = 3;  // rows of the gate block
 
 __host__ __device__ constexpr int rec_bytes(int mode) {
   return mode == MODE_F32 ? kRecBytesF32 : kRecBytesBF16;
 }
+// index of the block pair (i, p), p <= i / 2
+__host__ __device__ constexpr int pair_index(int i, int p) { return i + (i == 3) + p; }
+// byte offsets of 16x16 tile (i, j), j <= i + (i even), in the record: its pair's
+// 16 bytes per lane, first or second 8 (add 16 lane).  T lo parts follow T hi by one
+// pair; P lo parts (fp32 inputs) sit at kRecPL - kRecP further.
+__host__ __device__ constexpr int rec_t_off(int i, int j) {
+  return kRecT + 2 * pair_index(i, j >> 1) * kPairBytes + 8 * (j & 1);
+}
+__host__ __device__ constexpr int rec_p_off(int i, int j) {
+  return kRecP + pair_index(i, j >> 1) * kPairBytes + 8 * (j & 1);
+}
+// index of 16x16 tile (bi, bj), bj <= bi, of a lower-triangular 64x64 matrix
 __host__ __device__ constexpr int tile_index(int bi, int bj) { return bi * (bi + 1) / 2 + bj; }
 
 template <bool AS, bool BS>

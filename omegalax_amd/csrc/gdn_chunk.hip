@@ -58,8 +58,6 @@ struct Cfg {
   static constexpr int REC = rec_bytes(MODE);
   static constexpr int NREC16 = REC / 16;
   static constexpr int NI_R = (NREC16 + NT - 1) / NT;
-  // per-wave scratch: S^T, the B operand of K S and Q S
-  static constexpr int WS = NS * 16 * LDK * 2;
   // bf16 rows with dk = 128 are loaded straight from global memory into one of two
   // LDS buffers (no register staging): unpadded rows with XOR-swizzled 16-byte
   // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
@@ -68,8 +66,9 @@ struct Cfg {
   static constexpr int NBUF = DIRECT ? 2 : 1;
   static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
   static constexpr int SZV = DIRECT ? C * BV : NS * C * LDT;  // elements of a V buffer
-  static constexpr int TOTAL = NBUF * (2 * SZK * 2 + SZV * 2 + REC) + NWC * WS;
+  static constexpr int TOTAL = NBUF * (2 * SZK * 2 + SZV * 2 + REC);
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
+  static_assert(!DIRECT || REC % 1024 == 0, "direct loads move the record in 1 KiB pieces");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
   static_assert(NI_KQ * NT == 2 * C * SEGS && (C * SEGS) % NT == 0, "item split");
   static_assert(NI_V * NT == C * (BV / 8), "item split");
@@ -160,29 +159,70 @@ __device__ __forceinline__ u32x2 swz_rows4_v(const bf16_t* base, int row0, int c
   return ds_read_tr(base + swz_off<BV>(row0 + 4 * q + (s >> 2), col0 + 4 * (s & 3)));
 }
 
+// The state's row order: row r of state tile t is dk index
+//   32 (t / 2) + 8 (r / 4) + 4 (t % 2) + r % 4,
+// so that tiles 2 s2 and 2 s2 + 1 side by side are the 16x16x32 B operand over dk
+// 32 s2 .. 32 s2 + 31 in natural order.  kt_rows4* read, for the state update, the
+// A operand rows of tile t transposed out of a [token][dk] buffer: lane (q, r) gets
+// tokens row0 + 4q .. +3 of dk column (row r of tile t); source lane s of each
+// 16-lane group points at token row0 + 4q + s/4 and the 4 columns of row group s%4.
+__device__ __forceinline__ int kt_col(int t, int s) { return 32 * (t >> 1) + 4 * (t & 1) + 8 * (s & 3); }
+__device__ __forceinline__ u32x2 kt_rows4_swz(const bf16_t* base, int row0, int t) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  return ds_read_tr(base + swz_off<128>(row0 + 4 * q + (s >> 2), kt_col(t, s)));
+}
+__device__ __forceinline__ u32x2 kt_rows4(const bf16_t* base, int ld, int row0, int t) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  return ds_read_tr(base + (row0 + 4 * q + (s >> 2)) * ld + kt_col(t, s));
+}
+// dk index of element v of lane group q in state tile t
+__device__ __forceinline__ int state_row(int t, int q, int v) { return 32 * (t >> 1) + 8 * q + 4 * (t & 1) + v; }
+
+__device__ __forceinline__ u32x4 join(u32x2 a, u32x2 b) { return u32x4{a[0], a[1], b[0], b[1]}; }
+
+// base + off bytes; a uniform 64-bit base plus a 32-bit lane offset is one
+// scalar-base memory instruction with no per-lane 64-bit address arithmetic
+template <class T>
+__device__ __forceinline__ T* at_bytes(T* base, unsigned off) {
+  return (T*)((unsigned char*)base + off);
+}
+template <class T>
+__device__ __forceinline__ const T* at_bytes(const T* base, unsigned off) {
+  return (const T*)((const unsigned char*)base + off);
+}
+
+// Buffer resource over `bytes` bytes at p (raw, stride 0): stores through it take a
+// 32-bit lane offset and a uniform scalar offset, with no per-lane address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
+}
+
 // Issue the loads of one chunk straight into an LDS buffer (global_load_lds_dwordx4:
 // lane i of an instruction writes 16 bytes at the buffer offset + 16 i).  Per wave: 4
-// instructions of K rows, 4 of Q, 2 of V and 4 of the record, each covering 1 KiB of
-// the buffer.  Rows past the sequence end repeat the last valid row: every product
-// they enter is multiplied by their zero beta, so they need no clearing.
+// instructions of K rows, 4 of Q, 2 of V and up to 5 of the record, each covering
+// 1 KiB of the buffer.  Rows past the sequence end repeat the last valid row: every
+// product they enter is multiplied by their zero beta, so they need no clearing.
 // PART selects a part of the instructions (0: record, 1: v, 2: k, 3: q) or all (-1),
-// so that the issue can be spread over a chunk's phases.
+// so that the issue can be spread over a chunk's phases.  Addresses are a uniform
+// base plus a 32-bit lane byte offset (scalar-base loads).
 template <int DK, int MODE, int PART = -1>
 __device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0, int nvalid,
                                              const unsigned char* rec, int hk, int h, int col0,
                                              bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
   typedef __attribute__((address_space(3))) void lds_void;
   typedef __attribute__((address_space(1))) void glob_void;
-  const int l = lane_id(), w = threadIdx.x >> 6;
+  constexpr int NRP = rec_bytes(MODE) / 1024;  // 1 KiB record pieces
+  const int l = lane_id(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
   const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
   const bf16_t* vb = (const bf16_t*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
   if constexpr (PART == -1 || PART == 0) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int mi = 4 * w + m;
-      __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
-                                       (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+    for (int m = 0; m < (NRP + 3) / 4; ++m) {
+      const int mi = 4 * m + w;
+      if (mi < NRP)
+        __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
+                                         (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
     }
   }
   if constexpr (PART == -1 || PART == 1) {
@@ -190,10 +230,10 @@ __device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0,
     for (int m = 0; m < 2; ++m) {
       const int mi = 2 * w + m;               // rows 8 mi .. 8 mi + 7
       const int row = 8 * mi + (l >> 3);
-      const int rr = row < nvalid ? row : nvalid - 1;
+      const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
       const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
-      const unsigned vo = (unsigned)rr * (unsigned)p.vs_ld + 8u * g;
-      __builtin_amdgcn_global_load_lds((glob_void*)(vb + vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
+      const unsigned vo = 2u * (rr * (unsigned)p.vs_ld + 8u * g);
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
     }
   }
   if constexpr (PART == -1 || PART == 2 || PART == 3) {
@@ -201,15 +241,15 @@ __device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0,
     for (int m = 0; m < 4; ++m) {
       const int mi = 4 * w + m;               // rows 4 mi .. 4 mi + 3
       const int row = 4 * mi + (l >> 4);
-      const int rr = row < nvalid ? row : nvalid - 1;
+      const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
       const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));  // logical segment
       if constexpr (PART != 3) {
-        const unsigned ko = (unsigned)rr * (unsigned)p.ks_ld + 8u * g;
-        __builtin_amdgcn_global_load_lds((glob_void*)(kb + ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
+        const unsigned ko = 2u * (rr * (unsigned)p.ks_ld + 8u * g);
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(kb, ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
       }
       if constexpr (PART != 2) {
-        const unsigned qo = (unsigned)rr * (unsigned)p.qs_ld + 8u * g;
-        __builtin_amdgcn_global_load_lds((glob_void*)(qb + qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+        const unsigned qo = 2u * (rr * (unsigned)p.qs_ld + 8u * g);
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(qb, qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
       }
     }
   }
@@ -234,7 +274,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   __shared__ __align__(16) bf16_t sQ0[Q_::SZK], sQ1[DIRECT ? Q_::SZK : 8];
   __shared__ __align__(16) bf16_t sV0[Q_::SZV], sV1[DIRECT ? Q_::SZV : 8];
   __shared__ __align__(16) unsigned char sRec0[Q_::REC], sRec1[DIRECT ? Q_::REC : 16];
-  __shared__ __align__(16) bf16_t sWS[NWC * Q_::WS / 2];  // per-wave scratch
   constexpr int K_LO = C * LDK, V_LO = C * LDT;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -264,7 +303,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     return p.rec + ((size_t)ci * p.Hv + h) * Q_::REC;
   };
 
-  // state slice S[dk][16w + (0..15)] in MFMA C layout: S[t][v] = S[16t + 4lq + v][16w + lr]
+  // state slice S[dk][16w + (0..15)] in MFMA C layout, rows in the state's row order:
+  // S[t][v] = S[state_row(t, lq, v)][16w + lr]
   f32x4 S[DK / 16];
   const size_t state_off = ((size_t)n * p.Hv + h) * DK * DV + col0 + 16 * wave + lr;
   if (p.initial_state) {
@@ -272,21 +312,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        S[t][v] = p.initial_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV];
+        S[t][v] = p.initial_state[state_off + (size_t)state_row(t, lq, v) * DV];
   } else {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t) S[t] = zero4();
   }
 
-  bf16_t* wS = sWS + wave * (Q_::WS / 2);  // S^T [16][LDK] (hi, lo)
-  constexpr int WS_LO = 16 * LDK;
 
   // output addressing: row stride and the lane's constant offset within a chunk
   const int nparts = nb * NWC;                       // partial sums of o^2 per row (layer)
   const int o_rs = p.Hv * DV, s_rs = p.Hv * nparts;  // row strides of o and of the sums
   // unsigned: a uniform 64-bit base plus a zero-extended 32-bit lane offset is one
   // scalar-base memory instruction with no per-lane 64-bit address arithmetic
-  const unsigned o_lane = 4u * lq * o_rs + 16u * wave + lr, s_lane = 4u * lq * s_rs;
+  const unsigned o_elem = 4u * lq * o_rs + 16u * wave + lr;
+  const unsigned o_lane = 4u * o_elem, o_lane_h = 2u * o_elem;  // bytes: fp32 o, bf16 o
+  const unsigned s_lane = 16u * lq * s_rs;                      // bytes: fp32 sums
 
   Prefetch<DK, MODE> pf;
   if (nchunks > 0) {
@@ -386,14 +426,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
 
     // ------------------------------------------------------------ K S, Q S, right-hand side
-    // S^T goes to the wave's scratch as the B operand of K S and Q S.  Every operand
-    // that does not depend on S is read from LDS in one batch while it lands, so
-    // the products below run back to back on registers.
-#pragma unroll
-    for (int t = 0; t < DK / 16; ++t) {
-      if constexpr (IS) store_ct_split(wS, wS + WS_LO, LDK, 16 * t, 0, S[t]);
-      else store_ct_bf16(wS, LDK, 16 * t, 0, S[t]);
-    }
+    // The B operand of K S and Q S over dk block s2 is the state itself: lane (q, r)
+    // holds tiles 2 s2 and 2 s2 + 1, dk 32 s2 + 8q + (0..7) of column r (the state's
+    // row order), packed to bf16 straight from the accumulators.  Every operand that
+    // does not depend on S is read from LDS in one batch while the state update of
+    // the previous chunk drains.
     constexpr int NSK = DK / 32;
     u32x4 kh[4][NSK], kl[4][NSK], qh[4][NSK], ql[4][NSK];
 #pragma unroll
@@ -424,10 +461,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         vv[i][3] += __uint_as_float(vl[1] & 0xffff0000u);
       }
     }
-    wave_lds_fence();
     u32x4 sh[NSK], sl[NSK];
 #pragma unroll
-    for (int s2 = 0; s2 < NSK; ++s2) frag2<IS>(wS, WS_LO, LDK, 0, 32 * s2, sh[s2], sl[s2]);
+    for (int s2 = 0; s2 < NSK; ++s2) {
+      sh[s2] = join(pack_hi4(S[2 * s2]), pack_hi4(S[2 * s2 + 1]));
+      if constexpr (IS) sl[s2] = join(pack_lo4(S[2 * s2]), pack_lo4(S[2 * s2 + 1]));
+      else sl[s2] = sh[s2];
+    }
     f32x4 KS[4], QS[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -441,14 +481,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
         KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
         QS[i] = mm<IS, IS>(QS[i], qh[i][s2], ql[i][s2], sh[s2], sl[s2]);
       }
+    if constexpr (DIRECT && !IS) {
+      // all fragment reads go out back to back, then the state packs, then the
+      // products: one LDS round trip for the phase instead of one per few products
+      __builtin_amdgcn_sched_group_barrier(0x100, 8 * NSK + 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4 * NSK, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8 * NSK, 0);
+    }
     stage_next(std::integral_constant<int, 1>{});
-    // T fragments for V_new = T R (read while the products run)
-    u32x2 th[10], tl[10];
+    // T operands of V_new = T R, one per block pair (read while the products run)
+    u32x4 th[kNPairs], tl[kNPairs];
 #pragma unroll
-    for (int x = 0; x < 10; ++x) {
-      const unsigned char* tp = sRec + kRecT + 2 * x * kTileBytes + 8 * l;
-      th[x] = *(const u32x2*)tp;
-      tl[x] = *(const u32x2*)(tp + kTileBytes);
+    for (int x = 0; x < kNPairs; ++x) {
+      const unsigned char* tp = sRec + kRecT + 2 * x * kPairBytes + 16 * l;
+      th[x] = *(const u32x4*)tp;
+      tl[x] = *(const u32x4*)(tp + kPairBytes);
     }
     // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
     f32x4 R[4];
@@ -464,118 +511,159 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     }
 
     // ------------------------------------------------------------ V_new = T R
-    // A C-layout tile (lane (q, r) holds rows 4q..4q+3 of column r) is exactly the
-    // B operand layout of the 16x16x16 MFMA, so R feeds the products from
-    // registers; T comes as ready A-operand fragments.  The hi*hi, hi*lo and
-    // lo*hi parts accumulate separately: twelve independent chains.
-    u32x2 Rh[4], Rl[4];
+    // Two C-layout tiles of R (token blocks 2p, 2p+1) side by side are the B operand
+    // of a 16x16x32 MFMA over that block pair, in the contraction order of the
+    // record's T pairs.  hi*hi, hi*lo and lo*hi accumulate in one chain per row block.
+    u32x4 Rh[2], Rl[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      Rh[i] = pack_hi4(R[i]);
-      Rl[i] = pack_lo4(R[i]);
+    for (int pp = 0; pp < 2; ++pp) {
+      Rh[pp] = join(pack_hi4(R[2 * pp]), pack_hi4(R[2 * pp + 1]));
+      Rl[pp] = join(pack_lo4(R[2 * pp]), pack_lo4(R[2 * pp + 1]));
     }
     f32x4 U[4];
-    u32x2 Uh[4], Ul[4];  // bf16 hi/lo of V_new blocks as B operands
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 a0 = zero4(), a1 = zero4(), a2 = zero4();
+      f32x4 a = zero4();
 #pragma unroll
-      for (int kb = 0; kb <= i; ++kb) {
-        const int x = tile_index(i, kb);
-        a0 = mma16k16(th[x], Rh[kb], a0);
-        a1 = mma16k16(th[x], Rl[kb], a1);
-        a2 = mma16k16(tl[x], Rh[kb], a2);
+      for (int pp = 0; pp <= i / 2; ++pp) {
+        const int x = pair_index(i, pp);
+        a = mma16(th[x], Rh[pp], a);
+        a = mma16(th[x], Rl[pp], a);
+        a = mma16(tl[x], Rh[pp], a);
       }
-      U[i] = a0 + a1 + a2;
-      Uh[i] = pack_hi4(U[i]);
-      Ul[i] = pack_lo4(U[i]);
+      U[i] = a;
+    }
+    if constexpr (DIRECT && !IS) {
+      // the T operands and gate rows are read in one batch ahead of the products
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kNPairs + 8, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 80, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 18, 1);
+    }
+    u32x4 Uh[2], Ul[2];  // bf16 hi/lo of V_new block pairs as B operands
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      Uh[pp] = join(pack_hi4(U[2 * pp]), pack_hi4(U[2 * pp + 1]));
+      if constexpr (OS) Ul[pp] = join(pack_lo4(U[2 * pp]), pack_lo4(U[2 * pp + 1]));
     }
     stage_next(std::integral_constant<int, 2>{});
-    // P fragments and the K^T fragments of the state update (read while V_new forms)
-    u32x2 ph[10], pl[10];
+    // P operands and the K^T operands of the state update (read while V_new forms)
+    u32x4 ph[kNPairs], pl[kNPairs];
 #pragma unroll
-    for (int x = 0; x < 10; ++x) {
-      ph[x] = *(const u32x2*)(sRec + kRecP + x * kTileBytes + 8 * l);
-      if constexpr (OS) pl[x] = *(const u32x2*)(sRec + kRecPL + x * kTileBytes + 8 * l);
+    for (int x = 0; x < kNPairs; ++x) {
+      ph[x] = *(const u32x4*)(sRec + kRecP + x * kPairBytes + 16 * l);
+      if constexpr (OS) pl[x] = *(const u32x4*)(sRec + kRecPL + x * kPairBytes + 16 * l);
       else pl[x] = ph[x];
     }
-    // K^T blocks of the state update as 16x16x16 A operands: lane (q, r) holds
-    // K[16kb + 4q .. +3][16t + r], four token rows of one dk column
-    u32x2 kth[DK / 16][4], ktl[DK / 16][4];
+    // K^T operands of the state update, 16x32 over token blocks 2p, 2p+1: lane (q, r)
+    // holds K[32p + 4q .. +3][d] then K[32p + 16 + 4q .. +3][d] for the dk index d of
+    // row r of state tile t (dk 32 (t/2) + 8 (r/4) + 4 (t%2) + r%4)
+    u32x4 kth[DK / 16][2], ktl[DK / 16][2];
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        kth[t][kb] = DIRECT ? swz_rows4_k(sK, 16 * kb, 16 * t) : rows4_tr(sK, LDK, 16 * kb, 16 * t);
-        ktl[t][kb] = IS ? rows4_tr(sK + K_LO, LDK, 16 * kb, 16 * t) : kth[t][kb];
+      for (int pp = 0; pp < 2; ++pp) {
+        if constexpr (DIRECT) {
+          kth[t][pp] = join(kt_rows4_swz(sK, 32 * pp, t), kt_rows4_swz(sK, 32 * pp + 16, t));
+          ktl[t][pp] = kth[t][pp];
+        } else {
+          kth[t][pp] = join(kt_rows4(sK, LDK, 32 * pp, t), kt_rows4(sK, LDK, 32 * pp + 16, t));
+          if constexpr (IS)
+            ktl[t][pp] = join(kt_rows4(sK + K_LO, LDK, 32 * pp, t), kt_rows4(sK + K_LO, LDK, 32 * pp + 16, t));
+          else ktl[t][pp] = kth[t][pp];
+        }
       }
-    // Vt = diag(e^{G_last - G}) V_new: its C-layout blocks are the 16x16x16 B operands of
-    // the state update, so it stays in registers (hi and lo)
-    u32x2 vth[4], vtl[4];
+    // Vt = diag(e^{G_last - G}) V_new: its C-layout tiles side by side are the B
+    // operands of the state update, so it stays in registers (hi and lo)
+    u32x4 vth[2], vtl[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 vt;
-      const float4 el = *(const float4*)(sEL + 16 * i + 4 * lq);
-      vt[0] = U[i][0] * el.x; vt[1] = U[i][1] * el.y; vt[2] = U[i][2] * el.z; vt[3] = U[i][3] * el.w;
-      vth[i] = pack_hi4(vt);
-      vtl[i] = pack_lo4(vt);
+    for (int pp = 0; pp < 2; ++pp) {
+      f32x4 vt[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int i = 2 * pp + hh;
+        const float4 el = *(const float4*)(sEL + 16 * i + 4 * lq);
+        vt[hh][0] = U[i][0] * el.x; vt[hh][1] = U[i][1] * el.y;
+        vt[hh][2] = U[i][2] * el.z; vt[hh][3] = U[i][3] * el.w;
+      }
+      vth[pp] = join(pack_hi4(vt[0]), pack_hi4(vt[1]));
+      vtl[pp] = join(pack_lo4(vt[0]), pack_lo4(vt[1]));
     }
 
     // ------------------------------------------------------------ O = scale e^G (Q S) + P V_new
+    f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 o;
       const float4 eg = *(const float4*)(sEG + 16 * i + 4 * lq);
-      o[0] = p.scale * eg.x * QS[i][0]; o[1] = p.scale * eg.y * QS[i][1];
-      o[2] = p.scale * eg.z * QS[i][2]; o[3] = p.scale * eg.w * QS[i][3];
+      o[i][0] = p.scale * eg.x * QS[i][0]; o[i][1] = p.scale * eg.y * QS[i][1];
+      o[i][2] = p.scale * eg.z * QS[i][2]; o[i][3] = p.scale * eg.w * QS[i][3];
 #pragma unroll
-      for (int jb = 0; jb <= i; ++jb) {  // P is lower triangular
-        const int x = tile_index(i, jb);
-        o = mma16k16(ph[x], Uh[jb], o);
+      for (int pp = 0; pp <= i / 2; ++pp) {  // P is lower triangular
+        const int x = pair_index(i, pp);
+        o[i] = mma16(ph[x], Uh[pp], o[i]);
         if constexpr (OS) {
-          o = mma16k16(ph[x], Ul[jb], o);
-          o = mma16k16(pl[x], Uh[jb], o);
-        }
-      }
-      // row 16i + 4lq + v of the chunk: chunk base + (16i + v) rows (uniform) + the
-      // lane's constant offset
-      if constexpr (MODE != MODE_LAYER) {
-        float* ochunk = p.o + (t0 * p.Hv + h) * (long long)DV + col0;
-        if (nvalid == C) {  // uniform: every row of a full chunk is stored
-#pragma unroll
-          for (int v = 0; v < 4; ++v) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = o[v];
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (16 * i + 4 * lq + v < nvalid) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = o[v];
-        }
-      } else {
-        // unnormalised o in bf16 and this wave's share of sum(o^2) over its 16
-        // columns; the epilogue kernel adds the shares and applies the norm
-        bf16_t* ochunk = (bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0;
-        float* schunk = p.ss_part + (t0 * p.Hv + h) * (long long)nparts + blk * NWC + wave;
-        float ss[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) ss[v] = group_sum_dpp<16>(o[v] * o[v]);
-        if (nvalid == C) {  // uniform: every row of a full chunk is stored
-#pragma unroll
-          for (int v = 0; v < 4; ++v) (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
-          if (lr == 0) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss[v];
-          }
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            if (16 * i + 4 * lq + v < nvalid) {
-              (ochunk + (long long)(16 * i + v) * o_rs)[o_lane] = f2bf(o[v]);
-              if (lr == 0) (schunk + (long long)(16 * i + v) * s_rs)[s_lane] = ss[v];
-            }
-          }
+          o[i] = mma16(ph[x], Ul[pp], o[i]);
+          o[i] = mma16(pl[x], Uh[pp], o[i]);
         }
       }
     }
-
+    // row 16i + 4lq + v of the chunk: the chunk's rows 16i + v (a uniform offset) plus
+    // the lane's constant byte offset; every row of a full chunk is stored (uniform)
+    if constexpr (MODE != MODE_LAYER) {
+      const auto ob = buf_rsrc(p.o + (t0 * p.Hv + h) * (long long)DV + col0, 4u * C * o_rs);
+      auto store = [&](int i, int v) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[i][v]), ob, o_lane, 4 * (16 * i + v) * o_rs, 0);
+      };
+      if (nvalid == C) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) store(i, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (16 * i + 4 * lq + v < nvalid) store(i, v);
+      }
+    } else {
+      // unnormalised o in bf16 and this wave's share of sum(o^2) over its 16 columns;
+      // the epilogue kernel adds the shares and applies the norm
+      const auto ob = buf_rsrc((bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0, 2u * C * o_rs);
+      const auto sb = buf_rsrc(p.ss_part + (t0 * p.Hv + h) * (long long)nparts + blk * NWC + wave,
+                               4u * C * s_rs);
+      float ss[4][4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ss[i][v] = group_sum_dpp<16>(o[i][v] * o[i][v]);
+      auto store = [&](int i, int v) {
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(o[i][v]), ob, o_lane_h, 2 * (16 * i + v) * o_rs, 0);
+      };
+      auto store_ss = [&](int i, int v) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ss[i][v]), sb, s_lane, 4 * (16 * i + v) * s_rs, 0);
+      };
+      if (nvalid == C) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) store(i, v);
+        if (lr == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) store_ss(i, v);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (16 * i + 4 * lq + v < nvalid) {
+              store(i, v);
+              if (lr == 0) store_ss(i, v);
+            }
+      }
+    }
 
     stage_next(std::integral_constant<int, 3>{});
 
@@ -586,10 +674,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 #pragma unroll
       for (int v = 0; v < 4; ++v) S[t][v] *= gl;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        S[t] = mma16k16(kth[t][kb], vth[kb], S[t]);
-        S[t] = mma16k16(kth[t][kb], vtl[kb], S[t]);
-        if constexpr (IS) S[t] = mma16k16(ktl[t][kb], vth[kb], S[t]);
+      for (int pp = 0; pp < 2; ++pp) {
+        S[t] = mma16(kth[t][pp], vth[pp], S[t]);
+        S[t] = mma16(kth[t][pp], vtl[pp], S[t]);
+        if constexpr (IS) S[t] = mma16(ktl[t][pp], vth[pp], S[t]);
       }
     }
   };
@@ -608,7 +696,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
-        p.final_state[state_off + (size_t)(16 * t + 4 * lq + v) * DV] = S[t][v];
+        p.final_state[state_off + (size_t)state_row(t, lq, v) * DV] = S[t][v];
   }
 
   if constexpr (MODE == MODE_LAYER) {

@@ -89,8 +89,9 @@ __device__ __forceinline__ f32x4 blk_mul_c(const Blk& x, const Blk& y) {
   return mm3k16(zero4(), x.ah, x.al, y.ch, y.cl);
 }
 
+// one 16x16 tile's A fragment into its half of a record pair (16 bytes per lane)
 __device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
-  *(u32x2*)(rec + off + lane_id() * 8) = f;
+  *(u32x2*)(rec + off + lane_id() * 16) = f;
 }
 
 // conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243:
@@ -538,9 +539,16 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             const u32x2 th = pack_hi4(Ta), tl = pack_lo4(Ta);
             sTd[(2 * bi) * 64 + l] = th;  // A fragments of T_ww for the other waves
             sTd[(2 * bi + 1) * 64 + l] = tl;
-            const int tw = kRecT + 2 * tile_index(bi, bi) * kTileBytes;
-            put_tile(rec, tw, th);
-            put_tile(rec, tw + kTileBytes, tl);
+            put_tile(rec, rec_t_off(bi, bi), th);
+            put_tile(rec, rec_t_off(bi, bi) + kPairBytes, tl);
+            if ((bi & 1) == 0) {
+              // the zero upper tile (bi, bi + 1) that completes row block bi's last pair
+              const u32x2 z = {0u, 0u};
+              put_tile(rec, rec_t_off(bi, bi + 1), z);
+              put_tile(rec, rec_t_off(bi, bi + 1) + kPairBytes, z);
+              put_tile(rec, rec_p_off(bi, bi + 1), z);
+              if constexpr (IS) put_tile(rec, rec_p_off(bi, bi + 1) + (kRecPL - kRecP), z);
+            }
           } else {
             u32x2* d = sLf + 2 * 64 * tile_index(bi, bj) + l;
             d[0] = pack_hi4(val);
@@ -553,9 +561,8 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             const int m = 16 * bj + 4 * lq + v;
             val[v] = sc * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i >= m);
           }
-          const int tix = tile_index(bi, bj);
-          put_tile(rec, kRecP + tix * kTileBytes, pack_hi4(val));
-          if constexpr (IS) put_tile(rec, kRecPL + tix * kTileBytes, pack_lo4(val));
+          put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
+          if constexpr (IS) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
         }
       }
       __syncthreads();  // L blocks and the diagonal inverses of all waves are in LDS
@@ -590,9 +597,8 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           const f32x4 TijT = mm3k16(zero4(), xh, xl, th, tl);
           Th[i] = pack_hi4(Tij);
           Tl[i] = pack_lo4(Tij);
-          const int off = kRecT + 2 * tile_index(i, j) * kTileBytes;
-          put_tile(rec, off, pack_hi4(TijT));
-          put_tile(rec, off + kTileBytes, pack_lo4(TijT));
+          put_tile(rec, rec_t_off(i, j), pack_hi4(TijT));
+          put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(TijT));
         }
       }
       __syncthreads();  // sLf / sTd are rewritten for the next value head

@@ -96,11 +96,11 @@ def _ws_size(B=2, T=100, Hk=2, Hv=4, dk=128, dv=128, N=2, dt=_lib.BF16):
 
 
 def test_chunk_workspace_size_covers_records_and_normalised_qk():
-    # records: (ceil(B*T/64) + N) slots x Hv x 16 KiB (bf16) or 21 KiB (fp32), plus q/k
+    # records: (ceil(B*T/64) + N) slots x Hv x 19 KiB (bf16) or 25 KiB (fp32), plus q/k
     bf, f32 = _ws_size(dt=_lib.BF16), _ws_size(dt=_lib.F32)
     slots = (2 * 100 + 63) // 64 + 2
-    assert bf >= slots * 4 * 16384 + 2 * 200 * 2 * 128 * 2
-    assert f32 >= slots * 4 * 21504 + 2 * 200 * 2 * 128 * 4
+    assert bf >= slots * 4 * 19456 + 2 * 200 * 2 * 128 * 2
+    assert f32 >= slots * 4 * 25600 + 2 * 200 * 2 * 128 * 4
     assert f32 > bf
     assert _ws_size(T=1000) > _ws_size(T=100)
     prefill = _lib.lib().omx_gdn_prefill_workspace_size(2, 100, 2, 4, 128, 128, 2)
