@@ -15,9 +15,14 @@
 // 64-column block of dv) walks that sequence's chunks in order.  Wavefront w
 // owns state columns [16w, 16w+16) of the block: its fp32 slice S[dk][16] stays
 // in MFMA accumulator registers for the whole sequence, and every product that
-// touches it runs on that wavefront alone, between two workgroup barriers per
-// chunk that guard the shared staging arrays.  The next chunk's K, Q, V rows and
-// record are loaded into registers while the current chunk computes.
+// touches it runs on that wavefront alone.  All products are 16x16x32 MFMAs: the
+// state's rows are kept in an order (state_row) in which two accumulator tiles
+// side by side are the B operand of K S and Q S, and T, P arrive from the record
+// as 16x32 operands over pairs of 16-token blocks whose contraction order matches
+// two C-layout tiles of R or V_new side by side.  With bf16 inputs and dk = 128
+// the next chunk's K, Q, V rows and record are loaded straight into the other of
+// two LDS buffers while the current chunk computes (one workgroup barrier per
+// chunk); otherwise they are staged through registers.
 //
 // Precision.  MFMA inputs are bf16 with fp32 accumulation.  K, Q, V are bf16 on
 // the bf16 and layer paths (exact), or fp32 split into hi+lo bf16 pairs
@@ -63,6 +68,10 @@ struct Cfg {
   // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
   // into padded rows.
   static constexpr bool DIRECT = MODE != MODE_F32 && DK == 128;
+  // with direct loads a fifth wavefront issues them (it shares a SIMD with one of the
+  // four compute wavefronts, so each may hold at most half the register file)
+  static constexpr int NTH = DIRECT ? NT + 64 : NT;
+  static constexpr int WPE = DIRECT ? 2 : 1;
   static constexpr int NBUF = DIRECT ? 2 : 1;
   static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
   static constexpr int SZV = DIRECT ? C * BV : NS * C * LDT;  // elements of a V buffer
@@ -197,68 +206,91 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(void* p, unsigned byt
   return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
 }
 
-// Issue the loads of one chunk straight into an LDS buffer (global_load_lds_dwordx4:
-// lane i of an instruction writes 16 bytes at the buffer offset + 16 i).  Per wave: 4
-// instructions of K rows, 4 of Q, 2 of V and up to 5 of the record, each covering
-// 1 KiB of the buffer.  Rows past the sequence end repeat the last valid row: every
-// product they enter is multiplied by their zero beta, so they need no clearing.
-// PART selects a part of the instructions (0: record, 1: v, 2: k, 3: q) or all (-1),
-// so that the issue can be spread over a chunk's phases.  Addresses are a uniform
-// base plus a 32-bit lane byte offset (scalar-base loads).
-template <int DK, int MODE, int PART = -1>
-__device__ __forceinline__ void stage_direct(const ChunkParams& p, long long t0, int nvalid,
-                                             const unsigned char* rec, int hk, int h, int col0,
-                                             bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
-  typedef __attribute__((address_space(3))) void lds_void;
+// Issue one chunk's loads straight into an LDS buffer (global_load_lds_dwordx4: lane i
+// of an instruction writes 16 bytes at the buffer offset + 16 i), all from the loader
+// wavefront: 16 instructions each of K and Q rows, 8 of V rows and one per KiB of the
+// record.  Rows past the sequence end repeat the last valid row: every product they
+// enter is multiplied by their zero beta, so they need no clearing.  Addresses are a
+// uniform base plus a 32-bit lane byte offset (scalar-base loads).
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) bf16_t lds_bf16;
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
+
+// The buffers are passed as LDS-space pointers (cast where the __shared__ arrays are
+// named), so no generic-to-LDS conversion happens here.
+template <int DK, int MODE>
+__device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, int nvalid,
+                                          const unsigned char* rec, int hk, int h, int col0,
+                                          lds_bf16* sK, lds_bf16* sQ, lds_bf16* sV, lds_u8* sRec) {
   typedef __attribute__((address_space(1))) void glob_void;
-  constexpr int NRP = rec_bytes(MODE) / 1024;  // 1 KiB record pieces
-  const int l = lane_id(), w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int NRP = rec_bytes(MODE) / 1024;
+  const int l = lane_id();
   const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
   const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
   const bf16_t* vb = (const bf16_t*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
-  if constexpr (PART == -1 || PART == 0) {
+  const unsigned kld = (unsigned)p.ks_ld, qld = (unsigned)p.qs_ld, vld = (unsigned)p.vs_ld;
+  if (nvalid == C) {
+    // K/Q instruction mi covers rows 4 mi + l/16, whose swizzle repeats every 4
+    // instructions, and V instruction mi rows 8 mi + l/8, whose swizzle does not depend
+    // on mi: a few lane offsets plus uniform row steps
 #pragma unroll
-    for (int m = 0; m < (NRP + 3) / 4; ++m) {
-      const int mi = 4 * m + w;
-      if (mi < NRP)
-        __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
-                                         (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+    for (int m0 = 0; m0 < 4; ++m0) {
+      const unsigned row = 4u * m0 + (unsigned)(l >> 4);
+      const unsigned g = (unsigned)((l & 15) ^ swz_k((int)row));
+      const unsigned ko = 2u * (row * kld + 8u * g), qo = 2u * (row * qld + 8u * g);
+#pragma unroll
+      for (int mi = m0; mi < 16; mi += 4) {
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(kb + (long long)(4 * (mi - m0)) * p.ks_ld, ko),
+                                         (lds_void*)(sK + 512 * mi), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(qb + (long long)(4 * (mi - m0)) * p.qs_ld, qo),
+                                         (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+      }
     }
-  }
-  if constexpr (PART == -1 || PART == 1) {
+    const unsigned vrow = (unsigned)(l >> 3);
+    const unsigned vo = 2u * (vrow * vld + 8u * (unsigned)((l & 7) ^ swz_v((int)vrow)));
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int mi = 2 * w + m;               // rows 8 mi .. 8 mi + 7
+    for (int mi = 0; mi < 8; ++mi)
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb + (long long)(8 * mi) * p.vs_ld, vo),
+                                       (lds_void*)(sV + 512 * mi), 16, 0, 0);
+  } else {
+    // a sequence's last, partial chunk: rows past its end repeat the last valid row
+#pragma unroll
+    for (int mi = 0; mi < 16; ++mi) {
+      const int row = 4 * mi + (l >> 4);
+      const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
+      const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(kb, 2u * (rr * kld + 8u * g)),
+                                       (lds_void*)(sK + 512 * mi), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(qb, 2u * (rr * qld + 8u * g)),
+                                       (lds_void*)(sQ + 512 * mi), 16, 0, 0);
+    }
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
       const int row = 8 * mi + (l >> 3);
       const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
       const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
-      const unsigned vo = 2u * (rr * (unsigned)p.vs_ld + 8u * g);
-      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, vo), (lds_void*)(sV + 512 * mi), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, 2u * (rr * vld + 8u * g)),
+                                       (lds_void*)(sV + 512 * mi), 16, 0, 0);
     }
   }
-  if constexpr (PART == -1 || PART == 2 || PART == 3) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int mi = 4 * w + m;               // rows 4 mi .. 4 mi + 3
-      const int row = 4 * mi + (l >> 4);
-      const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
-      const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));  // logical segment
-      if constexpr (PART != 3) {
-        const unsigned ko = 2u * (rr * (unsigned)p.ks_ld + 8u * g);
-        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(kb, ko), (lds_void*)(sK + 512 * mi), 16, 0, 0);
-      }
-      if constexpr (PART != 2) {
-        const unsigned qo = 2u * (rr * (unsigned)p.qs_ld + 8u * g);
-        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(qb, qo), (lds_void*)(sQ + 512 * mi), 16, 0, 0);
-      }
-    }
-  }
+  for (int mi = 0; mi < NRP; ++mi)
+    __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
+                                     (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+}
+
+// Workgroup barrier ordering LDS accesses only (no wait for outstanding global stores).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 template <int DK, int MODE>
-// One workgroup per CU is the design point (the state fills the register file), so the
-// compiler may use the whole file instead of holding back for a second workgroup.
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void scan_kernel(ChunkParams p) {
+// One workgroup per CU is the design point (the state fills the register file): the
+// compiler may use the whole file (half of it with a loader wavefront, which shares a
+// SIMD) instead of holding back for a second workgroup.
+__global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE>::WPE, Cfg<DK, MODE>::WPE))) void scan_kernel(ChunkParams p) {
   using Q_ = Cfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
@@ -278,6 +310,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = DIRECT && wave == NWC;  // issues the direct loads, computes nothing
   // XCD-aware numbering: workgroups are dealt round-robin over the 8 XCDs
   // (blockIdx % 8); renumber so that consecutive work items -- the gqa x nb
   // workgroups reading the same key head's q/k -- run on one XCD and share its L2.
@@ -307,7 +340,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   // S[t][v] = S[state_row(t, lq, v)][16w + lr]
   f32x4 S[DK / 16];
   const size_t state_off = ((size_t)n * p.Hv + h) * DK * DV + col0 + 16 * wave + lr;
-  if (p.initial_state) {
+  if (p.initial_state && !loader) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
@@ -331,38 +364,30 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   Prefetch<DK, MODE> pf;
   if (nchunks > 0) {
     const int nv0 = (int)((s1 - s0) < C ? (s1 - s0) : C);
-    if constexpr (DIRECT) stage_direct<DK, MODE>(p, s0, nv0, rec_of(0), hk, h, col0, sK0, sQ0, sV0, sRec0);
-    else prefetch<DK, MODE>(p, pf, s0, nv0, rec_of(0), hk, h, col0);
+    if constexpr (DIRECT) {
+      if (loader) {
+        stage_all<DK, MODE>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
+                            (lds_bf16*)sV0, (lds_u8*)sRec0);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the first barrier
+      }
+    } else {
+      prefetch<DK, MODE>(p, pf, s0, nv0, rec_of(0), hk, h, col0);
+    }
   }
 
-  // one chunk: reads buffer (sK, sQ, sV, sRec); with direct loads, issues chunk j+1's
-  // loads into buffer (nK, nQ, nV, nRec)
-  auto run_chunk = [&](const int j, bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec,
-                       bf16_t* nK, bf16_t* nQ, bf16_t* nV, unsigned char* nRec) {
+  // one chunk on the compute wavefronts, from buffer (sK, sQ, sV, sRec)
+  auto run_chunk = [&](const int j, bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
-    // the next chunk's loads go out in four parts spread over this chunk's phases, so
-    // the four wavefronts do not queue all their loads at once
-    const bool more = DIRECT && j + 1 < nchunks;
-    const long long tn = t0 + C;
-    const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
-    const unsigned char* recn = rec_of(more ? j + 1 : j);
-    auto stage_next = [&](auto part) {
-      if constexpr (DIRECT)
-        if (more)
-          stage_direct<DK, MODE, decltype(part)::value>(p, tn, nvn, recn, hk, h, col0, nK, nQ, nV, nRec);
-    };
     const float* sGate = (const float*)(sRec + kRecG);
     const float* sBeta = sGate + kGateBeta * C;  // beta
     const float* sBE = sGate + kGateBE * C;      // beta e^G
     const float* sEG = sGate + kGateEG * C;      // e^G
     const float* sEL = sGate + kGateEL * C;      // e^{G_last - G}
     if constexpr (DIRECT) {
-      // this wave's loads of chunk j have landed; after the barrier every wave's have,
-      // and chunk j-1, the last reader of the other buffer, is finished everywhere
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      __syncthreads();
-      stage_next(std::integral_constant<int, 0>{});
+      // the loader's loads of chunk j have landed (it waited before arriving), and
+      // chunk j-1, the last reader of the other buffer, is finished everywhere
+      lds_barrier();
     } else {
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
@@ -488,7 +513,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       __builtin_amdgcn_sched_group_barrier(0x002, 4 * NSK, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8 * NSK, 0);
     }
-    stage_next(std::integral_constant<int, 1>{});
     // T operands of V_new = T R, one per block pair (read while the products run)
     u32x4 th[kNPairs], tl[kNPairs];
 #pragma unroll
@@ -545,7 +569,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       Uh[pp] = join(pack_hi4(U[2 * pp]), pack_hi4(U[2 * pp + 1]));
       if constexpr (OS) Ul[pp] = join(pack_lo4(U[2 * pp]), pack_lo4(U[2 * pp + 1]));
     }
-    stage_next(std::integral_constant<int, 2>{});
     // P operands and the K^T operands of the state update (read while V_new forms)
     u32x4 ph[kNPairs], pl[kNPairs];
 #pragma unroll
@@ -665,7 +688,6 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       }
     }
 
-    stage_next(std::integral_constant<int, 3>{});
 
     // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
     const float gl = sEG[C - 1];
@@ -683,15 +705,33 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
   };
 
   if constexpr (DIRECT) {
-    for (int j = 0; j < nchunks; j += 2) {
-      run_chunk(j, sK0, sQ0, sV0, sRec0, sK1, sQ1, sV1, sRec1);
-      if (j + 1 < nchunks) run_chunk(j + 1, sK1, sQ1, sV1, sRec1, sK0, sQ0, sV0, sRec0);
+    if (loader) {
+      // one barrier per chunk, as the compute wavefronts: after the barrier at the top of
+      // chunk j, buffer (j + 1) % 2 is free and receives chunk j + 1
+      auto load = [&](int j, lds_bf16* nK, lds_bf16* nQ, lds_bf16* nV, lds_u8* nRec) {
+        lds_barrier();
+        if (j + 1 < nchunks) {
+          const long long tn = s0 + (long long)(j + 1) * C;
+          const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
+          stage_all<DK, MODE>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the next barrier
+      };
+      for (int j = 0; j < nchunks; j += 2) {
+        load(j, (lds_bf16*)sK1, (lds_bf16*)sQ1, (lds_bf16*)sV1, (lds_u8*)sRec1);
+        if (j + 1 < nchunks) load(j + 1, (lds_bf16*)sK0, (lds_bf16*)sQ0, (lds_bf16*)sV0, (lds_u8*)sRec0);
+      }
+    } else {
+      for (int j = 0; j < nchunks; j += 2) {
+        run_chunk(j, sK0, sQ0, sV0, sRec0);
+        if (j + 1 < nchunks) run_chunk(j + 1, sK1, sQ1, sV1, sRec1);
+      }
     }
   } else {
-    for (int j = 0; j < nchunks; ++j) run_chunk(j, sK0, sQ0, sV0, sRec0, sK0, sQ0, sV0, sRec0);
+    for (int j = 0; j < nchunks; ++j) run_chunk(j, sK0, sQ0, sV0, sRec0);
   }
 
-  if (p.final_state) {
+  if (p.final_state && !loader) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
@@ -706,7 +746,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       const int K = p.conv_k;
       const bool own_qk = (h % gqa) == 0 && blk == 0;
       constexpr int HW = 2 * DK + BV;  // q | k | this block's v channels
-      for (int it = tid; it < HW * (K - 1); it += NT) {
+      for (int it = tid; it < HW * (K - 1); it += Q_::NTH) {
         const int ci = it / (K - 1), jj = it % (K - 1);
         if (ci < 2 * DK && !own_qk) continue;
         int ch;
@@ -730,7 +770,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(1, 1))) void
 template <int DK, int MODE>
 hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
   const unsigned grid = (unsigned)(p.N * p.Hv * p.nb);
-  hipLaunchKernelGGL((scan_kernel<DK, MODE>), dim3(grid), dim3(NT), 0, stream, p);
+  hipLaunchKernelGGL((scan_kernel<DK, MODE>), dim3(grid), dim3(Cfg<DK, MODE>::NTH), 0, stream, p);
   return hipGetLastError();
 }
 
