@@ -3,11 +3,11 @@
 //
 // The preparation kernel writes, for every (chunk, value head), a record that
 // the scan reads back in one piece:
-//   T = (I + L)^-1, the inverse of the chunk's unit lower-triangular system
-//       (deltanet.py:100-113), as bf16 hi + lo MFMA A-operand fragments;
+//   T diag(beta), with T = (I + L)^-1 the inverse of the chunk's unit lower-triangular
+//       system (deltanet.py:100-113), as bf16 hi + lo MFMA A-operand fragments;
 //   P = lower(scale (q_i . k_j) e^{G_i - G_j}) (deltanet.py:130-131), bf16 (hi + lo
 //       for fp32 inputs), as A-operand fragments;
-//   the gate vectors beta, beta e^G, e^G and e^{G_last - G} (fp32).
+//   the gate vectors e^G, scale e^G, e^{G_last - G} and beta (fp32).
 // The 64x64 lower-triangular T and P are stored as 16x32 A operands of the
 // 16x16x32 MFMA whose contraction runs over two 16-token blocks 2p, 2p+1: for
 // row block i and block pair p <= i/2, lane (q, r) = (lane / 16, lane % 16)
@@ -39,7 +39,9 @@ constexpr int kRecG = kRecP + kNPairs * kPairBytes;      // 4 x 64 fp32 gate vec
 constexpr int kRecPL = kRecG + 4 * kC * 4;               // fp32 inputs: P lo parts
 constexpr int kRecBytesBF16 = kRecPL;                    // 19456
 constexpr int kRecBytesF32 = kRecPL + kNPairs * kPairBytes;  // 25600
-constexpr int kGateBeta = 0, kGateBE = 1, kGateEG = 2, kGateEL = 3;  // rows of the gate block
+// rows of the gate block: e^G, scale e^G, e^{G_last - G} (its last entry, always 1, is
+// replaced by e^{G_last}), beta
+constexpr int kGateEG = 0, kGateEGS = 1, kGateEL = 2, kGateBeta = 3;
 
 __host__ __device__ constexpr int rec_bytes(int mode) {
   return mode == MODE_F32 ? kRecBytesF32 : kRecBytesBF16;

@@ -6,8 +6,8 @@
 // chunks beforehand by the preparation kernel (gdn_prep.hip), which leaves a
 // record per (chunk, value head).  This kernel carries the state S across a
 // sequence's chunks:
-//     R     = diag(beta) V - diag(beta e^G) (K S)
-//     V_new = T R                  (= U - W S of deltanet.py:115-116, 133-134)
+//     R     = V - diag(e^G) (K S)
+//     V_new = T diag(beta) R       (= U - W S of deltanet.py:115-116, 133-134)
 //     O     = scale e^G (Q S) + P V_new                        (:130-137)
 //     S    <- e^{G_last} S + K^T diag(e^{G_last - G}) V_new    (:139-142)
 //
@@ -380,10 +380,9 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
     const float* sGate = (const float*)(sRec + kRecG);
-    const float* sBeta = sGate + kGateBeta * C;  // beta
-    const float* sBE = sGate + kGateBE * C;      // beta e^G
-    const float* sEG = sGate + kGateEG * C;      // e^G
-    const float* sEL = sGate + kGateEL * C;      // e^{G_last - G}
+    const float* sEG = sGate + kGateEG * C;    // e^G
+    const float* sEGS = sGate + kGateEGS * C;  // scale e^G
+    const float* sEL = sGate + kGateEL * C;    // e^{G_last - G}; e^{G_last} at C - 1
     if constexpr (DIRECT) {
       // the loader's loads of chunk j have landed (it waited before arriving), and
       // chunk j-1, the last reader of the other buffer, is finished everywhere
@@ -521,20 +520,19 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
       th[x] = *(const u32x4*)tp;
       tl[x] = *(const u32x4*)(tp + kPairBytes);
     }
-    // R = diag(beta) V - diag(beta e^G) K S at rows 16i + 4lq + v, column 16w + lr
+    // R = V - diag(e^G) K S at rows 16i + 4lq + v, column 16w + lr (diag(beta) is
+    // folded into the record's T)
     f32x4 R[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r0 = 16 * i + 4 * lq;
-      const float4 bt = *(const float4*)(sBeta + r0);
-      const float4 be = *(const float4*)(sBE + r0);
-      R[i][0] = bt.x * vv[i][0] - be.x * KS[i][0];
-      R[i][1] = bt.y * vv[i][1] - be.y * KS[i][1];
-      R[i][2] = bt.z * vv[i][2] - be.z * KS[i][2];
-      R[i][3] = bt.w * vv[i][3] - be.w * KS[i][3];
+      const float4 eg = *(const float4*)(sEG + 16 * i + 4 * lq);
+      R[i][0] = vv[i][0] - eg.x * KS[i][0];
+      R[i][1] = vv[i][1] - eg.y * KS[i][1];
+      R[i][2] = vv[i][2] - eg.z * KS[i][2];
+      R[i][3] = vv[i][3] - eg.w * KS[i][3];
     }
 
-    // ------------------------------------------------------------ V_new = T R
+    // ------------------------------------------------------------ V_new = T diag(beta) R
     // Two C-layout tiles of R (token blocks 2p, 2p+1) side by side are the B operand
     // of a 16x16x32 MFMA over that block pair, in the contraction order of the
     // record's T pairs.  hi*hi, hi*lo and lo*hi accumulate in one chain per row block.
@@ -605,20 +603,36 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
       for (int hh = 0; hh < 2; ++hh) {
         const int i = 2 * pp + hh;
         const float4 el = *(const float4*)(sEL + 16 * i + 4 * lq);
+        // row C - 1's factor is e^0 = 1; its slot holds e^{G_last}
+        const float el3 = (i == 3 && lq == 3) ? 1.f : el.w;
         vt[hh][0] = U[i][0] * el.x; vt[hh][1] = U[i][1] * el.y;
-        vt[hh][2] = U[i][2] * el.z; vt[hh][3] = U[i][3] * el.w;
+        vt[hh][2] = U[i][2] * el.z; vt[hh][3] = U[i][3] * el3;
       }
       vth[pp] = join(pack_hi4(vt[0]), pack_hi4(vt[1]));
       vtl[pp] = join(pack_lo4(vt[0]), pack_lo4(vt[1]));
+    }
+
+    // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
+    const float gl = sEL[C - 1];  // e^{G_last}
+#pragma unroll
+    for (int t = 0; t < DK / 16; ++t) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) S[t][v] *= gl;
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        S[t] = mma16(kth[t][pp], vth[pp], S[t]);
+        S[t] = mma16(kth[t][pp], vtl[pp], S[t]);
+        if constexpr (IS) S[t] = mma16(ktl[t][pp], vth[pp], S[t]);
+      }
     }
 
     // ------------------------------------------------------------ O = scale e^G (Q S) + P V_new
     f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 eg = *(const float4*)(sEG + 16 * i + 4 * lq);
-      o[i][0] = p.scale * eg.x * QS[i][0]; o[i][1] = p.scale * eg.y * QS[i][1];
-      o[i][2] = p.scale * eg.z * QS[i][2]; o[i][3] = p.scale * eg.w * QS[i][3];
+      const float4 eg = *(const float4*)(sEGS + 16 * i + 4 * lq);
+      o[i][0] = eg.x * QS[i][0]; o[i][1] = eg.y * QS[i][1];
+      o[i][2] = eg.z * QS[i][2]; o[i][3] = eg.w * QS[i][3];
 #pragma unroll
       for (int pp = 0; pp <= i / 2; ++pp) {  // P is lower triangular
         const int x = pair_index(i, pp);
@@ -689,19 +703,6 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     }
 
 
-    // ------------------------------------------------------------ S <- e^{G_last} S + K^T Vt
-    const float gl = sEG[C - 1];
-#pragma unroll
-    for (int t = 0; t < DK / 16; ++t) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) S[t][v] *= gl;
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        S[t] = mma16(kth[t][pp], vth[pp], S[t]);
-        S[t] = mma16(kth[t][pp], vtl[pp], S[t]);
-        if constexpr (IS) S[t] = mma16(ktl[t][pp], vth[pp], S[t]);
-      }
-    }
   };
 
   if constexpr (DIRECT) {

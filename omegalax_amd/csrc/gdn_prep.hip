@@ -89,6 +89,12 @@ __device__ __forceinline__ f32x4 blk_mul_c(const Blk& x, const Blk& y) {
   return mm3k16(zero4(), x.ah, x.al, y.ch, y.cl);
 }
 
+// beta of the columns 16 bj + 4 lq + (0..3) an A-layout tile holds (gw: G, then beta)
+__device__ __forceinline__ f32x4 col_beta(const float* gw, int bj) {
+  const float4 b = *(const float4*)(gw + kC + 16 * bj + 4 * (lane_id() >> 4));
+  return f32x4{b.x, b.y, b.z, b.w};
+}
+
 // one 16x16 tile's A fragment into its half of a record pair (16 bytes per lane)
 __device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
   *(u32x2*)(rec + off + lane_id() * 16) = f;
@@ -464,10 +470,10 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         gw[C + l] = bt;
         if (wave == 0) {
           float* rg = (float*)(rec + kRecG);
-          rg[kGateBeta * C + l] = bt;
-          rg[kGateBE * C + l] = bt * eg;
           rg[kGateEG * C + l] = eg;
-          rg[kGateEL * C + l] = __expf(Gl - G);
+          rg[kGateEGS * C + l] = p.scale * eg;
+          rg[kGateEL * C + l] = l == C - 1 ? __expf(Gl) : __expf(Gl - G);
+          rg[kGateBeta * C + l] = bt;
         }
         wave_lds_fence();
       }
@@ -539,8 +545,10 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             const u32x2 th = pack_hi4(Ta), tl = pack_lo4(Ta);
             sTd[(2 * bi) * 64 + l] = th;  // A fragments of T_ww for the other waves
             sTd[(2 * bi + 1) * 64 + l] = tl;
-            put_tile(rec, rec_t_off(bi, bi), th);
-            put_tile(rec, rec_t_off(bi, bi) + kPairBytes, tl);
+            // the record holds T diag(beta): column 16 bi + 4 lq + v scaled by its beta
+            const f32x4 Tb = Ta * col_beta(gw, bi);
+            put_tile(rec, rec_t_off(bi, bi), pack_hi4(Tb));
+            put_tile(rec, rec_t_off(bi, bi) + kPairBytes, pack_lo4(Tb));
             if ((bi & 1) == 0) {
               // the zero upper tile (bi, bi + 1) that completes row block bi's last pair
               const u32x2 z = {0u, 0u};
@@ -597,8 +605,9 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           const f32x4 TijT = mm3k16(zero4(), xh, xl, th, tl);
           Th[i] = pack_hi4(Tij);
           Tl[i] = pack_lo4(Tij);
-          put_tile(rec, rec_t_off(i, j), pack_hi4(TijT));
-          put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(TijT));
+          const f32x4 Tb = TijT * col_beta(gw, j);  // T_ij diag(beta), A layout
+          put_tile(rec, rec_t_off(i, j), pack_hi4(Tb));
+          put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(Tb));
         }
       }
       __syncthreads();  // sLf / sTd are rewritten for the next value head
