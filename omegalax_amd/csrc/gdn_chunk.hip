@@ -189,22 +189,6 @@ __device__ __forceinline__ int state_row(int t, int q, int v) { return 32 * (t >
 
 __device__ __forceinline__ u32x4 join(u32x2 a, u32x2 b) { return u32x4{a[0], a[1], b[0], b[1]}; }
 
-// base + off bytes; a uniform 64-bit base plus a 32-bit lane offset is one
-// scalar-base memory instruction with no per-lane 64-bit address arithmetic
-template <class T>
-__device__ __forceinline__ T* at_bytes(T* base, unsigned off) {
-  return (T*)((unsigned char*)base + off);
-}
-template <class T>
-__device__ __forceinline__ const T* at_bytes(const T* base, unsigned off) {
-  return (const T*)((const unsigned char*)base + off);
-}
-
-// Buffer resource over `bytes` bytes at p (raw, stride 0): stores through it take a
-// 32-bit lane offset and a uniform scalar offset, with no per-lane address arithmetic.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, (int)bytes, 0x00020000);
-}
 
 // Issue one chunk's loads straight into an LDS buffer (global_load_lds_dwordx4: lane i
 // of an instruction writes 16 bytes at the buffer offset + 16 i), all from the loader

@@ -96,18 +96,20 @@ __device__ __forceinline__ f32x4 col_beta(const float* gw, int bj) {
 }
 
 // one 16x16 tile's A fragment into its half of a record pair (16 bytes per lane)
-__device__ __forceinline__ void put_tile(unsigned char* rec, int off, u32x2 f) {
-  *(u32x2*)(rec + off + lane_id() * 16) = f;
+__device__ __forceinline__ void put_tile(__amdgpu_buffer_rsrc_t rec, int off, u32x2 f) {
+  __builtin_amdgcn_raw_buffer_store_b64(f, rec, 16 * lane_id(), off, 0);
 }
 
 // conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243:
 // wt[e][d] multiplies the input d tokens back (tap K-1-d); taps beyond K are 0
-__device__ __forceinline__ void load_conv_w(const ChunkParams& p, int ch0, float (*wt)[4]) {
+__device__ __forceinline__ void load_conv_w(const ChunkParams& p, int chu, int chl, float (*wt)[4]) {
   const int K = p.conv_k;
+  const int ch0 = chu + chl;
   if (K == 4) {  // uniform: each channel's taps are one 16-byte row
+    const float* wb = p.conv_w + (size_t)chu * 4;  // uniform base, lane channel offset
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float4 w = *(const float4*)(p.conv_w + (size_t)(ch0 + e) * 4);
+      const float4 w = *(const float4*)at_bytes(wb, 16u * (unsigned)(chl + e));
       wt[e][0] = round_bf(w.w);
       wt[e][1] = round_bf(w.z);
       wt[e][2] = round_bf(w.y);
@@ -150,12 +152,24 @@ __device__ __forceinline__ u32x4 conv_input(const ChunkParams& p, int n, long lo
 // row r0 + m.
 template <int ROWS>
 __device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long s0, long long t0,
-                                          int nvalid, int r0, int ch0, u32x4* raw) {
+                                          int nvalid, int r0, int chu, int chl, u32x4* raw) {
+  if (t0 - 3 >= s0) {
+    // uniform: every input row is inside the sequence; a uniform base three rows
+    // before the chunk plus a 32-bit lane offset
+    const bf16_t* base = (const bf16_t*)p.mixed_qkv + (t0 - 3) * p.conv_dim + chu;
+#pragma unroll
+    for (int k = 0; k < ROWS + 3; ++k) {
+      int row = r0 - 3 + k;
+      row = row < nvalid ? row : nvalid - 1;  // padded rows: in bounds, zeroed below
+      raw[k] = *(const u32x4*)at_bytes(base, 2u * ((unsigned)(row + 3) * (unsigned)p.conv_dim + (unsigned)chl));
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < ROWS + 3; ++k) {
     int row = r0 - 3 + k;
     row = row < nvalid ? row : nvalid - 1;  // padded rows: in bounds, zeroed below
-    raw[k] = conv_input(p, n, s0, t0 + row, ch0);
+    raw[k] = conv_input(p, n, s0, t0 + row, chu + chl);
   }
 }
 
@@ -184,13 +198,14 @@ __device__ __forceinline__ void conv_compute(const u32x4* raw, const float (*wt)
 }
 
 // conv_load then conv_compute, with the window and weights local to the call
+// (channels chu + chl .. +7: chu uniform, chl the lane's part)
 template <int ROWS, class Emit>
 __device__ __forceinline__ void conv_rows(const ChunkParams& p, int n, long long s0, long long t0,
-                                          int nvalid, int r0, int ch0, Emit emit) {
+                                          int nvalid, int r0, int chu, int chl, Emit emit) {
   u32x4 raw[ROWS + 3];
   float wt[8][4];
-  load_conv_w(p, ch0, wt);
-  conv_load<ROWS>(p, n, s0, t0, nvalid, r0, ch0, raw);
+  load_conv_w(p, chu, chl, wt);
+  conv_load<ROWS>(p, n, s0, t0, nvalid, r0, chu, chl, raw);
   conv_compute<ROWS>(raw, wt, nvalid, r0, emit);
 }
 
@@ -269,31 +284,37 @@ __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTa
     // the conv input windows are loaded where they are consumed (holding them
     // across the compute phase would halve the occupancy)
   } else {
+    // uniform row-0 bases plus 32-bit lane byte offsets
+    constexpr unsigned ES = F32 ? 4u : 2u;
+    const unsigned char* kb = (const unsigned char*)p.k + (t.t0 * p.k_ld + (long long)t.hk * DK) * ES;
+    const unsigned char* qb = (const unsigned char*)p.q + (t.t0 * p.q_ld + (long long)t.hk * DK) * ES;
 #pragma unroll
     for (int k = 0; k < Q_::NI_KQ; ++k) {
       constexpr int PER = C * SEGS;
       const int which = (k * NT) / PER;  // 0 = k, 1 = q (compile time)
       const int rem = (k * NT) % PER + tid;
       const int r = rem / SEGS, seg = rem % SEGS;
-      const long long tok = t.t0 + (r < t.nvalid ? r : t.nvalid - 1);  // padded rows: zeroed later
-      load_raw<F32>(which == 0 ? p.k : p.q,
-                    tok * (which == 0 ? p.k_ld : p.q_ld) + (long long)t.hk * DK + seg * 8,
-                    &pf.raw[k * Q_::RAWW]);
+      const unsigned rr = (unsigned)(r < t.nvalid ? r : t.nvalid - 1);  // padded rows: zeroed later
+      const unsigned off = ES * (rr * (unsigned)(which == 0 ? p.k_ld : p.q_ld) + 8u * seg);
+      const u32x4* src = (const u32x4*)at_bytes(which == 0 ? kb : qb, off);
+      pf.raw[k * Q_::RAWW] = src[0];
+      if constexpr (F32) pf.raw[k * Q_::RAWW + 1] = src[1];
     }
   }
   const int gqa = p.Hv / p.Hk;
+  const long long g0 = t.t0 * p.Hv + (long long)t.hk * gqa;  // token t0, first value head
 #pragma unroll
   for (int gg = 0; gg < kGatePf; ++gg) {
     pf.ga[gg] = 0.f;
     pf.gb[gg] = 0.f;
     if (gg < gqa && l < t.nvalid) {
-      const long long idx = (t.t0 + l) * p.Hv + t.hk * gqa + gg;
+      const unsigned lo = (unsigned)l * (unsigned)p.Hv;  // lane = token
       if constexpr (MODE == MODE_LAYER) {
-        pf.ga[gg] = bf2f(((const bf16_t*)p.a)[idx]);
-        pf.gb[gg] = bf2f(((const bf16_t*)p.b)[idx]);
+        pf.ga[gg] = bf2f(*at_bytes((const bf16_t*)p.a + g0 + gg, 2u * lo));
+        pf.gb[gg] = bf2f(*at_bytes((const bf16_t*)p.b + g0 + gg, 2u * lo));
       } else {
-        pf.ga[gg] = p.g[idx];
-        pf.gb[gg] = p.beta[idx];
+        pf.ga[gg] = *at_bytes(p.g + g0 + gg, 4u * lo);
+        pf.gb[gg] = *at_bytes(p.beta + g0 + gg, 4u * lo);
       }
     }
   }
@@ -348,27 +369,30 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         constexpr int RP = 64 / SEGS, ROWS = C / RP;
         const int g = l % SEGS, r0 = (l / SEGS) * ROWS;
         bf16_t* dst = (wave == 0 ? sK : sQ) + 8 * g;
-        bf16_t* gout = (bf16_t*)(wave == 0 ? p.kn : p.qn) + (long long)hk * DK + 8 * g;
-        conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (wave == 0 ? p.Hk * DK : 0) + hk * DK + 8 * g,
+        // row t0 of this key head (uniform) plus the lane's byte offset
+        bf16_t* gout = (bf16_t*)(wave == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK + (long long)hk * DK;
+        const unsigned ostride = (unsigned)(p.Hk * DK);
+        conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (wave == 0 ? p.Hk * DK : 0) + hk * DK, 8 * g,
                         [&](int m, float* y) {
           l2norm8<SEGS>(y);
           const u32x4 hw = pack8(y);
           const int r = r0 + m;
           *(u32x4*)(dst + r * LDK) = hw;
-          if (r < nvalid) *(u32x4*)(gout + (t0 + r) * (long long)p.Hk * DK) = hw;
+          if (r < nvalid) *(u32x4*)at_bytes(gout, 2u * ((unsigned)r * ostride + 8u * g)) = hw;
         });
       } else {
         const int VG = gqa * p.DV / 8;  // 8-channel groups of v
         const int vch0 = 2 * p.Hk * DK + hk * gqa * p.DV;
-        bf16_t* vout = (bf16_t*)p.vc + (long long)hk * gqa * p.DV;
+        bf16_t* vout = (bf16_t*)p.vc + t0 * (long long)p.Hv * p.DV + (long long)hk * gqa * p.DV;
+        const unsigned vstride = (unsigned)(p.Hv * p.DV);
         for (int it = tid - 128; it < VG * 4; it += 128) {
           const int g = it % VG, r0 = (it / VG) * 16;
           if (r0 >= nvalid) continue;
           auto emit = [&](int m, float* y) {
             const int r = r0 + m;
-            if (r < nvalid) *(u32x4*)(vout + (t0 + r) * (long long)p.Hv * p.DV + 8 * g) = pack8(y);
+            if (r < nvalid) *(u32x4*)at_bytes(vout, 2u * ((unsigned)r * vstride + 8u * g)) = pack8(y);
           };
-          conv_rows<16>(p, n, s0, t0, nvalid, r0, vch0 + 8 * g, emit);
+          conv_rows<16>(p, n, s0, t0, nvalid, r0, vch0, 8 * g, emit);
         }
       }
     } else {
@@ -392,13 +416,15 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         if constexpr (IS) *(u32x4*)(dst + K_LO) = pack8_lo(x);
         void* out = which == 0 ? p.kn : p.qn;
         if (out && r < nvalid) {
-          const long long o = (t0 + r) * (long long)p.Hk * DK + (long long)hk * DK + seg * 8;
+          // row t0 of this key head (uniform) plus the lane's byte offset
+          const long long o0 = t0 * (long long)p.Hk * DK + (long long)hk * DK;
+          const unsigned lo = (unsigned)r * (unsigned)(p.Hk * DK) + 8u * seg;
           if constexpr (F32) {
-            float4* d4 = (float4*)((float*)out + o);
+            float4* d4 = (float4*)at_bytes((float*)out + o0, 4u * lo);
             d4[0] = float4{x[0], x[1], x[2], x[3]};
             d4[1] = float4{x[4], x[5], x[6], x[7]};
           } else {
-            *(u32x4*)((bf16_t*)out + o) = hw;
+            *(u32x4*)at_bytes((bf16_t*)out + o0, 2u * lo) = hw;
           }
         }
       }
@@ -439,7 +465,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
 
     for (int gg = 0; gg < gqa; ++gg) {
       const int h = hk * gqa + gg;
-      unsigned char* rec = p.rec + ((size_t)ci * p.Hv + h) * rec_stride;
+      const auto rec = buf_rsrc(p.rec + ((size_t)ci * p.Hv + h) * rec_stride, (unsigned)rec_stride);
 
       // gates of value head h, one token per lane; every wave scans its own copy
       {
@@ -448,13 +474,14 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           g = sGin[gg * 2 * C + l];
           bt = sGin[gg * 2 * C + C + l];
         } else if (l < nvalid) {
-          const long long idx = (t0 + l) * p.Hv + h;
+          const long long i0 = t0 * p.Hv + h;
+          const unsigned lo = (unsigned)l * (unsigned)p.Hv;
           if constexpr (MODE == MODE_LAYER) {
-            g = bf2f(((const bf16_t*)p.a)[idx]);
-            bt = bf2f(((const bf16_t*)p.b)[idx]);
+            g = bf2f(*at_bytes((const bf16_t*)p.a + i0, 2u * lo));
+            bt = bf2f(*at_bytes((const bf16_t*)p.b + i0, 2u * lo));
           } else {
-            g = p.g[idx];
-            bt = p.beta[idx];
+            g = *at_bytes(p.g + i0, 4u * lo);
+            bt = *at_bytes(p.beta + i0, 4u * lo);
           }
         }
         if constexpr (MODE == MODE_LAYER) {
@@ -469,11 +496,13 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         gw[l] = G * 1.4426950408889634f;
         gw[C + l] = bt;
         if (wave == 0) {
-          float* rg = (float*)(rec + kRecG);
-          rg[kGateEG * C + l] = eg;
-          rg[kGateEGS * C + l] = p.scale * eg;
-          rg[kGateEL * C + l] = l == C - 1 ? __expf(Gl) : __expf(Gl - G);
-          rg[kGateBeta * C + l] = bt;
+          auto put = [&](int row, float x) {
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), rec, 4 * l, kRecG + 4 * C * row, 0);
+          };
+          put(kGateEG, eg);
+          put(kGateEGS, p.scale * eg);
+          put(kGateEL, l == C - 1 ? __expf(Gl) : __expf(Gl - G));
+          put(kGateBeta, bt);
         }
         wave_lds_fence();
       }
