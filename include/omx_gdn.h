@@ -114,8 +114,7 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
 /*
  * Bytes of device workspace omx_gdn_prefill needs (16-byte aligned): the chunk
  * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v, and
- * the unnormalised bf16 o with partial sums of o^2 that the gated-norm epilogue
- * combines.
+ * the unnormalised bf16 o that the gated-norm epilogue reads.
  */
 size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
                                       int64_t dv, int64_t N);

@@ -55,7 +55,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // normalised k and q, (layer) the conv output of v, the bf16 o and the partial
 // sums of o^2 for the gated norm, and the chunk offsets of packed sequences.
 struct ChunkWs {
-  size_t rec, kn, qn, vc, opart, sspart, off, total;
+  size_t rec, kn, qn, vc, opart, off, total;
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
@@ -77,8 +77,6 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
     w.opart = o;
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
-    w.sspart = o;
-    o += align_up(tokens * (size_t)Hv * (size_t)omx::layer_norm_parts((int)dv) * 4, 256);
   }
   w.off = o;
   o += align_up((size_t)(N + 1) * 4, 256);
@@ -320,13 +318,12 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
   p.eps = eps;
   p.qk_l2norm = 1;
   p.o_part = (char*)workspace + ws.opart;
-  p.ss_part = (float*)((char*)workspace + ws.sspart);
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
   REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
   if (e == hipSuccess)
-    e = omx::launch_norm_epilogue(p.o_part, p.ss_part, z, norm_w, out, tokens * Hv, (int)dv,
-                                  omx::layer_norm_parts((int)dv), eps, (hipStream_t)stream);
+    e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, eps,
+                                  (hipStream_t)stream);
   return launch_status(e, fn);
 }
 

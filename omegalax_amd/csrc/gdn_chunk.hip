@@ -31,8 +31,7 @@
 // enters K S / Q S, and P, V_new enter P V_new, as single bf16.
 //
 // Modes: MODE_BF16 / MODE_F32 (core function) store o in fp32.  MODE_LAYER stores
-// o in bf16 with each wavefront's partial sums of o^2 per token; the epilogue
-// kernel (gdn_epilogue.hip) adds them and applies the gated RMSNorm
+// o in bf16; the epilogue kernel (gdn_epilogue.hip) applies the gated RMSNorm
 // (deltanet.py:282-293).
 #include <type_traits>
 
@@ -337,13 +336,11 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
 
 
   // output addressing: row stride and the lane's constant offset within a chunk
-  const int nparts = nb * NWC;                       // partial sums of o^2 per row (layer)
-  const int o_rs = p.Hv * DV, s_rs = p.Hv * nparts;  // row strides of o and of the sums
+  const int o_rs = p.Hv * DV;  // row stride of o
   // unsigned: a uniform 64-bit base plus a zero-extended 32-bit lane offset is one
   // scalar-base memory instruction with no per-lane 64-bit address arithmetic
   const unsigned o_elem = 4u * lq * o_rs + 16u * wave + lr;
   const unsigned o_lane = 4u * o_elem, o_lane_h = 2u * o_elem;  // bytes: fp32 o, bf16 o
-  const unsigned s_lane = 16u * lq * s_rs;                      // bytes: fp32 sums
 
   Prefetch<DK, MODE> pf;
   if (nchunks > 0) {
@@ -647,42 +644,22 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
             if (16 * i + 4 * lq + v < nvalid) store(i, v);
       }
     } else {
-      // unnormalised o in bf16 and this wave's share of sum(o^2) over its 16 columns;
-      // the epilogue kernel adds the shares and applies the norm
+      // unnormalised o in bf16; the epilogue kernel applies the norm
       const auto ob = buf_rsrc((bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0, 2u * C * o_rs);
-      const auto sb = buf_rsrc(p.ss_part + (t0 * p.Hv + h) * (long long)nparts + blk * NWC + wave,
-                               4u * C * s_rs);
-      float ss[4][4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) ss[i][v] = group_sum_dpp<16>(o[i][v] * o[i][v]);
       auto store = [&](int i, int v) {
         __builtin_amdgcn_raw_buffer_store_b16(f2bf(o[i][v]), ob, o_lane_h, 2 * (16 * i + v) * o_rs, 0);
-      };
-      auto store_ss = [&](int i, int v) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ss[i][v]), sb, s_lane, 4 * (16 * i + v) * s_rs, 0);
       };
       if (nvalid == C) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int v = 0; v < 4; ++v) store(i, v);
-        if (lr == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) store_ss(i, v);
-        }
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            if (16 * i + 4 * lq + v < nvalid) {
-              store(i, v);
-              if (lr == 0) store_ss(i, v);
-            }
+            if (16 * i + 4 * lq + v < nvalid) store(i, v);
       }
     }
 
@@ -764,8 +741,6 @@ hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
 int chunk_block_cols() { return BV; }
 
 int chunk_record_bytes(int mode) { return rec_bytes(mode); }
-
-int layer_norm_parts(int dv) { return dv / BV * NWC; }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
   if (dv % BV != 0 || dv > 256) return false;

@@ -58,7 +58,6 @@ struct ChunkParams {
   void* conv_state_out;        // [N, conv_dim, K-1] bf16 or null
   void* out;                   // [tokens, Hv*DV] bf16
   void* o_part;                // unnormalised o [tokens, Hv, DV] bf16 (workspace)
-  float* ss_part;              // partial sums of o^2 [tokens, Hv, layer_norm_parts(DV)] (workspace)
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
@@ -94,13 +93,10 @@ hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);
 hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream);
 hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream);
 
-// Gated RMSNorm of the layer prefill from bf16 o and nparts partial sums of o^2 per
-// row: out = w * o * rsqrt(sum/dv + eps) * silu(z).
-hipError_t launch_norm_epilogue(const void* o_part, const float* ss_part, const void* z,
-                                const float* norm_w, void* out, long long rows, int dv, int nparts,
-                                float eps, hipStream_t stream);
-// partial sums of o^2 per (token, value head) row that the layer scan writes
-int layer_norm_parts(int dv);
+// Gated RMSNorm of the layer prefill from bf16 o: out = w * o * rsqrt(mean(o^2) + eps)
+// * silu(z) per (token, value head) row of dv (dv / 8 at most 32).
+hipError_t launch_norm_epilogue(const void* o_part, const void* z, const float* norm_w, void* out,
+                                long long rows, int dv, float eps, hipStream_t stream);
 
 bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();
