@@ -106,7 +106,8 @@ __device__ __forceinline__ u32x2 pack_hi4(f32x4 x) {
   return u32x2{pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3])};
 }
 __device__ __forceinline__ u32x2 pack_lo4(f32x4 x) {
-  return u32x2{pack_bf16(lo_part(x[0]), lo_part(x[1])), pack_bf16(lo_part(x[2]), lo_part(x[3]))};
+  const u32x2 h = pack_hi4(x);
+  return u32x2{pack_lo_pair(x[0], x[1], h[0]), pack_lo_pair(x[2], x[3], h[1])};
 }
 
 // unpack 8 input values (bf16 or fp32) from raw load words
@@ -144,8 +145,9 @@ __device__ __forceinline__ u32x4 pack8(const float* x) {
                pack_bf16(x[6], x[7])};
 }
 __device__ __forceinline__ u32x4 pack8_lo(const float* x) {
-  return u32x4{pack_bf16(lo_part(x[0]), lo_part(x[1])), pack_bf16(lo_part(x[2]), lo_part(x[3])),
-               pack_bf16(lo_part(x[4]), lo_part(x[5])), pack_bf16(lo_part(x[6]), lo_part(x[7]))};
+  const u32x4 h = pack8(x);
+  return u32x4{pack_lo_pair(x[0], x[1], h[0]), pack_lo_pair(x[2], x[3], h[1]),
+               pack_lo_pair(x[4], x[5], h[2]), pack_lo_pair(x[6], x[7], h[3])};
 }
 
 // Sequence n's token range [s0, s1): packed by cu_seqlens (clamped to [0, T], so a

@@ -26,6 +26,21 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// bf16 lo parts of two floats whose bf16 hi parts are packed in h: (x0 - hi0, x1 - hi1)
+// rounded to bf16.  Each difference is one bf16 dot product, x_k + (-1) hi_k + 0: the
+// products are exact and the difference of two close floats is exact.
+// The selectors (-1, 0) and (0, -1) are held in scalar registers: an inline float
+// constant in a packed bf16 operand does not mean the bf16 pair.
+__device__ __forceinline__ uint32_t pack_lo_pair(float x0, float x1, uint32_t h) {
+  uint32_t m0, m1;
+  asm("" : "=s"(m0) : "0"(0x0000BF80u));  // bf16 (-1, 0)
+  asm("" : "=s"(m1) : "0"(0xBF800000u));  // bf16 (0, -1)
+  const bf16x2_t hb = __builtin_bit_cast(bf16x2_t, h);
+  const float l0 = __builtin_amdgcn_fdot2_f32_bf16(hb, __builtin_bit_cast(bf16x2_t, m0), x0, false);
+  const float l1 = __builtin_amdgcn_fdot2_f32_bf16(hb, __builtin_bit_cast(bf16x2_t, m1), x1, false);
+  return pack_bf16(l0, l1);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // log(1 + e^x), the softplus of jax.nn.softplus; exact branch for large x.
