@@ -262,13 +262,6 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                      (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
 }
 
-// Workgroup barrier ordering LDS accesses only (no wait for outstanding global stores).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 template <int DK, int MODE>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a

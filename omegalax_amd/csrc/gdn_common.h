@@ -26,6 +26,15 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// Workgroup barrier that orders LDS accesses only: it does not wait for the wave's
+// outstanding global loads and stores (__syncthreads does), so prefetches and result
+// stores stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // bf16 lo parts of two floats whose bf16 hi parts are packed in h: (x0 - hi0, x1 - hi1)
 // rounded to bf16.  Each difference is one bf16 dot product, x_k + (-1) hi_k + 0: the
 // products are exact and the difference of two close floats is exact.

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // L2 norm of q and k at the input precision (deltanet.py:30-32, 65-66)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     ss = wave_sum(ss);
     if (lane == 0) s_scal[wave] = rsqrtf(ss + 1e-6f);
   }
-  __syncthreads();
+  lds_barrier();
   const bool round_act = LAYER || sizeof(InT) == 2;
   const float scale = p.scale;
   for (int i = tid; i < DK; i += kThreads) {
@@ -138,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     s_q[i] = qn * scale;
     s_k[i] = kn;
   }
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     float d = 0.f;
     for (int i = lane; i < DK; i += 64) d += s_q[i] * s_k[i];
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       vpark[j] = (vi < gqa * DV) ? s_red_kv[vi / DV][vi % DV] : 0.f;
     }
   }
-  __syncthreads();
+  lds_barrier();
   const float qk = s_scal[2];
 
   const int cg = tid % CG, rg = tid / CG;
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     s_red_kv[rg][4 * cg + 2] = kv.z; s_red_kv[rg][4 * cg + 3] = kv.w;
     s_red_qs[rg][4 * cg + 0] = qs.x; s_red_qs[rg][4 * cg + 1] = qs.y;
     s_red_qs[rg][4 * cg + 2] = qs.z; s_red_qs[rg][4 * cg + 3] = qs.w;
-    __syncthreads();
+    lds_barrier();
     if (tid < DV) {
       float skv = 0.f, sqs = 0.f;
 #pragma unroll
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       s_delta[tid] = delta;
       s_o[tid] = alpha * sqs + qk * delta;
     }
-    __syncthreads();
+    lds_barrier();
     float4 dl = *(const float4*)(s_delta + 4 * cg);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
         ss = wave_sum(ss);
         if (lane == 0) s_scal[3] = rsqrtf(ss / DV + p.eps);
       }
-      __syncthreads();
+      lds_barrier();
       const float rn = s_scal[3];
       bf16_t* out = (bf16_t*)p.out + ((size_t)b * p.Hv + h) * DV;
       const bf16_t* z = (const bf16_t*)p.z + ((size_t)b * p.Hv + h) * DV;
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       float* o = p.o + ((size_t)b * p.Hv + h) * DV;
       for (int i = tid; i < DV; i += kThreads) o[i] = s_o[i];
     }
-    __syncthreads();
+    lds_barrier();
     if (hh + 1 < gqa) {
 #pragma unroll
       for (int r = 0; r < R; ++r) st[r] = stn[r];

@@ -436,10 +436,11 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         sGin[gg * 2 * C + C + l] = pf.gb[gg];
       }
     }
-    // the next task's loads land while this one computes
+    // the next task's loads land while this one computes (the barrier below does not
+    // wait for them, nor for the normalised rows' stores)
     if constexpr (prep_persistent<MODE>())
       if (task + 1 < last) prep_prefetch<DK, MODE>(p, prep_task(p, task + 1, n_ci), pf);
-    __syncthreads();
+    lds_barrier();
 
     // -------------------------------------------------------------- Gram tiles
     // Tile (bi, bj) is computed as (rows of block bj) x (rows of block bi)^T, so lane
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           if constexpr (IS) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
         }
       }
-      __syncthreads();  // L blocks and the diagonal inverses of all waves are in LDS
+      lds_barrier();  // L blocks and the diagonal inverses of all waves are in LDS
 
       // block column j = wave: T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj, i = j+1..3.
       // X is an MFMA result in C layout: the B operand here, and read the other way the
@@ -639,7 +640,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(Tb));
         }
       }
-      __syncthreads();  // sLf / sTd are rewritten for the next value head
+      lds_barrier();  // sLf / sTd are rewritten for the next value head
     }
   }
 }
