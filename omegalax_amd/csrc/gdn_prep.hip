@@ -404,9 +404,11 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         const int r = rem / SEGS, seg = rem % SEGS;
         float x[8];
         unpack8<F32>(&pf.raw[k * Q_::RAWW], x);
-        const float keep = (float)(r < nvalid);
+        if (nvalid < C) {  // uniform: a sequence's last chunk; its padded rows are zero
+          const float keep = (float)(r < nvalid);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] *= keep;
+          for (int e = 0; e < 8; ++e) x[e] *= keep;
+        }
         if (p.qk_l2norm) l2norm8<SEGS>(x);
         // bf16 inputs: the normalised row is rounded to bf16 (the reference
         // normalises in the input dtype); the pack below does the rounding
@@ -415,7 +417,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         *(u32x4*)dst = hw;
         if constexpr (IS) *(u32x4*)(dst + K_LO) = pack8_lo(x);
         void* out = which == 0 ? p.kn : p.qn;
-        if (out && r < nvalid) {
+        if (out && (nvalid == C || r < nvalid)) {
           // row t0 of this key head (uniform) plus the lane's byte offset
           const long long o0 = t0 * (long long)p.Hk * DK + (long long)hk * DK;
           const unsigned lo = (unsigned)r * (unsigned)(p.Hk * DK) + 8u * seg;
