@@ -153,18 +153,6 @@ __device__ __forceinline__ u32x4 conv_input(const ChunkParams& p, int n, long lo
 template <int ROWS>
 __device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long s0, long long t0,
                                           int nvalid, int r0, int chu, int chl, u32x4* raw) {
-  if (t0 - 3 >= s0) {
-    // uniform: every input row is inside the sequence; a uniform base three rows
-    // before the chunk plus a 32-bit lane offset
-    const bf16_t* base = (const bf16_t*)p.mixed_qkv + (t0 - 3) * p.conv_dim + chu;
-#pragma unroll
-    for (int k = 0; k < ROWS + 3; ++k) {
-      int row = r0 - 3 + k;
-      row = row < nvalid ? row : nvalid - 1;  // padded rows: in bounds, zeroed below
-      raw[k] = *(const u32x4*)at_bytes(base, 2u * ((unsigned)(row + 3) * (unsigned)p.conv_dim + (unsigned)chl));
-    }
-    return;
-  }
 #pragma unroll
   for (int k = 0; k < ROWS + 3; ++k) {
     int row = r0 - 3 + k;
@@ -252,6 +240,16 @@ __device__ __forceinline__ PrepTask prep_task(const ChunkParams& p, int task, in
   seq_range(p.cu_seqlens, t.n, p.T, t.s0, s1);
   t.t0 = t.s0 + (long long)c * C;
   t.nvalid = (int)((s1 - t.t0) < C ? (s1 - t.t0) : C);
+  // the task is uniform over the workgroup: keep it in scalar registers (values read
+  // from the offset arrays would otherwise sit in vector registers)
+  t.ci = __builtin_amdgcn_readfirstlane(t.ci);
+  t.hk = __builtin_amdgcn_readfirstlane(t.hk);
+  t.n = __builtin_amdgcn_readfirstlane(t.n);
+  t.nvalid = __builtin_amdgcn_readfirstlane(t.nvalid);
+  t.s0 = ((long long)__builtin_amdgcn_readfirstlane((int)(t.s0 >> 32)) << 32) |
+         (unsigned)__builtin_amdgcn_readfirstlane((int)t.s0);
+  t.t0 = ((long long)__builtin_amdgcn_readfirstlane((int)(t.t0 >> 32)) << 32) |
+         (unsigned)__builtin_amdgcn_readfirstlane((int)t.t0);
   return t;
 }
 
