@@ -8,5 +8,11 @@ from .deltanet import (  # noqa: F401
     GDNError, chunk_gated_delta_rule, gdn_decode_step, gdn_prefill,
     recurrent_gated_delta_rule_step,
 )
+from .layer import (  # noqa: F401
+    GDNConfig, GDNLayerCache, GDNParams, gated_deltanet_decode, gated_deltanet_forward,
+    gated_deltanet_prefill_cache, gdn_params_from_hf, gdn_params_to_hf, load_gdn_layers,
+    make_gdn_cache,
+)
+from .segments import lengths_to_cu_seqlens, right_pad_lengths, segment_ids_to_cu_seqlens  # noqa: F401
 
 __version__ = "0.1.0"
