@@ -65,7 +65,7 @@ def test_layer_forward_matches_oracle_with_mask():
     torch.cuda.synchronize()
     # the oracle from the same bf16 projection outputs
     h = hidden * mask[:, :, None].to(hidden.dtype)
-    mixed, z, a, b = (F.linear(h, w) for w in (p.in_proj_qkv, p.in_proj_z, p.in_proj_b, p.in_proj_a))
+    mixed, z, a, b = (F.linear(h, w) for w in (p.in_proj_qkv, p.in_proj_z, p.in_proj_a, p.in_proj_b))
     ref_n, _, _ = O.gdn_prefill_layer(np_(mixed), np_(z).reshape(B, T, cfg.num_v_heads, cfg.head_v_dim),
                                       np_(a), np_(b), np_(p.conv_w), np_(p.A_log), np_(p.dt_bias),
                                       np_(p.norm_w), Hk=cfg.num_k_heads, dk=cfg.head_k_dim,
@@ -119,6 +119,7 @@ def test_right_padded_prefill_cache_then_decode_equals_full_prefill():
         ref = gated_deltanet_forward(p, cfg, full[b:b + 1, :n + steps].contiguous())
         torch.cuda.synchronize()
         assert rel(np_(out_p[b, :n]), np_(ref[0, :n])) < BF16_TOL, b
-        assert float(out_p[b, n:].abs().max()) == 0.0  # padded positions
+        if n < T:
+            assert float(out_p[b, n:].abs().max()) == 0.0  # padded positions
         for s in range(steps):
             assert rel(np_(outs[s][b]), np_(ref[0, n + s])) < BF16_TOL, (b, s)
