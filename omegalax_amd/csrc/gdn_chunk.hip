@@ -332,7 +332,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
   const int o_rs = p.Hv * DV;  // row stride of o
   // unsigned: a uniform 64-bit base plus a zero-extended 32-bit lane offset is one
   // scalar-base memory instruction with no per-lane 64-bit address arithmetic
-  const unsigned o_elem = 4u * lq * o_rs + 16u * wave + lr;
+  // (output tiles are transposed: lane (q, r) holds row r, columns 16w + 4q .. +3)
+  const unsigned o_elem = (unsigned)lr * o_rs + 16u * wave + 4u * lq;
   const unsigned o_lane = 4u * o_elem, o_lane_h = 2u * o_elem;  // bytes: fp32 o, bf16 o
 
   Prefetch<DK, MODE> pf;
@@ -477,7 +478,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
 #pragma unroll
       for (int i = 0; i < 4; ++i) {  // eight independent accumulation chains
         KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
-        QS[i] = mm<IS, IS>(QS[i], qh[i][s2], ql[i][s2], sh[s2], sl[s2]);
+        QS[i] = mm<IS, IS>(QS[i], sh[s2], sl[s2], qh[i][s2], ql[i][s2]);  // (Q S)^T
       }
     if constexpr (DIRECT && !IS) {
       // all fragment reads go out back to back, then the state packs, then the
@@ -601,58 +602,60 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     }
 
     // ------------------------------------------------------------ O = scale e^G (Q S) + P V_new
+    // Computed transposed, O^T = S^T Q^T + V_new^T P^T: the packed state and V_new (B
+    // operands above) serve as A operands and the Q and P fragments as B operands, since
+    // both operand layouts hold "row r, contraction slots 8q .. 8q+7".  Lane (q, r) then
+    // holds token 16i + r, columns 16w + 4q .. +3 of the wave's slice: one 16-byte (fp32)
+    // or 8-byte (bf16) store per row block, and one gate factor per lane.
     f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 eg = *(const float4*)(sEGS + 16 * i + 4 * lq);
-      o[i][0] = eg.x * QS[i][0]; o[i][1] = eg.y * QS[i][1];
-      o[i][2] = eg.z * QS[i][2]; o[i][3] = eg.w * QS[i][3];
+      const float eg = sEGS[16 * i + lr];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o[i][v] = eg * QS[i][v];
 #pragma unroll
       for (int pp = 0; pp <= i / 2; ++pp) {  // P is lower triangular
         const int x = pair_index(i, pp);
-        o[i] = mma16(ph[x], Uh[pp], o[i]);
+        o[i] = mma16(Uh[pp], ph[x], o[i]);
         if constexpr (OS) {
-          o[i] = mma16(ph[x], Ul[pp], o[i]);
-          o[i] = mma16(pl[x], Uh[pp], o[i]);
+          o[i] = mma16(Ul[pp], ph[x], o[i]);
+          o[i] = mma16(Uh[pp], pl[x], o[i]);
         }
       }
     }
-    // row 16i + 4lq + v of the chunk: the chunk's rows 16i + v (a uniform offset) plus
-    // the lane's constant byte offset; every row of a full chunk is stored (uniform)
+    // row 16i + r of the chunk: a uniform row-block offset plus the lane's constant byte
+    // offset; every row of a full chunk is stored (uniform)
     if constexpr (MODE != MODE_LAYER) {
       const auto ob = buf_rsrc(p.o + (t0 * p.Hv + h) * (long long)DV + col0, 4u * C * o_rs);
-      auto store = [&](int i, int v) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[i][v]), ob, o_lane, 4 * (16 * i + v) * o_rs, 0);
+      auto store = [&](int i) {
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__float_as_uint(o[i][0]), __float_as_uint(o[i][1]), __float_as_uint(o[i][2]),
+                  __float_as_uint(o[i][3])},
+            ob, o_lane, 4 * 16 * i * o_rs, 0);
       };
       if (nvalid == C) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) store(i, v);
+        for (int i = 0; i < 4; ++i) store(i);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (16 * i + 4 * lq + v < nvalid) store(i, v);
+          if (16 * i + lr < nvalid) store(i);
       }
     } else {
       // unnormalised o in bf16; the epilogue kernel applies the norm
       const auto ob = buf_rsrc((bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0, 2u * C * o_rs);
-      auto store = [&](int i, int v) {
-        __builtin_amdgcn_raw_buffer_store_b16(f2bf(o[i][v]), ob, o_lane_h, 2 * (16 * i + v) * o_rs, 0);
+      auto store = [&](int i) {
+        __builtin_amdgcn_raw_buffer_store_b64(
+            u32x2{pack_bf16(o[i][0], o[i][1]), pack_bf16(o[i][2], o[i][3])}, ob, o_lane_h,
+            2 * 16 * i * o_rs, 0);
       };
       if (nvalid == C) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) store(i, v);
+        for (int i = 0; i < 4; ++i) store(i);
       } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            if (16 * i + 4 * lq + v < nvalid) store(i, v);
+          if (16 * i + lr < nvalid) store(i);
       }
     }
 
