@@ -151,6 +151,42 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
                            int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, float scale,
                            void* stream);
 
+/*
+ * Backward pass (VJP) of omx_gdn_chunk_fwd.  Replaces the reverse-mode derivative
+ * JAX takes of chunk_gated_delta_rule (deltanet.py:53-153) when the reference trains
+ * through it (value_and_grad in trainers/vlm.py:157-195, remat at model.py:202): given
+ * the forward's inputs and the cotangents of o (and of the final state), returns the
+ * gradients of every input.  Inputs have the meaning and layout of omx_gdn_chunk_fwd;
+ * the forward is recomputed inside (nothing is kept between the two calls).
+ *
+ *   d_o            [B, T, Hv, dv] f32, cotangent of o
+ *   d_final_state  [N, Hv, dk, dv] f32 or NULL (zeros)
+ *   dq, dk         [B, T, Hk, dk] in_dtype: gradients of the raw q, k (through the
+ *                  in-kernel L2 norm when qk_l2norm != 0, summed over each key head's
+ *                  value heads)
+ *   dv             [B, T, Hv, dv] in_dtype
+ *   dg, dbeta      [B, T, Hv] f32
+ *   d_initial_state [N, Hv, dk, dv] f32 or NULL
+ * Compiled shapes: bf16 inputs dk 64/128, fp32 inputs dk 32/64; dv 64/128.
+ */
+int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
+                      const float* g, const float* beta, const float* initial_state,
+                      const int32_t* cu_seqlens, int64_t N, const float* d_o,
+                      const float* d_final_state, void* dq, void* dk, void* dv, float* dg,
+                      float* dbeta, float* d_initial_state, int64_t B, int64_t T, int64_t Hk,
+                      int64_t Hv, int64_t dk_dim, int64_t dv_dim, int64_t chunk_size,
+                      float scale, int qk_l2norm, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/*
+ * Bytes of device workspace omx_gdn_chunk_bwd needs (16-byte aligned): the forward's
+ * workspace, the per-chunk fp32 X = (I + L)^-1, L, P and gates, the state entering and
+ * the state gradient leaving every chunk, V_new and its gradient, and per-value-head
+ * gradients of the normalised q and k.
+ */
+size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                                        int64_t dk, int64_t dv, int64_t N, int in_dtype);
+
 #ifdef __cplusplus
 }
 #endif

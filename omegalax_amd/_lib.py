@@ -39,6 +39,10 @@ SIGNATURES = {
                                  _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "omx_gdn_recurrent_step": (_i, [_p, _p, _p, _i, _p, _p, _p, _p,
                                     _i64, _i64, _i64, _i64, _i64, _f, _p]),
+    "omx_gdn_chunk_bwd": (_i, [_p, _p, _p, _i, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p,
+                               _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _sz,
+                               _p]),
+    "omx_gdn_chunk_bwd_workspace_size": (_sz, [_i64] * 7 + [_i]),
 }
 
 

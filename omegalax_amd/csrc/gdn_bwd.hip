@@ -1,0 +1,831 @@
+// Backward pass (VJP) of the chunked gated delta rule on gfx950.
+//
+// The reference trains through chunk_gated_delta_rule (omegalax/models/qwen3_5/
+// deltanet.py:53-153) with JAX reverse-mode autodiff (trainers/vlm.py:157-195); this
+// file computes that derivative.  Per chunk (G = in-chunk cumsum of g, Gamma_im =
+// e^{G_i - G_m} for i >= m, X = (I + L)^-1 with L = diag(beta) Lg, Lg = strict_lower(
+// K K^T * Gamma), P = lower(scale Q K^T * Gamma); deltanet.py:98-142):
+//     V_new = X diag(beta) (V - diag(e^G) K S)               (:115-116, 133-134)
+//     O     = scale diag(e^G) Q S + P V_new                   (:136-137)
+//     S'    = e^{G_last} S + K^T diag(e^{G_last - G}) V_new   (:139-142)
+// Three kernels, after the forward's preparation and scan have been rerun in their
+// backward variants (which leave X, Lg, P, G per chunk and the state entering every
+// chunk plus V_new):
+//  1. rscan_kernel walks each sequence's chunks backwards carrying dS, the gradient of
+//     the state leaving the chunk, in registers (one workgroup per (sequence, value head,
+//     64 columns of dv), 16 columns per wavefront):
+//         dV_new = P^T dO + diag(e^{G_last - G}) K dS
+//         dS    <- e^{G_last} dS + scale Q^T diag(e^G) dO - K^T diag(e^G) diag(beta) X^T dV_new
+//     and stores dS per chunk and dV_new.
+//  2. cgrad_kernel forms, for every (chunk, value head) at once, the chunk-local
+//     gradients of q, k (per value head), v, g and beta from S, dS, V_new, dV_new and
+//     the chunk's matrices, differentiating :100-142 step by step (the derivation is the
+//     one of the fp64 test oracle, oracle/gdn_vjp.py).
+//  3. qk_final_kernel sums the per-value-head q/k gradients over each key head's value
+//     heads (the adjoint of the repeat-interleave, :272-280) and applies the L2-norm
+//     backward (:30-32), writing dq, dk at the input precision.
+// All products are 16x16x32 bf16 MFMAs on operands split into bf16 hi + lo parts
+// (hi*hi + hi*lo + lo*hi, fp32-accurate to ~2^-16); operands known to be exact bf16
+// (bf16 q/k rows) skip their lo part.
+#include <type_traits>
+
+#include "gdn_chunk.h"
+#include "gdn_kernels.h"
+
+namespace omx {
+
+namespace {
+
+constexpr int C = kC;
+constexpr int NT = kNT;
+constexpr int LDF = C + 4;  // row stride (floats) of 64-wide fp32 LDS matrices
+
+struct Op {
+  u32x4 h, l;
+};
+
+// bf16 hi and lo parts of 8 values (x = hi + lo to ~2^-16 relative)
+template <bool LO = true>
+__device__ __forceinline__ Op split8(const float* x) {
+  Op o;
+  o.h = pack8(x);
+  if constexpr (LO) o.l = pack8_lo(x);
+  else o.l = o.h;
+  return o;
+}
+
+// acc += A B: hi*hi, plus hi*lo when B has a lo part, plus lo*hi when A has one
+template <bool AL, bool BL>
+__device__ __forceinline__ f32x4 mm3(f32x4 acc, const Op& a, const Op& b) {
+  acc = mma16(a.h, b.h, acc);
+  if constexpr (BL) acc = mma16(a.h, b.l, acc);
+  if constexpr (AL) acc = mma16(a.l, b.h, acc);
+  return acc;
+}
+
+// B operand from two C-layout tiles side by side (block-pair contraction order)
+__device__ __forceinline__ Op join_op(f32x4 a, f32x4 b) {
+  Op o;
+  o.h = u32x4{pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]),
+              pack_bf16(b[2], b[3])};
+  const u32x2 la = pack_lo4(a), lb = pack_lo4(b);
+  o.l = u32x4{la[0], la[1], lb[0], lb[1]};
+  return o;
+}
+
+__device__ __forceinline__ float ldx(const float* p) { return *p; }
+__device__ __forceinline__ float ldx(const bf16_t* p) { return bf2f(*p); }
+
+// Contraction index of operand slot e in lane group q: the natural order 8q + e, or the
+// block-pair order (4q + e%4, then 16 + 4q + e%4) of two C-layout tiles side by side.
+template <bool PAIR>
+__device__ __forceinline__ int kslot(int q, int e) {
+  return PAIR ? 4 * q + (e & 3) + 16 * (e >> 2) : 8 * q + e;
+}
+
+// operand row `row` of a row-major M[row][k], slots over k from k0
+template <bool PAIR, class T>
+__device__ __forceinline__ void frag_row(const T* m, int ld, int row, int k0, float* x) {
+  const int q = lane_id() >> 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = ldx(m + row * ld + k0 + kslot<PAIR>(q, e));
+}
+// operand column `col` of a row-major M[k][col], slots over the rows from k0
+template <bool PAIR, class T>
+__device__ __forceinline__ void frag_col(const T* m, int ld, int col, int k0, float* x) {
+  const int q = lane_id() >> 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = ldx(m + (k0 + kslot<PAIR>(q, e)) * ld + col);
+}
+
+// global: 8 consecutive values of row `row` from column k0 + 8q (zero when row >= nvalid)
+template <class T>
+__device__ __forceinline__ void gfrag_row(const T* base, long long ld, int row, int nvalid, int k0,
+                                          float* x) {
+  const int q = lane_id() >> 4;
+  if (row < nvalid) {
+    const T* pr = base + (long long)row * ld + k0 + 8 * q;
+    if constexpr (std::is_same<T, float>::value) {
+      const float4 a = ((const float4*)pr)[0], b = ((const float4*)pr)[1];
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+      x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+      const u32x4 w = *(const u32x4*)pr;
+      unpack8<false>(&w, x);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  }
+}
+// global: column `col`, rows k0 + 8q + e (zero at rows >= nvalid)
+__device__ __forceinline__ void gfrag_col(const float* base, long long ld, int col, int k0,
+                                          int nvalid, float* x) {
+  const int q = lane_id() >> 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int m = k0 + 8 * q + e;
+    x[e] = m < nvalid ? base[(long long)m * ld + col] : 0.f;
+  }
+}
+
+// 4 elements at src (zero when !valid) into LDS
+__device__ __forceinline__ void copy4(float* dst, const float* src, bool valid) {
+  *(float4*)dst = valid ? *(const float4*)src : float4{0.f, 0.f, 0.f, 0.f};
+}
+__device__ __forceinline__ void copy4(bf16_t* dst, const bf16_t* src, bool valid) {
+  *(u32x2*)dst = valid ? *(const u32x2*)src : u32x2{0u, 0u};
+}
+
+// Row sums of a C-layout tile (rows 16 bi + 4q + v, summed over its 16 columns) added
+// into arr[row] (lanes r == 0 write; one lane per row); column sums likewise.
+__device__ __forceinline__ void add_rows(float* arr, int bi, f32x4 x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float s = x[v];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    s += __shfl_xor(s, 8);
+    x[v] = s;
+  }
+  if ((l & 15) == 0) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) arr[16 * bi + 4 * (l >> 4) + v] += x[v];
+  }
+}
+__device__ __forceinline__ void add_cols(float* arr, int bj, f32x4 x) {
+  const int l = lane_id();
+  float s = x[0] + x[1] + x[2] + x[3];
+  s += __shfl_xor(s, 16);
+  s += __shfl_xor(s, 32);
+  if ((l >> 4) == 0) arr[16 * bj + (l & 15)] += s;
+}
+
+__device__ __forceinline__ float wave_sum(float s) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
+  return s;
+}
+
+__device__ __forceinline__ int rec_mode(bool f32) { return f32 ? MODE_F32 : MODE_BF16; }
+
+// ============================================================================ reverse scan
+
+template <int DK, bool F32>
+__global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
+  using KT = typename std::conditional<F32, float, bf16_t>::type;
+  constexpr int LDK = DK + (F32 ? 4 : 8);
+  __shared__ __align__(16) KT sK[C * LDK];
+  __shared__ __align__(16) KT sQ[C * LDK];
+  __shared__ __align__(16) float sDO[C * LDF];
+  __shared__ __align__(16) float sX[C * LDF];
+  __shared__ __align__(16) float sP[C * LDF];
+  __shared__ __align__(16) float sGate[4 * C];
+
+  const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nb = p.nb, wid = blockIdx.x;
+  const int blk = wid % nb, h = (wid / nb) % p.Hv, n = wid / (nb * p.Hv);
+  const int gqa = p.Hv / p.Hk, hk = h / gqa;
+  const int DV = p.DV, col0 = 64 * blk, c = 16 * wave;
+  long long s0, s1;
+  seq_range(p.cu_seqlens, n, p.T, s0, s1);
+  const int nchunks = (int)((s1 - s0 + C - 1) / C);
+  const int cbase = p.chunk_off ? p.chunk_off[n] : n * p.nch;
+  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32));
+  const long long rs = (long long)p.Hv * DV;  // row stride of dO / dV_new
+
+  // dS[t][v] = dS[16t + 4lq + v][col0 + c + lr]: gradient of the state leaving the chunk
+  f32x4 dS[DK / 16];
+  const size_t st_off = ((size_t)n * p.Hv + h) * DK * DV + col0 + c + lr;
+#pragma unroll
+  for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      dS[t][v] = p.dht ? p.dht[st_off + (size_t)(16 * t + 4 * lq + v) * DV] : 0.f;
+
+  for (int j = nchunks - 1; j >= 0; --j) {
+    const long long t0 = s0 + (long long)j * C;
+    const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
+    const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
+    __syncthreads();  // the previous chunk's readers are done
+    // ---------------------------------------------------------------- stage
+    for (int it = tid; it < 2 * C * (DK / 4); it += NT) {
+      const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
+      const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
+      const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
+                      (long long)hk * DK + c4;
+      copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
+    }
+    for (int it = tid; it < C * 16; it += NT) {
+      const int row = it >> 4, c4 = 4 * (it & 15);
+      const float* src = p.dO + (t0 + (row < nvalid ? row : 0)) * rs + (long long)h * DV + col0 + c4;
+      copy4(sDO + row * LDF + c4, src, row < nvalid);
+    }
+    const float* xb = p.xlpg + ((size_t)slot * p.Hv + h) * kXlpgFloats;
+    for (int it = tid; it < 2 * C * 16; it += NT) {
+      const int which = it / (C * 16), rem = it % (C * 16);
+      const int row = rem >> 4, c4 = 4 * (rem & 15);
+      copy4((which ? sP : sX) + row * LDF + c4, xb + (which ? kXlpgP : kXlpgX) + row * C + c4, true);
+    }
+    sGate[tid] = ((const float*)(p.rec + ((size_t)slot * p.Hv + h) * rec_stride + kRecG))[tid];
+    __syncthreads();
+    const float* sEG = sGate + kGateEG * C;
+    const float* sEGS = sGate + kGateEGS * C;
+    const float* sEL = sGate + kGateEL * C;  // e^{G_last - G}; e^{G_last} in the last slot
+    const float* sB = sGate + kGateBeta * C;
+
+    // gradient of the state leaving chunk j, for the chunk-local gradients
+    {
+      float* dd = p.dstates + ((size_t)slot * p.Hv + h) * DK * DV + col0 + c + lr;
+#pragma unroll
+      for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) dd[(size_t)(16 * t + 4 * lq + v) * DV] = dS[t][v];
+    }
+
+    // ---------------------------------------------------------------- K dS
+    Op dsb[DK / 32];
+#pragma unroll
+    for (int s = 0; s < DK / 32; ++s) dsb[s] = join_op(dS[2 * s], dS[2 * s + 1]);
+    f32x4 kds[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < DK / 32; ++s) {
+        float x[8];
+        frag_row<true>(sK, LDK, 16 * i + lr, 32 * s, x);
+        acc = mm3<F32, true>(acc, split8<F32>(x), dsb[s]);
+      }
+      kds[i] = acc;
+    }
+    // ---------------------------------------------------------------- dV_new = P^T dO + e^{G_last-G} K dS
+    f32x4 dvn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int p2 = i / 2; p2 < 2; ++p2) {  // P^T is upper triangular
+        float a[8], b[8];
+        frag_col<false>(sP, LDF, 16 * i + lr, 32 * p2, a);
+        frag_col<false>(sDO, LDF, c + lr, 32 * p2, b);
+        acc = mm3<true, true>(acc, split8(a), split8(b));
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * i + 4 * lq + v;
+        const float el = row == C - 1 ? 1.f : sEL[row];
+        dvn[i][v] = acc[v] + el * kds[i][v];
+      }
+    }
+    {
+      float* dd = p.dvnew + t0 * rs + (long long)h * DV + col0 + c + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (16 * i + 4 * lq + v < nvalid) dd[(long long)(16 * i + 4 * lq + v) * rs] = dvn[i][v];
+    }
+    // ---------------------------------------------------------------- Y = diag(beta) X^T dV_new
+    Op dvp[2];
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) dvp[pp] = join_op(dvn[2 * pp], dvn[2 * pp + 1]);
+    f32x4 y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int p2 = i / 2; p2 < 2; ++p2) {  // X^T is upper triangular
+        float a[8];
+        frag_col<true>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        acc = mm3<true, true>(acc, split8(a), dvp[p2]);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) y[i][v] = sB[16 * i + 4 * lq + v] * acc[v];
+    }
+    // ---------------------------------------------------------------- dS update
+    Op b1[2], b2[2];
+#pragma unroll
+    for (int p2 = 0; p2 < 2; ++p2) {
+      float x[8];
+      frag_col<false>(sDO, LDF, c + lr, 32 * p2, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= sEGS[32 * p2 + 8 * lq + e];
+      b1[p2] = split8(x);
+      f32x4 ya, yb;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        ya[v] = -sEG[32 * p2 + 4 * lq + v] * y[2 * p2][v];
+        yb[v] = -sEG[32 * p2 + 16 + 4 * lq + v] * y[2 * p2 + 1][v];
+      }
+      b2[p2] = join_op(ya, yb);
+    }
+    const float egl = sEL[C - 1];
+#pragma unroll
+    for (int t = 0; t < DK / 16; ++t) {
+      f32x4 acc;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[v] = egl * dS[t][v];
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        float a[8];
+        frag_col<false>(sQ, LDK, 16 * t + lr, 32 * p2, a);
+        acc = mm3<F32, true>(acc, split8<F32>(a), b1[p2]);
+        frag_col<true>(sK, LDK, 16 * t + lr, 32 * p2, a);
+        acc = mm3<F32, true>(acc, split8<F32>(a), b2[p2]);
+      }
+      dS[t] = acc;
+    }
+  }
+  if (p.dh0) {
+#pragma unroll
+    for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) p.dh0[st_off + (size_t)(16 * t + 4 * lq + v) * DV] = dS[t][v];
+  }
+}
+
+// ============================================================================ chunk-local gradients
+
+template <int DK, int DV, bool F32>
+__global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
+  using KT = typename std::conditional<F32, float, bf16_t>::type;
+  using In = KT;  // v has the input precision too
+  constexpr int LDK = DK + (F32 ? 4 : 8);
+  constexpr int LDW = DK + 4;
+  constexpr int NCB = DK / 16, NKB = (NCB + 3) / 4;  // dk column blocks; per wavefront
+  constexpr int NVB = DV / 16, NVW = (NVB + 3) / 4;  // dv column blocks; per wavefront
+  __shared__ __align__(16) KT sK[C * LDK];
+  __shared__ __align__(16) KT sQ[C * LDK];
+  __shared__ __align__(16) float sX[C * LDF];
+  __shared__ __align__(16) float sDW[C * LDW];
+  __shared__ __align__(16) float sDX[C * LDF];
+  __shared__ __align__(16) float sDP[C * LDF];
+  __shared__ __align__(16) float sM[C * LDF];
+  __shared__ float sG[C], sBt[C];
+  // per-wavefront partial row / column sums (deterministic: one writer per entry at a time)
+  __shared__ float sRowG[4][C], sColG[4][C], sRowB[4][C], sRowT[4][C], sRP[4][C];
+  __shared__ float sRed[4];
+
+  const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int Hv = p.Hv, h = blockIdx.x % Hv, ci = blockIdx.x / Hv;
+  int n, cc;
+  if (p.chunk_off) {
+    if (ci >= p.chunk_off[p.N]) return;
+    int lo = 0, hi = p.N;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.chunk_off[mid] <= ci) lo = mid;
+      else hi = mid;
+    }
+    n = lo;
+    cc = ci - p.chunk_off[lo];
+  } else {
+    n = ci / p.nch;
+    cc = ci % p.nch;
+  }
+  long long s0, s1;
+  seq_range(p.cu_seqlens, n, p.T, s0, s1);
+  const long long t0 = s0 + (long long)cc * C;
+  const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
+  if (nvalid <= 0) return;
+  const int gqa = Hv / p.Hk, hk = h / gqa;
+  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32));
+  const float* xb = p.xlpg + ((size_t)ci * Hv + h) * kXlpgFloats;
+  const float* Sg = p.states + ((size_t)ci * Hv + h) * DK * DV;
+  const float* dSg = p.dstates + ((size_t)ci * Hv + h) * DK * DV;
+  const long long rs = (long long)Hv * DV;  // row stride of dO, V_new, dV_new, v
+  const float* dOb = p.dO + t0 * rs + (long long)h * DV;
+  const float* Vnb = p.vnew + t0 * rs + (long long)h * DV;
+  const float* dVnb = p.dvnew + t0 * rs + (long long)h * DV;
+  const In* vb = (const In*)p.v + t0 * rs + (long long)h * DV;
+  const float scale = p.scale;
+
+  // ---------------------------------------------------------------- stage
+  for (int it = tid; it < 2 * C * (DK / 4); it += NT) {
+    const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
+    const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
+    const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
+                    (long long)hk * DK + c4;
+    copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
+  }
+  for (int it = tid; it < C * 16; it += NT) {
+    const int row = it >> 4, c4 = 4 * (it & 15);
+    copy4(sX + row * LDF + c4, xb + kXlpgX + row * C + c4, true);
+  }
+  if (tid < C) {
+    sG[tid] = xb[kXlpgG + tid];
+    sBt[tid] = ((const float*)(p.rec + ((size_t)ci * Hv + h) * rec_stride + kRecG))[kGateBeta * C + tid];
+  }
+  {
+    const int w = tid >> 6;
+    sRowG[w][l] = 0.f;
+    sColG[w][l] = 0.f;
+    sRowB[w][l] = 0.f;
+    sRowT[w][l] = 0.f;
+    sRP[w][l] = 0.f;
+  }
+  __syncthreads();
+
+  const float Gl = sG[C - 1];
+  auto eg = [&](int row) { return __expf(sG[row]); };
+  auto el = [&](int row) { return row == C - 1 ? 1.f : __expf(Gl - sG[row]); };
+  auto gam = [&](int row, int col) {
+    return row >= col ? __expf(fminf(sG[row] - sG[col], 0.f)) : 0.f;
+  };
+  float* rowG = sRowG[wave];
+  float* colG = sColG[wave];
+  float* rowB = sRowB[wave];
+  float* rowT = sRowT[wave];
+  float* rP = sRP[wave];
+
+  // dq, dk accumulators of the wavefront's dk column blocks cb = wave + 4 kb
+  f32x4 dq[NKB][4], dk[NKB][4];
+
+  // ---------------------------------------------------------------- products over dv
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int cb = wave + 4 * kb;
+    if (cb >= NCB) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 x1 = zero4(), dkd = zero4(), dw = zero4();
+#pragma unroll
+      for (int u = 0; u < DV / 32; ++u) {
+        float a[8], b[8];
+        gfrag_row(Sg, DV, 16 * cb + lr, DK, 32 * u, b);
+        const Op bs = split8(b);
+        gfrag_row(dOb, rs, 16 * i + lr, nvalid, 32 * u, a);
+        x1 = mm3<true, true>(x1, split8(a), bs);           // dO S^T
+        gfrag_row(dVnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+        dw = mm3<true, true>(dw, split8(a), bs);           // dV_new S^T
+        gfrag_row(dSg, DV, 16 * cb + lr, DK, 32 * u, b);
+        gfrag_row(Vnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+        dkd = mm3<true, true>(dkd, split8(a), split8(b));  // V_new dS^T
+      }
+      f32x4 gx, rr;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * i + 4 * lq + v, col = 16 * cb + lr;
+        x1[v] *= eg(row);                                  // X1 = diag(e^G) dO S^T
+        gx[v] = scale * ldx(sQ + row * LDK + col) * x1[v];
+        const float e = el(row);
+        rr[v] = dkd[v] * ldx(sK + row * LDK + col) * e;    // dkdec * kdec
+        dkd[v] *= e;
+        sDW[row * LDW + col] = -dw[v];                     // dW = -dV_new S^T
+      }
+      dq[kb][i] = x1;
+      dk[kb][i] = dkd;
+      add_rows(rowG, i, gx);
+      add_rows(rP, i, rr);
+    }
+  }
+  // dP = (dO V_new^T) * tril, row block `wave`; dXa = dV_new v^T
+  f32x4 dxa[4];
+  {
+    const int bi = wave;
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4 dp = zero4(), xa = zero4();
+#pragma unroll
+      for (int u = 0; u < DV / 32; ++u) {
+        float a[8], b[8];
+        gfrag_row(vb, rs, 16 * bj + lr, nvalid, 32 * u, b);
+        gfrag_row(dVnb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+        xa = mm3<true, F32>(xa, split8(a), split8<F32>(b));
+        if (bj <= bi) {
+          gfrag_row(Vnb, rs, 16 * bj + lr, nvalid, 32 * u, b);
+          gfrag_row(dOb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+          dp = mm3<true, true>(dp, split8(a), split8(b));
+        }
+      }
+      dxa[bj] = xa;
+      f32x4 pdp;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
+        const float d = row >= col ? dp[v] : 0.f;
+        pdp[v] = d * xb[kXlpgP + row * C + col];
+        sDP[row * LDF + col] = d * gam(row, col);          // dPg = dP * Gamma
+      }
+      add_rows(rowG, bi, pdp);
+      add_cols(colG, bj, -pdp);
+    }
+  }
+  // sum of dS_end * S over the state (the e^{G_last} S term of the state update)
+  {
+    float sds = 0.f;
+    for (int it = tid; it < DK * DV / 4; it += NT) {
+      const float4 a = ((const float4*)Sg)[it], b = ((const float4*)dSg)[it];
+      sds += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+    }
+    sds = wave_sum(sds);
+    if (l == 0) sRed[wave] = sds;
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- dX = dU vb^T + dW kbe^T
+  {
+    const int bi = wave;
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int s = 0; s < DK / 32; ++s) {
+        float a[8], b[8];
+        frag_row<false>(sDW, LDW, 16 * bi + lr, 32 * s, a);
+        frag_row<false>(sK, LDK, 16 * bj + lr, 32 * s, b);
+        acc = mm3<true, F32>(acc, split8(a), split8<F32>(b));
+      }
+      const int col = 16 * bj + lr;
+      const float bc = sBt[col], ec = eg(col);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * bi + 4 * lq + v;
+        sDX[row * LDF + col] = bc * (dxa[bj][v] + ec * acc[v]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- dvb = X^T dU, dkbe = X^T dW
+#pragma unroll
+  for (int kv = 0; kv < NVW; ++kv) {
+    const int cv = wave + 4 * kv;
+    if (cv >= NVB) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int p2 = i / 2; p2 < 2; ++p2) {
+        float a[8], b[8];
+        frag_col<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        gfrag_col(dVnb, rs, 16 * cv + lr, 32 * p2, nvalid, b);
+        acc = mm3<true, true>(acc, split8(a), split8(b));
+      }
+      f32x4 vd;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * i + 4 * lq + v, col = 16 * cv + lr;
+        const float vv = row < nvalid ? ldx(vb + (long long)row * rs + col) : 0.f;
+        vd[v] = vv * acc[v];
+        const float dvv = sBt[row] * acc[v];
+        if (row < nvalid) {
+          if constexpr (F32) ((float*)p.dv)[(t0 + row) * rs + (long long)h * DV + col] = dvv;
+          else ((bf16_t*)p.dv)[(t0 + row) * rs + (long long)h * DV + col] = f2bf(dvv);
+        }
+      }
+      add_rows(rowB, i, vd);
+    }
+  }
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int cb = wave + 4 * kb;
+    if (cb >= NCB) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int p2 = i / 2; p2 < 2; ++p2) {
+        float a[8], b[8];
+        frag_col<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        frag_col<false>(sDW, LDW, 16 * cb + lr, 32 * p2, b);
+        acc = mm3<true, true>(acc, split8(a), split8(b));
+      }
+      f32x4 kt;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * i + 4 * lq + v, col = 16 * cb + lr;
+        kt[v] = ldx(sK + row * LDK + col) * acc[v];
+        dk[kb][i][v] += sBt[row] * eg(row) * acc[v];
+      }
+      add_rows(rowT, i, kt);
+    }
+  }
+  // M1 = X^T dX, row block `wave` (read back only by this wavefront)
+  {
+    const int bi = wave;
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4 acc = zero4();
+      for (int p2 = bi / 2; p2 < 2; ++p2) {  // X^T is upper triangular
+        float a[8], b[8];
+        frag_col<false>(sX, LDF, 16 * bi + lr, 32 * p2, a);
+        frag_col<false>(sDX, LDF, 16 * bj + lr, 32 * p2, b);
+        acc = mm3<true, true>(acc, split8(a), split8(b));
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sM[(16 * bi + 4 * lq + v) * LDF + 16 * bj + lr] = acc[v];
+    }
+  }
+  wave_lds_fence();
+  // ---------------------------------------------------------------- dL = -strict_lower(M1 X^T)
+  {
+    const int bi = wave;
+    f32x4 dl[4];
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4 acc = zero4();
+      if (bj <= bi) {
+#pragma unroll
+        for (int p2 = 0; p2 <= bj / 2; ++p2) {
+          float a[8], b[8];
+          frag_row<false>(sM, LDF, 16 * bi + lr, 32 * p2, a);
+          frag_row<false>(sX, LDF, 16 * bj + lr, 32 * p2, b);
+          acc = mm3<true, true>(acc, split8(a), split8(b));
+        }
+      }
+      dl[bj] = acc;
+    }
+    wave_lds_fence();  // every read of M1 is complete before its rows are overwritten
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) {
+      f32x4 lb, ld;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
+        const float d = row > col ? -dl[bj][v] : 0.f;
+        const float lg = xb[kXlpgLg + row * C + col];
+        lb[v] = d * lg;
+        ld[v] = d * sBt[row] * lg;                      // dL * L
+        sM[row * LDF + col] = sBt[row] * d * gam(row, col);  // Qm = diag(beta) (dL * Gamma)
+      }
+      add_rows(rowB, bi, lb);
+      add_rows(rowG, bi, ld);
+      add_cols(colG, bj, -ld);
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- (Qm + Qm^T) k, dPg^T qs, dPg k
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int cb = wave + 4 * kb;
+    if (cb >= NCB) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 a_k = dk[kb][i], a_q = dq[kb][i], a_t = zero4();
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        float a[8], b[8];
+        frag_col<false>(sK, LDK, 16 * cb + lr, 32 * p2, b);
+        const Op bk = split8<F32>(b);
+        // symmetric Qm + Qm^T
+        {
+          float x[8], y[8];
+          frag_row<false>(sM, LDF, 16 * i + lr, 32 * p2, x);
+          frag_col<false>(sM, LDF, 16 * i + lr, 32 * p2, y);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] = x[e] + y[e];
+          a_k = mm3<true, F32>(a_k, split8(a), bk);
+        }
+        if (p2 <= i / 2) {  // dPg is lower triangular
+          frag_row<false>(sDP, LDF, 16 * i + lr, 32 * p2, a);
+          a_q = mm3<true, F32>(a_q, split8(a), bk);
+        }
+        if (p2 >= i / 2) {  // dPg^T is upper triangular
+          frag_col<false>(sDP, LDF, 16 * i + lr, 32 * p2, a);
+          frag_col<false>(sQ, LDK, 16 * cb + lr, 32 * p2, b);
+          a_t = mm3<true, F32>(a_t, split8(a), split8<F32>(b));
+        }
+      }
+      float* dqo = p.dqh + (t0 * Hv + h) * (long long)DK;
+      float* dko = p.dkh + (t0 * Hv + h) * (long long)DK;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * i + 4 * lq + v, col = 16 * cb + lr;
+        if (row < nvalid) {
+          dqo[(long long)row * Hv * DK + col] = scale * a_q[v];
+          dko[(long long)row * Hv * DK + col] = a_k[v] + scale * a_t[v];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---------------------------------------------------------------- dG, dbeta, dg
+  if (wave == 0) {
+    const int i = l;
+    float rg = 0.f, rt = 0.f, rb = 0.f, rp = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      rg += sRowG[w][i] + sColG[w][i] - sRP[w][i];
+      rt += sRowT[w][i];
+      rb += sRowB[w][i];
+      rp += sRP[w][i];
+    }
+    const float t = __expf(sG[i]) * rt;
+    float dG = rg + sBt[i] * t;
+    const float db = rb + t;
+    const float rsum = wave_sum(rp);
+    const float sds = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+    if (i == C - 1) dG += rsum + __expf(Gl) * sds;
+    // dg_t = sum_{i >= t} dG_i (G = cumsum(g), deltanet.py:98)
+    float x = dG;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const float y = __shfl_down(x, o);
+      if (i + o < 64) x += y;
+    }
+    if (i < nvalid) {
+      p.dg[(t0 + i) * Hv + h] = x;
+      p.dbeta[(t0 + i) * Hv + h] = db;
+    }
+  }
+}
+
+// ============================================================================ q/k finalisation
+
+// One wavefront per (token, key head) row of dq or dk: the sum over the key head's value
+// heads, then (qk_l2norm) the L2-norm backward dx = r (dy - y (y . dy)), y = x r,
+// r = rsqrt(sum x^2 + 1e-6) (deltanet.py:30-32; the bf16 rounding of y is differentiated
+// as the identity, as autodiff does for a dtype cast).
+template <bool F32>
+__global__ __launch_bounds__(NT) void qk_final_kernel(BwdParams p, long long rows) {
+  using In = typename std::conditional<F32, float, bf16_t>::type;
+  const int l = threadIdx.x & 63;
+  const long long rid = (long long)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+  if (rid >= 2 * rows) return;
+  const int which = (int)(rid / rows);
+  const long long row = rid % rows;
+  const long long token = row / p.Hk;
+  const int hk = (int)(row % p.Hk), dk = p.dk, gqa = p.Hv / p.Hk;
+  const float* src = (which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk;
+  const In* x_in = (const In*)(which ? p.k : p.q) + row * dk;
+  float d[2], x[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int a = l + 64 * e;
+    d[e] = 0.f;
+    x[e] = 0.f;
+    if (a < dk) {
+      for (int g = 0; g < gqa; ++g) d[e] += src[(long long)g * dk + a];
+      x[e] = ldx(x_in + a);
+    }
+  }
+  if (p.qk_l2norm) {
+    const float r = rsqrtf(wave_sum(x[0] * x[0] + x[1] * x[1]) + 1e-6f);
+    const float y0 = x[0] * r, y1 = x[1] * r;
+    const float yd = wave_sum(y0 * d[0] + y1 * d[1]);
+    d[0] = r * (d[0] - y0 * yd);
+    d[1] = r * (d[1] - y1 * yd);
+  }
+  In* out = (In*)(which ? p.dk_out : p.dq) + row * dk;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int a = l + 64 * e;
+    if (a < dk) {
+      if constexpr (F32) out[a] = d[e];
+      else out[a] = f2bf(d[e]);
+    }
+  }
+}
+
+template <int DK, bool F32>
+hipError_t launch_bwd_dk(const BwdParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((rscan_kernel<DK, F32>), dim3((unsigned)(p.N * p.Hv * p.nb)), dim3(NT), 0,
+                     stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const unsigned grid = (unsigned)((long long)p.n_rec * p.Hv);
+  if (grid > 0) {
+    if (p.DV == 128)
+      hipLaunchKernelGGL((cgrad_kernel<DK, 128, F32>), dim3(grid), dim3(NT), 0, stream, p);
+    else
+      hipLaunchKernelGGL((cgrad_kernel<DK, 64, F32>), dim3(grid), dim3(NT), 0, stream, p);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const long long rows = (long long)p.T * (p.cu_seqlens ? 1 : p.N) * p.Hk;
+  if (rows > 0) {
+    const unsigned g2 = (unsigned)((2 * rows + NT / 64 - 1) / (NT / 64));
+    hipLaunchKernelGGL((qk_final_kernel<F32>), dim3(g2), dim3(NT), 0, stream, p, rows);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+}  // namespace
+
+bool bwd_dims_supported(int dk, int dv, bool f32_inputs) {
+  if (dv != 64 && dv != 128) return false;
+  if (f32_inputs) return dk == 32 || dk == 64;
+  return dk == 64 || dk == 128;
+}
+
+hipError_t launch_bwd(const BwdParams& p, hipStream_t stream) {
+  if (p.in_f32) {
+    if (p.dk == 64) return launch_bwd_dk<64, true>(p, stream);
+    if (p.dk == 32) return launch_bwd_dk<32, true>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (p.dk == 128) return launch_bwd_dk<128, false>(p, stream);
+  if (p.dk == 64) return launch_bwd_dk<64, false>(p, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace omx

@@ -84,6 +84,41 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
   return w;
 }
 
+// Workspace of the backward pass: the forward's (records, normalised q/k, chunk
+// offsets), then the prep's fp32 X, Lg, P, G per (chunk slot, value head), the state
+// entering and the state gradient leaving every chunk, V_new and its gradient, and the
+// per-value-head gradients of the normalised q and k.
+struct BwdWs {
+  ChunkWs f;
+  size_t xlpg, states, dstates, vnew, dvnew, dqh, dkh, total;
+};
+
+BwdWs bwd_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
+             int mode) {
+  BwdWs w{};
+  w.f = chunk_ws(B, T, Hk, Hv, dk, dv, N, mode);
+  if (B < 0 || T < 0 || Hk < 0 || Hv < 0 || dk < 0 || dv < 0 || N < 0) return w;
+  const size_t tokens = (size_t)(B * T);
+  const size_t slots = (tokens + 63) / 64 + (size_t)N;
+  size_t o = w.f.total;
+  w.xlpg = o;
+  o += align_up(slots * (size_t)Hv * omx::kXlpgFloatsHost * 4, 256);
+  w.states = o;
+  o += align_up(slots * (size_t)(Hv * dk * dv) * 4, 256);
+  w.dstates = o;
+  o += align_up(slots * (size_t)(Hv * dk * dv) * 4, 256);
+  w.vnew = o;
+  o += align_up(tokens * (size_t)(Hv * dv) * 4, 256);
+  w.dvnew = o;
+  o += align_up(tokens * (size_t)(Hv * dv) * 4, 256);
+  w.dqh = o;
+  o += align_up(tokens * (size_t)(Hv * dk) * 4, 256);
+  w.dkh = o;
+  o += align_up(tokens * (size_t)(Hv * dk) * 4, 256);
+  w.total = o;
+  return w;
+}
+
 int check_heads(const char* fn, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv) {
   REQUIRE(Hk >= 1 && Hv >= 1, "%s: head counts must be positive (Hk=%lld, Hv=%lld)", fn,
           (long long)Hk, (long long)Hv);
@@ -101,7 +136,7 @@ extern "C" {
 
 const char* omx_gdn_last_error(void) { return g_last_error.c_str(); }
 
-int omx_gdn_abi_version(void) { return 101; }
+int omx_gdn_abi_version(void) { return 102; }
 
 int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
                         const float* conv_w, const float* A_log, const float* dt_bias,
@@ -165,8 +200,7 @@ namespace {
 
 // Point the kernels at the workspace and launch: chunk plan (packed sequences),
 // preparation over all chunks, then the scan; all on `stream`, in order.
-hipError_t launch_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int mode,
-                          hipStream_t stream) {
+void setup_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int mode) {
   char* base = (char*)workspace;
   p.nch = (p.T + 63) / 64;
   p.n_rec = p.cu_seqlens ? (int)((p.T + 63) / 64 + p.N) : p.N * p.nch;
@@ -193,6 +227,11 @@ hipError_t launch_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspac
     p.vs = p.v;
     p.vs_ld = p.v_ld;
   }
+}
+
+hipError_t launch_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int mode,
+                          hipStream_t stream) {
+  setup_chunked(p, ws, workspace, mode);
   hipError_t e = hipSuccess;
   if (p.cu_seqlens) e = omx::launch_chunk_plan(p, stream);
   if (e == hipSuccess) e = omx::launch_prep(p, mode, stream);
@@ -325,6 +364,99 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
     e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, eps,
                                   (hipStream_t)stream);
   return launch_status(e, fn);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- backward
+extern "C" {
+
+size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                        int64_t dv, int64_t N, int in_dtype) {
+  return bwd_ws(B, T, Hk, Hv, dk, dv, N,
+                in_dtype == OMX_GDN_F32 ? omx::kModeF32 : omx::kModeBF16).total;
+}
+
+int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
+                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
+                      int64_t N, const float* d_o, const float* d_final_state, void* dq, void* dk,
+                      void* dv, float* dg, float* dbeta, float* d_initial_state, int64_t B,
+                      int64_t T, int64_t Hk, int64_t Hv, int64_t dk_dim, int64_t dv_dim,
+                      int64_t chunk_size, float scale, int qk_l2norm, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  const char* fn = "omx_gdn_chunk_bwd";
+  int rc = check_heads(fn, Hk, Hv, dk_dim, dv_dim);
+  if (rc) return rc;
+  REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
+          in_dtype);
+  REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
+  REQUIRE(B >= 0 && T >= 0, "%s: negative shape (B=%lld, T=%lld)", fn, (long long)B, (long long)T);
+  REQUIRE(B * T <= (int64_t)1 << 31, "%s: too many tokens (%lld)", fn, (long long)(B * T));
+  REQUIRE(std::isfinite(scale), "%s: scale must be finite", fn);
+  if (cu_seqlens) {
+    REQUIRE(B == 1, "%s: cu_seqlens requires batch 1 (got %lld)", fn, (long long)B);
+    REQUIRE(N >= 1 && N <= (1 << 20), "%s: sequence count %lld out of range", fn, (long long)N);
+  } else {
+    REQUIRE(N == B, "%s: without cu_seqlens N must equal B (%lld vs %lld)", fn, (long long)N,
+            (long long)B);
+  }
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  if (!omx::bwd_dims_supported((int)dk_dim, (int)dv_dim, f32))
+    return fail(OMX_GDN_EUNSUPPORTED,
+                "%s: head dims dk=%lld dv=%lld not compiled for %s inputs (bf16: dk 64/128, "
+                "fp32: dk 32/64; dv 64/128)",
+                fn, (long long)dk_dim, (long long)dv_dim, f32 ? "fp32" : "bf16");
+  const int mode = f32 ? omx::kModeF32 : omx::kModeBF16;
+  const BwdWs ws = bwd_ws(B, T, Hk, Hv, dk_dim, dv_dim, N, mode);
+  REQUIRE(workspace_bytes >= ws.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, ws.total);
+  if (N == 0) return ok();
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  if (B * T > 0) {
+    REQUIRE(q && k && v && g && beta && d_o && dq && dk && dv && dg && dbeta,
+            "%s: a required pointer is NULL", fn);
+    REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(d_o, 16),
+            "%s: q, k, v and d_o must be 16-byte aligned", fn);
+  }
+  omx::ChunkParams p{};
+  p.q = q; p.k = k; p.v = v;
+  p.q_ld = Hk * dk_dim; p.k_ld = Hk * dk_dim; p.v_ld = Hv * dv_dim;
+  p.g = g; p.beta = beta; p.o = nullptr;
+  p.initial_state = initial_state; p.final_state = nullptr; p.cu_seqlens = cu_seqlens;
+  p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk_dim;
+  p.DV = (int)dv_dim;
+  p.nb = (int)(dv_dim / omx::chunk_block_cols());
+  p.scale = scale; p.qk_l2norm = qk_l2norm ? 1 : 0;
+  REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
+  REQUIRE(((B * T + 63) / 64 + N) * Hv <= INT32_MAX, "%s: grid too large", fn);
+  char* base = (char*)workspace;
+  setup_chunked(p, ws.f, workspace, mode);
+  p.xlpg = (float*)(base + ws.xlpg);
+  p.states = (float*)(base + ws.states);
+  p.vnew = (float*)(base + ws.vnew);
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (p.cu_seqlens) e = omx::launch_chunk_plan(p, st);
+  if (e == hipSuccess) e = omx::launch_prep_bwd(p, mode, st);
+  if (e == hipSuccess) e = omx::launch_scan_bwd(p, mode, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  omx::BwdParams b{};
+  b.ks = p.ks; b.qs = p.qs; b.ks_ld = p.ks_ld; b.qs_ld = p.qs_ld;
+  b.v = v; b.dO = d_o; b.dht = d_final_state; b.rec = p.rec; b.xlpg = p.xlpg;
+  b.states = p.states; b.vnew = p.vnew;
+  b.dstates = (float*)(base + ws.dstates);
+  b.dvnew = (float*)(base + ws.dvnew);
+  b.dh0 = d_initial_state;
+  b.dqh = (float*)(base + ws.dqh);
+  b.dkh = (float*)(base + ws.dkh);
+  b.dv = dv; b.dg = dg; b.dbeta = dbeta;
+  b.q = q; b.k = k; b.dq = dq; b.dk_out = dk;
+  b.cu_seqlens = cu_seqlens; b.chunk_off = p.chunk_off;
+  b.N = p.N; b.T = p.T; b.Hk = p.Hk; b.Hv = p.Hv; b.dk = p.dk; b.DV = p.DV; b.nb = p.nb;
+  b.nch = p.nch; b.n_rec = p.n_rec; b.in_f32 = f32 ? 1 : 0; b.qk_l2norm = p.qk_l2norm;
+  b.scale = scale;
+  return launch_status(omx::launch_bwd(b, st), fn);
 }
 
 }  // extern "C"

@@ -262,7 +262,9 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                      (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
 }
 
-template <int DK, int MODE>
+// BWD (the backward pass's recompute): stores the state entering every chunk and V_new
+// instead of o.
+template <int DK, int MODE, bool BWD = false>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
 // SIMD) instead of holding back for a second workgroup.
@@ -424,6 +426,15 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     }
     }
 
+    if constexpr (BWD) {
+      // the state entering chunk j, for the backward pass
+      const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
+      float* sd = p.states + ((size_t)slot * p.Hv + h) * DK * DV + col0 + 16 * wave + lr;
+#pragma unroll
+      for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sd[(size_t)state_row(t, lq, v) * DV] = S[t][v];
+    }
     // ------------------------------------------------------------ K S, Q S, right-hand side
     // The B operand of K S and Q S over dk block s2 is the state itself: lane (q, r)
     // holds tiles 2 s2 and 2 s2 + 1, dk 32 s2 + 8q + (0..7) of column r (the state's
@@ -536,6 +547,14 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
       __builtin_amdgcn_sched_group_barrier(0x002, 80, 1);
       __builtin_amdgcn_sched_group_barrier(0x008, 18, 1);
     }
+    if constexpr (BWD) {
+      float* vd = p.vnew + ((size_t)t0 * p.Hv + h) * DV + col0 + 16 * wave + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (16 * i + 4 * lq + v < nvalid) vd[(size_t)(16 * i + 4 * lq + v) * p.Hv * DV] = U[i][v];
+    }
     u32x4 Uh[2], Ul[2];  // bf16 hi/lo of V_new block pairs as B operands
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
@@ -607,6 +626,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     // both operand layouts hold "row r, contraction slots 8q .. 8q+7".  Lane (q, r) then
     // holds token 16i + r, columns 16w + 4q .. +3 of the wave's slice: one 16-byte (fp32)
     // or 8-byte (bf16) store per row block, and one gate factor per lane.
+    if constexpr (BWD) return;
     f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -725,10 +745,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
   }
 }
 
-template <int DK, int MODE>
+template <int DK, int MODE, bool BWD = false>
 hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
   const unsigned grid = (unsigned)(p.N * p.Hv * p.nb);
-  hipLaunchKernelGGL((scan_kernel<DK, MODE>), dim3(grid), dim3(Cfg<DK, MODE>::NTH), 0, stream, p);
+  hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD>), dim3(grid), dim3(Cfg<DK, MODE>::NTH), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -745,6 +765,19 @@ bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
 }
 
 bool layer_dims_supported(int dk, int dv) { return chunk_dims_supported(dk, dv, false); }
+
+hipError_t launch_scan_bwd(const ChunkParams& p, int mode, hipStream_t stream) {
+  if (mode == MODE_F32) {
+    if (p.dk == 64) return launch_scan_cfg<64, MODE_F32, true>(p, stream);
+    if (p.dk == 32) return launch_scan_cfg<32, MODE_F32, true>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (mode == MODE_BF16) {
+    if (p.dk == 128) return launch_scan_cfg<128, MODE_BF16, true>(p, stream);
+    if (p.dk == 64) return launch_scan_cfg<64, MODE_BF16, true>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream) {
   if (mode == MODE_F32) {

@@ -78,7 +78,45 @@ struct ChunkParams {
   const void* qs;
   const void* vs;
   long long ks_ld, qs_ld, vs_ld;
+  // backward pass only (the backward variants of the two kernels write them)
+  float* xlpg;                 // prep: per (chunk slot, value head) X, Lg, P [64][64], G [64]
+  float* states;               // scan: the state entering each chunk [slot][Hv][dk][DV]
+  float* vnew;                 // scan: V_new [tokens][Hv][DV]
 };
+
+// Backward pass of the chunked rule (gdn_bwd.hip): the reverse state-gradient scan,
+// the chunk-parallel gradients and the q/k finalisation.
+struct BwdParams {
+  const void* ks;              // normalised (or raw) k rows [tokens][*][dk], input precision
+  const void* qs;
+  long long ks_ld, qs_ld;
+  const void* v;               // [tokens][Hv][DV], input precision
+  const float* dO;             // [tokens][Hv][DV]
+  const float* dht;            // [N][Hv][dk][DV] or null
+  const unsigned char* rec;    // prep records
+  const float* xlpg;           // prep backward extras
+  const float* states;         // state entering each chunk
+  const float* vnew;           // V_new
+  float* dstates;              // gradient of the state leaving each chunk [slot][Hv][dk][DV]
+  float* dvnew;                // gradient of V_new [tokens][Hv][DV]
+  float* dh0;                  // [N][Hv][dk][DV] or null
+  float* dqh;                  // per value head gradient of the normalised q [tokens][Hv][dk]
+  float* dkh;                  // likewise k
+  void* dv;                    // [tokens][Hv][DV], input precision
+  float* dg;                   // [tokens][Hv]
+  float* dbeta;                // [tokens][Hv]
+  const void* q;               // raw q, k [tokens][Hk][dk] (L2-norm backward)
+  const void* k;
+  void* dq;                    // [tokens][Hk][dk], input precision
+  void* dk_out;
+  const int32_t* cu_seqlens;
+  const int32_t* chunk_off;
+  int N, T, Hk, Hv, dk, DV, nb, nch, n_rec, in_f32, qk_l2norm;
+  float scale;
+};
+
+// floats of the backward extras per (chunk slot, value head): X, Lg, P [64][64], G [64]
+constexpr int kXlpgFloatsHost = 3 * 64 * 64 + 64;
 
 // kernel modes of the chunked prefill (template arguments of both kernels)
 constexpr int kModeBF16 = 0, kModeF32 = 1, kModeLayer = 2;
@@ -92,6 +130,11 @@ int chunk_record_bytes(int mode);
 hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);
 hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream);
 hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream);
+// backward variants: the prep also writes xlpg, the scan writes states and vnew (no o)
+hipError_t launch_prep_bwd(const ChunkParams& p, int mode, hipStream_t stream);
+hipError_t launch_scan_bwd(const ChunkParams& p, int mode, hipStream_t stream);
+bool bwd_dims_supported(int dk, int dv, bool f32_inputs);
+hipError_t launch_bwd(const BwdParams& p, hipStream_t stream);
 
 // Gated RMSNorm of the layer prefill from bf16 o: out = w * o * rsqrt(mean(o^2) + eps)
 // * silu(z) per (token, value head) row of dv (dv / 8 at most 32).

@@ -323,7 +323,16 @@ __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTa
 template <int MODE>
 constexpr int prep_min_blocks() { return MODE == MODE_LAYER ? 3 : 2; }
 
-template <int DK, int MODE>
+// A-layout 16x16 fp32 tile (lane (q, r) holds M[16 bi + r][16 bj + 4q .. +3]) into a
+// row-major 64x64 matrix
+__device__ __forceinline__ void put_f32_tile(float* m, int bi, int bj, f32x4 a) {
+  const int l = lane_id();
+  *(float4*)(m + (16 * bi + (l & 15)) * kC + 16 * bj + 4 * (l >> 4)) = float4{a[0], a[1], a[2], a[3]};
+}
+
+// BWD: also writes, per (chunk, value head), the fp32 matrices the backward pass reads
+// (X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in gdn_chunk.h).
+template <int DK, int MODE, bool BWD = false>
 __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
@@ -467,6 +476,16 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
     for (int gg = 0; gg < gqa; ++gg) {
       const int h = hk * gqa + gg;
       const auto rec = buf_rsrc(p.rec + ((size_t)ci * p.Hv + h) * rec_stride, (unsigned)rec_stride);
+      float* xb = BWD ? p.xlpg + ((size_t)ci * p.Hv + h) * kXlpgFloats : nullptr;
+      if constexpr (BWD) {
+        // the upper tiles of X, Lg and P are zero
+        for (int z = wave; z < 18; z += 4) {
+          const int mat = z / 6, u = z % 6;
+          const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2);
+          const int bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
+          put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
+        }
+      }
 
       // gates of value head h, one token per lane; every wave scans its own copy
       {
@@ -492,6 +511,8 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           bt = round_bf(sigmoidf_(bt)) * keep;
         }
         const float G = wave_scan_dpp(g);
+        if constexpr (BWD)
+          if (wave == 0) xb[kXlpgG + l] = G;
         const float Gl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(G), 63));
         const float eg = __expf(G);
         gw[l] = G * 1.4426950408889634f;
@@ -525,10 +546,21 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           const float bt = gw[C + i];
           // branch-free: the exponent is clamped to <= 0 (masked entries would
           // overflow) and the strictly-lower mask multiplies the result
-  #pragma unroll
+          if constexpr (BWD) {
+            f32x4 lg;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int m = 16 * bj + 4 * lq + v;
+              lg[v] = acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i > m);
+              val[v] = bt * lg[v];
+            }
+            put_f32_tile(xb + kXlpgLg, bi, bj, lg);
+          } else {
+#pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int m = 16 * bj + 4 * lq + v;
             val[v] = bt * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i > m);
+          }
           }
           if (ti == 0) {
             // The diagonal block.  With N = -L_ww (strictly lower, so N^16 = 0),
@@ -578,6 +610,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             // the record holds T diag(beta): column 16 bi + 4 lq + v scaled by its beta
             const f32x4 Tb = Ta * col_beta(gw, bi);
             put_tile(rec, rec_t_off(bi, bi), pack_hi4(Tb));
+            if constexpr (BWD) put_f32_tile(xb + kXlpgX, bi, bi, Ta);
             put_tile(rec, rec_t_off(bi, bi) + kPairBytes, pack_lo4(Tb));
             if ((bi & 1) == 0) {
               // the zero upper tile (bi, bi + 1) that completes row block bi's last pair
@@ -600,6 +633,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             val[v] = sc * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i >= m);
           }
           put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
+          if constexpr (BWD) put_f32_tile(xb + kXlpgP, bi, bj, val);
           if constexpr (IS) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
         }
       }
@@ -637,6 +671,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           Tl[i] = pack_lo4(Tij);
           const f32x4 Tb = TijT * col_beta(gw, j);  // T_ij diag(beta), A layout
           put_tile(rec, rec_t_off(i, j), pack_hi4(Tb));
+          if constexpr (BWD) put_f32_tile(xb + kXlpgX, i, j, TijT);
           put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(Tb));
         }
       }
@@ -659,7 +694,7 @@ int device_cus() {
   return cus[dev];
 }
 
-template <int DK, int MODE>
+template <int DK, int MODE, bool BWD = false>
 hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
   // persistent (core modes): two workgroups per compute unit walk the tasks, each
   // prefetching its next task while it computes the current one
@@ -667,7 +702,7 @@ hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
   if (tasks == 0) return hipSuccess;
   const long long cap = prep_persistent<MODE>() ? (long long)prep_min_blocks<MODE>() * device_cus() : tasks;
   const unsigned grid = (unsigned)(tasks < cap ? tasks : cap);
-  hipLaunchKernelGGL((prep_kernel<DK, MODE>), dim3(grid), dim3(NT), 0, stream, p);
+  hipLaunchKernelGGL((prep_kernel<DK, MODE, BWD>), dim3(grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -711,6 +746,19 @@ hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p.cu_seqlens, p.N, p.T,
                      p.chunk_off);
   return hipGetLastError();
+}
+
+hipError_t launch_prep_bwd(const ChunkParams& p, int mode, hipStream_t stream) {
+  if (mode == MODE_F32) {
+    if (p.dk == 64) return launch_prep_cfg<64, MODE_F32, true>(p, stream);
+    if (p.dk == 32) return launch_prep_cfg<32, MODE_F32, true>(p, stream);
+    return hipErrorInvalidValue;
+  }
+  if (mode == MODE_BF16) {
+    if (p.dk == 128) return launch_prep_cfg<128, MODE_BF16, true>(p, stream);
+    if (p.dk == 64) return launch_prep_cfg<64, MODE_BF16, true>(p, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream) {

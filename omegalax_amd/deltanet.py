@@ -17,7 +17,8 @@ import torch
 from . import _lib
 
 __all__ = [
-    "chunk_gated_delta_rule", "recurrent_gated_delta_rule_step", "gdn_prefill",
+    "chunk_gated_delta_rule", "chunk_gated_delta_rule_bwd", "recurrent_gated_delta_rule_step",
+    "gdn_prefill",
     "gdn_decode_step", "GDNError",
 ]
 
@@ -81,17 +82,7 @@ def _workspace(nbytes, device):
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
-def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=64, *,
-                           initial_state=None, output_final_state=False, cu_seqlens=None,
-                           scale=None, use_qk_l2norm=True):
-    """Chunked gated delta rule (deltanet.py:53-153) on libomx_gdn.
-
-    q/k [B,T,Hk,A] and v [B,T,H,U] (bf16 or fp32, same dtype); Hk may divide H
-    (GQA, repeat-interleave semantics of deltanet.py:272-280) or equal it.
-    g/beta [B,T,H].  Returns o [B,T,H,U] fp32, or (o, final_state) when
-    ``output_final_state``.  ``cu_seqlens`` (int32 [N+1], B == 1) packs N
-    sequences; ``initial_state`` is [N or B, H, A, U] fp32.
-    """
+def _prep_inputs(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seqlens):
     q, k, v = q_BTHA.contiguous(), k_BTHA.contiguous(), v_BTHU.contiguous()
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, v must share a dtype")
@@ -107,6 +98,14 @@ def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=6
         initial_state = _f32(initial_state)
         if tuple(initial_state.shape) != (N, H, A, U):
             raise ValueError(f"initial_state must be {(N, H, A, U)}, got {tuple(initial_state.shape)}")
+    return q, k, v, g, beta, initial_state, dev, (B, T, Hk, A, H, U, N)
+
+
+def _chunk_fwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size, initial_state,
+               output_final_state, cu_seqlens, scale, use_qk_l2norm):
+    q, k, v, g, beta, initial_state, dev, dims = _prep_inputs(
+        q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seqlens)
+    B, T, Hk, A, H, U, N = dims
     o = torch.empty((B, T, H, U), dtype=torch.float32, device=dev)
     fs = torch.empty((N, H, A, U), dtype=torch.float32, device=dev) if output_final_state else None
     sc = float(A ** -0.5) if scale is None else float(scale)
@@ -116,6 +115,99 @@ def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=6
     _lib.call("omx_gdn_chunk_fwd", _ptr(q), _ptr(k), _ptr(v), _dtype_code(q), _ptr(g), _ptr(beta),
               _ptr(initial_state), _ptr(cu_seqlens), N, _ptr(o), _ptr(fs), B, T, Hk, H, A, U,
               int(chunk_size), sc, int(bool(use_qk_l2norm)), _ptr(ws), ws_bytes, _stream(dev))
+    return o, fs
+
+
+def chunk_gated_delta_rule_bwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, do_BTHU, chunk_size=64, *,
+                               initial_state=None, d_final_state=None, cu_seqlens=None,
+                               scale=None, use_qk_l2norm=True):
+    """Gradients of ``chunk_gated_delta_rule`` at its inputs (the VJP JAX takes of
+    deltanet.py:53-153 when the reference trains through it), on libomx_gdn.
+
+    ``do_BTHU`` [B,T,H,U] is the cotangent of o, ``d_final_state`` [N,H,A,U] that of the
+    final state (None = zeros).  Returns (dq, dk, dv, dg, dbeta, d_initial_state): dq/dk
+    [B,T,Hk,A] and dv at the input dtype (gradients of the raw q/k, through the L2 norm
+    and summed over each key head's value heads), dg/dbeta [B,T,H] fp32,
+    d_initial_state [N,H,A,U] fp32.
+    """
+    q, k, v, g, beta, initial_state, dev, dims = _prep_inputs(
+        q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seqlens)
+    B, T, Hk, A, H, U, N = dims
+    do = _f32(do_BTHU)
+    _dev(do, d_final_state)
+    if tuple(do.shape) != (B, T, H, U):
+        raise ValueError(f"do must be {(B, T, H, U)}, got {tuple(do.shape)}")
+    if d_final_state is not None:
+        d_final_state = _f32(d_final_state)
+        if tuple(d_final_state.shape) != (N, H, A, U):
+            raise ValueError(f"d_final_state must be {(N, H, A, U)}")
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dg = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    db = torch.empty((B, T, H), dtype=torch.float32, device=dev)
+    dh0 = torch.empty((N, H, A, U), dtype=torch.float32, device=dev)
+    sc = float(A ** -0.5) if scale is None else float(scale)
+    L = _lib.lib()
+    ws_bytes = L.omx_gdn_chunk_bwd_workspace_size(B, T, Hk, H, A, U, N, _dtype_code(q))
+    ws = _workspace(ws_bytes, dev)
+    _lib.call("omx_gdn_chunk_bwd", _ptr(q), _ptr(k), _ptr(v), _dtype_code(q), _ptr(g), _ptr(beta),
+              _ptr(initial_state), _ptr(cu_seqlens), N, _ptr(do), _ptr(d_final_state), _ptr(dq),
+              _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _ptr(dh0), B, T, Hk, H, A, U,
+              int(chunk_size), sc, int(bool(use_qk_l2norm)), _ptr(ws), ws_bytes, _stream(dev))
+    return dq, dk, dv, dg, db, dh0
+
+
+class _ChunkGatedDeltaRule(torch.autograd.Function):
+    """Autograd node of the chunked rule: forward omx_gdn_chunk_fwd, backward
+    omx_gdn_chunk_bwd (the forward is recomputed there, as under the reference's remat,
+    model.py:202)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, cu_seqlens, chunk_size, scale,
+                use_qk_l2norm):
+        o, fs = _chunk_fwd(q, k, v, g, beta, chunk_size, initial_state, True, cu_seqlens, scale,
+                           use_qk_l2norm)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, cu_seqlens)
+        ctx.cfg = (chunk_size, scale, use_qk_l2norm)
+        ctx.set_materialize_grads(False)
+        return o, fs
+
+    @staticmethod
+    def backward(ctx, do, dfs):
+        q, k, v, g, beta, initial_state, cu_seqlens = ctx.saved_tensors
+        chunk_size, scale, use_qk_l2norm = ctx.cfg
+        if do is None:
+            do = torch.zeros(v.shape, dtype=torch.float32, device=v.device)
+        dq, dk, dv, dg, db, dh0 = chunk_gated_delta_rule_bwd(
+            q, k, v, g, beta, do, chunk_size, initial_state=initial_state, d_final_state=dfs,
+            cu_seqlens=cu_seqlens, scale=scale, use_qk_l2norm=use_qk_l2norm)
+        return (dq, dk, dv, dg, db, dh0 if initial_state is not None else None, None, None, None,
+                None)
+
+
+def chunk_gated_delta_rule(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size=64, *,
+                           initial_state=None, output_final_state=False, cu_seqlens=None,
+                           scale=None, use_qk_l2norm=True):
+    """Chunked gated delta rule (deltanet.py:53-153) on libomx_gdn.
+
+    q/k [B,T,Hk,A] and v [B,T,H,U] (bf16 or fp32, same dtype); Hk may divide H
+    (GQA, repeat-interleave semantics of deltanet.py:272-280) or equal it.
+    g/beta [B,T,H].  Returns o [B,T,H,U] fp32, or (o, final_state) when
+    ``output_final_state``.  ``cu_seqlens`` (int32 [N+1], B == 1) packs N
+    sequences; ``initial_state`` is [N or B, H, A, U] fp32.  When gradients are
+    enabled and an input requires them, the call is recorded for autograd and its
+    backward runs omx_gdn_chunk_bwd.
+    """
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad
+        for t in (q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state))
+    if needs_grad:
+        o, fs = _ChunkGatedDeltaRule.apply(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state,
+                                           cu_seqlens, chunk_size, scale, use_qk_l2norm)
+        return (o, fs) if output_final_state else o
+    o, fs = _chunk_fwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size, initial_state,
+                       output_final_state, cu_seqlens, scale, use_qk_l2norm)
     return (o, fs) if output_final_state else o
 
 

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().omx_gdn_abi_version() == 101
+    assert _lib.lib().omx_gdn_abi_version() == 102
 
 
 def _decode(**over):
@@ -139,3 +139,48 @@ def test_prefill_rejects_small_workspace():
     rc = L.omx_gdn_prefill(16, 16, 16, 16, 16, 16, 16, 16, 1e-6, None, 2, None, None, None, None, 16,
                            2, 100, 2, 4, 128, 128, 4, 64, 256, need - 1, None)
     assert rc == _lib.EINVAL and "workspace" in L.omx_gdn_last_error().decode()
+
+
+def _bwd_ws_size(B=2, T=100, Hk=2, Hv=4, dk=128, dv=128, N=2, dt=_lib.BF16):
+    return _lib.lib().omx_gdn_chunk_bwd_workspace_size(B, T, Hk, Hv, dk, dv, N, dt)
+
+
+def test_bwd_workspace_adds_states_and_chunk_matrices():
+    # forward workspace + per (slot, value head): X, Lg, P, G (49,408 B) and two fp32
+    # states, plus V_new / dV_new and the per-value-head dq / dk rows
+    slots = (2 * 100 + 63) // 64 + 2
+    need = (_ws_size() + slots * 4 * 49408 + 2 * slots * 4 * 128 * 128 * 4
+            + 2 * 200 * 4 * 128 * 4 + 2 * 200 * 4 * 128 * 4)
+    assert _bwd_ws_size() >= need
+    assert _bwd_ws_size(T=1000) > _bwd_ws_size(T=100)
+
+
+def _bwd(ws, ws_bytes, **over):
+    a = dict(q=16, k=16, v=16, dt=_lib.BF16, g=16, beta=16, s0=None, cu=None, N=2, do=16, dht=None,
+             dq=16, dk=16, dv=16, dg=16, db=16, dh0=None, B=2, T=100, Hk=2, Hv=4, dkd=128, dvd=128,
+             C=64, scale=0.088, norm=1, ws=ws, ws_bytes=ws_bytes, stream=None)
+    a.update(over)
+    L = _lib.lib()
+    rc = L.omx_gdn_chunk_bwd(*a.values())
+    return rc, L.omx_gdn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(ws_bytes=1024), _lib.EINVAL, "workspace"),
+    (dict(ws=24), _lib.EINVAL, "aligned"),
+    (dict(C=32), _lib.EINVAL, "chunk_size"),
+    (dict(dt=5), _lib.EINVAL, "in_dtype"),
+    (dict(N=3), _lib.EINVAL, "N must equal B"),
+    (dict(do=None), _lib.EINVAL, "NULL"),
+    (dict(dg=None), _lib.EINVAL, "NULL"),
+    (dict(Hv=5), _lib.EINVAL, "multiple of key heads"),
+    (dict(dkd=96), _lib.EUNSUPPORTED, "not compiled"),
+    (dict(dvd=256), _lib.EUNSUPPORTED, "not compiled"),
+    (dict(dt=_lib.F32), _lib.EUNSUPPORTED, "not compiled"),  # fp32 inputs: dk 32/64 only
+])
+def test_chunk_bwd_rejects_bad_arguments(over, code, msg):
+    args = dict(ws=256, ws_bytes=_bwd_ws_size())
+    args.update(over)
+    rc, err = _bwd(args.pop("ws"), args.pop("ws_bytes"), **args)
+    assert rc == code
+    assert msg in err
