@@ -10,6 +10,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
   core     one chunk_gated_delta_rule call at --batch/--seq-len/--k-heads/--v-heads
            (C1 by default; C4 is --batch 1 --seq-len 65536 --v-heads 64).
+  bwd      one chunk_gated_delta_rule_bwd call (the VJP: forward recompute, reverse state-
+           gradient scan, chunk-parallel gradients) at the core workload's shape.
   copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
 rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
@@ -38,6 +40,13 @@ C = 64
 def prefill_flops_per_token_head(dk, dv, c=C):
     """Matmuls of deltanet.py:107,115,116,130,133,136,137,142: 2C(3dk+2dv) + 6 dk dv."""
     return 2 * c * (3 * dk + 2 * dv) + 6 * dk * dv
+
+
+def bwd_flops_per_token_head(dk, dv, c=C):
+    """Matmuls of the reverse pass, forward recompute included (the fp64 oracle's
+    products, oracle/gdn_vjp.py): 8 of C x C x dk, 5 of C x C x dv, 8 of C x dk x dv and
+    the two C^3 products of dL = X^T dX X^T, per chunk; the triangular inverse excluded."""
+    return 16 * c * dk + 10 * c * dv + 16 * dk * dv + 4 * c * c
 
 
 def decode_bytes_per_seq(Hk, Hv, dk, dv, K=4):
@@ -182,6 +191,42 @@ def bench_core(B, T, Hk, Hv, d, steps, warmup, arrs=None):
     }
 
 
+def bench_bwd(B, T, Hk, Hv, d, steps, warmup):
+    """One chunk_gated_delta_rule_bwd call (bf16 q/k/v, fp32 gates and cotangent), HIP-event
+    timed: the backward variants of the prep and scan, the reverse scan, the chunk-parallel
+    gradient kernel and the q/k finalisation."""
+    import torch
+    from omegalax_amd import chunk_gated_delta_rule_bwd, workloads as W
+    rng = np.random.default_rng(8)
+
+    def act(*shape):
+        x = W.round_bf16(rng.standard_normal(shape, dtype=np.float32))
+        return torch.from_numpy(x).cuda().bfloat16()
+
+    q, k, v = act(B, T, Hk, d), act(B, T, Hk, d), act(B, T, Hv, d)
+    a = rng.standard_normal((B, T, Hv), dtype=np.float32)
+    A_log = rng.uniform(0, np.log(16), Hv).astype(np.float32)
+    dt = rng.uniform(-2, 0, Hv).astype(np.float32)
+    g = torch.from_numpy((-np.exp(A_log) * np.logaddexp(a + dt, 0)).astype(np.float32)).cuda()
+    beta = torch.from_numpy(1 / (1 + np.exp(-rng.standard_normal((B, T, Hv), dtype=np.float32)))).cuda()
+    do = torch.from_numpy(rng.standard_normal((B, T, Hv, d), dtype=np.float32)).cuda()
+
+    def bwd():
+        chunk_gated_delta_rule_bwd(q, k, v, g, beta, do, C)
+
+    _say(f"bwd: B={B} T={T} Hk={Hk} Hv={Hv} timing {steps} launches")
+    wall, ms = time_launches(bwd, steps, warmup)
+    flops = bwd_flops_per_token_head(d, d) * B * T * Hv
+    tf = flops / (ms * 1e-3) / 1e12
+    return {
+        "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
+                     "algorithmic_flops": flops,
+                     "kernels": "prep (bwd) + scan (bwd) + rscan + cgrad + qk_final"},
+    }
+
+
 # ----------------------------------------------------------------------------- prefill (C1)
 
 def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
@@ -237,7 +282,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode", "core", "copy"],
+    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "copy"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -268,6 +313,21 @@ def main():
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "f32", "data": "synthetic",
                           "config": {"workload": "256 MiB read + 256 MiB written"}}), flush=True)
+        return 0
+    if args.workload == "bwd":
+        B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads
+        res = bench_bwd(B, T, Hk, Hv, 128, args.steps, args.warmup)
+        line = {
+            "metric": "chunk_gated_delta_rule_bwd TFLOP/s (bf16 MFMA roofline)",
+            "value": res["roofline"]["achieved"], "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) activations and cotangents, random-init gates)",
+            "config": {"workload": f"chunk_gated_delta_rule_bwd B={B} T={T} Hk={Hk} Hv={Hv} d=128",
+                       "chunk": C},
+            "roofline": res["roofline"], "kernel_ms": res["kernel_ms"],
+        }
+        print(json.dumps(line), flush=True)
         return 0
     if args.workload == "core":
         B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads

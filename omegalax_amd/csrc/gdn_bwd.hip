@@ -129,6 +129,19 @@ __device__ __forceinline__ void gfrag_col(const float* base, long long ld, int c
   }
 }
 
+// 4 elements in registers (4 bf16 in two words, or 4 floats)
+template <class T> struct Vec4;
+template <> struct Vec4<float> { typedef float4 type; };
+template <> struct Vec4<bf16_t> { typedef u32x2 type; };
+__device__ __forceinline__ float4 load4(const float* src, bool valid) {
+  return valid ? *(const float4*)src : float4{0.f, 0.f, 0.f, 0.f};
+}
+__device__ __forceinline__ u32x2 load4(const bf16_t* src, bool valid) {
+  return valid ? *(const u32x2*)src : u32x2{0u, 0u};
+}
+__device__ __forceinline__ void store4(float* dst, float4 x) { *(float4*)dst = x; }
+__device__ __forceinline__ void store4(bf16_t* dst, u32x2 x) { *(u32x2*)dst = x; }
+
 // 4 elements at src (zero when !valid) into LDS
 __device__ __forceinline__ void copy4(float* dst, const float* src, bool valid) {
   *(float4*)dst = valid ? *(const float4*)src : float4{0.f, 0.f, 0.f, 0.f};
@@ -206,31 +219,71 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     for (int v = 0; v < 4; ++v)
       dS[t][v] = p.dht ? p.dht[st_off + (size_t)(16 * t + 4 * lq + v) * DV] : 0.f;
 
+  // Per-thread register prefetch of one chunk's inputs: K and Q rows, the chunk's dO
+  // columns, X and P, and one gate value; stored into LDS at the top of the chunk.
+  constexpr int NKQ = 2 * C * (DK / 4) / NT;
+  static_assert(NKQ * NT == 2 * C * (DK / 4), "item split");
+  typename Vec4<KT>::type pkq[NKQ];
+  float4 pdo[C * 16 / NT], pxp[2 * C * 16 / NT];
+  float pgate;
+  auto load_chunk = [&](int jj) {
+    const long long tt = s0 + (long long)jj * C;
+    const int nv = (int)((s1 - tt) < C ? (s1 - tt) : C);
+    const int sl = cbase + jj < p.n_rec ? cbase + jj : p.n_rec - 1;
+#pragma unroll
+    for (int m = 0; m < NKQ; ++m) {
+      const int it = tid + m * NT;
+      const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
+      const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
+      const KT* src = (const KT*)(which ? p.qs : p.ks) + (tt + (row < nv ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
+                      (long long)hk * DK + c4;
+      pkq[m] = load4(src, row < nv);
+    }
+#pragma unroll
+    for (int m = 0; m < C * 16 / NT; ++m) {
+      const int it = tid + m * NT;
+      const int row = it >> 4, c4 = 4 * (it & 15);
+      pdo[m] = load4(p.dO + (tt + (row < nv ? row : 0)) * rs + (long long)h * DV + col0 + c4, row < nv);
+    }
+    const float* xb = p.xlpg + ((size_t)sl * p.Hv + h) * kXlpgFloats;
+#pragma unroll
+    for (int m = 0; m < 2 * C * 16 / NT; ++m) {
+      const int it = tid + m * NT;
+      const int which = it / (C * 16), rem = it % (C * 16);
+      pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15), true);
+    }
+    pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int m = 0; m < NKQ; ++m) {
+      const int it = tid + m * NT;
+      const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
+      const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
+      store4((which ? sQ : sK) + row * LDK + c4, pkq[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < C * 16 / NT; ++m) {
+      const int it = tid + m * NT;
+      store4(sDO + (it >> 4) * LDF + 4 * (it & 15), pdo[m]);
+    }
+#pragma unroll
+    for (int m = 0; m < 2 * C * 16 / NT; ++m) {
+      const int it = tid + m * NT;
+      const int which = it / (C * 16), rem = it % (C * 16);
+      store4((which ? sP : sX) + (rem >> 4) * LDF + 4 * (rem & 15), pxp[m]);
+    }
+    sGate[tid] = pgate;
+  };
+  if (nchunks > 0) load_chunk(nchunks - 1);
+
   for (int j = nchunks - 1; j >= 0; --j) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
     const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
     __syncthreads();  // the previous chunk's readers are done
-    // ---------------------------------------------------------------- stage
-    for (int it = tid; it < 2 * C * (DK / 4); it += NT) {
-      const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
-      const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
-      const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
-                      (long long)hk * DK + c4;
-      copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
-    }
-    for (int it = tid; it < C * 16; it += NT) {
-      const int row = it >> 4, c4 = 4 * (it & 15);
-      const float* src = p.dO + (t0 + (row < nvalid ? row : 0)) * rs + (long long)h * DV + col0 + c4;
-      copy4(sDO + row * LDF + c4, src, row < nvalid);
-    }
-    const float* xb = p.xlpg + ((size_t)slot * p.Hv + h) * kXlpgFloats;
-    for (int it = tid; it < 2 * C * 16; it += NT) {
-      const int which = it / (C * 16), rem = it % (C * 16);
-      const int row = rem >> 4, c4 = 4 * (rem & 15);
-      copy4((which ? sP : sX) + row * LDF + c4, xb + (which ? kXlpgP : kXlpgX) + row * C + c4, true);
-    }
-    sGate[tid] = ((const float*)(p.rec + ((size_t)slot * p.Hv + h) * rec_stride + kRecG))[tid];
+    store_chunk();
+    if (j > 0) load_chunk(j - 1);  // lands while this chunk computes
     __syncthreads();
     const float* sEG = sGate + kGateEG * C;
     const float* sEGS = sGate + kGateEGS * C;
@@ -350,14 +403,20 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 
 // ============================================================================ chunk-local gradients
 
+// Eight wavefronts (two per SIMD: the LDS holds one workgroup per CU).  Wavefront w owns
+// dk column blocks w + 8m and dv column blocks w + 8m of the (chunk x head) gradients,
+// and of the 64x64 chunk matrices row block w % 4, column blocks 2 (w / 4) and
+// 2 (w / 4) + 1.
+constexpr int CW = 8, CNT = 64 * CW;
+
 template <int DK, int DV, bool F32>
-__global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
+__global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   using KT = typename std::conditional<F32, float, bf16_t>::type;
   using In = KT;  // v has the input precision too
   constexpr int LDK = DK + (F32 ? 4 : 8);
   constexpr int LDW = DK + 4;
-  constexpr int NCB = DK / 16, NKB = (NCB + 3) / 4;  // dk column blocks; per wavefront
-  constexpr int NVB = DV / 16, NVW = (NVB + 3) / 4;  // dv column blocks; per wavefront
+  constexpr int NCB = DK / 16, NKB = (NCB + CW - 1) / CW;  // dk column blocks; per wavefront
+  constexpr int NVB = DV / 16, NVW = (NVB + CW - 1) / CW;  // dv column blocks; per wavefront
   __shared__ __align__(16) KT sK[C * LDK];
   __shared__ __align__(16) KT sQ[C * LDK];
   __shared__ __align__(16) float sX[C * LDF];
@@ -367,8 +426,8 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   __shared__ __align__(16) float sM[C * LDF];
   __shared__ float sG[C], sBt[C];
   // per-wavefront partial row / column sums (deterministic: one writer per entry at a time)
-  __shared__ float sRowG[4][C], sColG[4][C], sRowB[4][C], sRowT[4][C], sRP[4][C];
-  __shared__ float sRed[4];
+  __shared__ float sRowG[CW][C], sColG[CW][C], sRowB[CW][C], sRowT[CW][C], sRP[CW][C];
+  __shared__ float sRed[CW];
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -406,14 +465,14 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   const float scale = p.scale;
 
   // ---------------------------------------------------------------- stage
-  for (int it = tid; it < 2 * C * (DK / 4); it += NT) {
+  for (int it = tid; it < 2 * C * (DK / 4); it += CNT) {
     const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
     const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
     const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
                     (long long)hk * DK + c4;
     copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
   }
-  for (int it = tid; it < C * 16; it += NT) {
+  for (int it = tid; it < C * 16; it += CNT) {
     const int row = it >> 4, c4 = 4 * (it & 15);
     copy4(sX + row * LDF + c4, xb + kXlpgX + row * C + c4, true);
   }
@@ -447,79 +506,102 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   f32x4 dq[NKB][4], dk[NKB][4];
 
   // ---------------------------------------------------------------- products over dv
+  // One pass over dv in 32-column steps; every fragment is loaded once per wavefront and
+  // serves all of the wavefront's products:
+  //   X1 = diag(e^G) dO S^T, dW = -dV_new S^T, dkdec = V_new dS^T (its dk column blocks),
+  //   dP = (dO V_new^T) * tril and dXa = dV_new v^T (its row block bi = wave).
+  f32x4 dw[NKB][4], dp[2], dxa[2];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dq[kb][i] = dk[kb][i] = dw[kb][i] = zero4();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) dp[j] = dxa[j] = zero4();
+  const int bi = wave & 3, half = wave >> 2;  // row block and column-block pair
+#pragma unroll
+  for (int u = 0; u < DV / 32; ++u) {
+    Op bs[NKB], bd[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int cb = wave + CW * kb;
+      if (cb >= NCB) continue;
+      float b[8];
+      gfrag_row(Sg, DV, 16 * cb + lr, DK, 32 * u, b);
+      bs[kb] = split8(b);
+      gfrag_row(dSg, DV, 16 * cb + lr, DK, 32 * u, b);
+      bd[kb] = split8(b);
+    }
+    Op ow, vw;  // dO and dV_new rows of block bi
+    {
+      float a[8];
+      gfrag_row(dOb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+      ow = split8(a);
+      gfrag_row(dVnb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+      vw = split8(a);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a[8];
+      gfrag_row(dOb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      const Op ao = split8(a);
+      gfrag_row(dVnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      const Op adv = split8(a);
+      gfrag_row(Vnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      const Op avn = split8(a);
+      gfrag_row(vb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      const Op av = split8<F32>(a);
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        if (wave + CW * kb >= NCB) continue;
+        dq[kb][i] = mm3<true, true>(dq[kb][i], ao, bs[kb]);    // dO S^T
+        dw[kb][i] = mm3<true, true>(dw[kb][i], adv, bs[kb]);   // dV_new S^T
+        dk[kb][i] = mm3<true, true>(dk[kb][i], avn, bd[kb]);   // V_new dS^T
+      }
+      if ((i >> 1) == half) {
+        dxa[i & 1] = mm3<true, F32>(dxa[i & 1], vw, av);              // dV_new v^T
+        if (i <= bi) dp[i & 1] = mm3<true, true>(dp[i & 1], ow, avn);  // dO V_new^T
+      }
+    }
+  }
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    const int cb = wave + 4 * kb;
+    const int cb = wave + CW * kb;
     if (cb >= NCB) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f32x4 x1 = zero4(), dkd = zero4(), dw = zero4();
-#pragma unroll
-      for (int u = 0; u < DV / 32; ++u) {
-        float a[8], b[8];
-        gfrag_row(Sg, DV, 16 * cb + lr, DK, 32 * u, b);
-        const Op bs = split8(b);
-        gfrag_row(dOb, rs, 16 * i + lr, nvalid, 32 * u, a);
-        x1 = mm3<true, true>(x1, split8(a), bs);           // dO S^T
-        gfrag_row(dVnb, rs, 16 * i + lr, nvalid, 32 * u, a);
-        dw = mm3<true, true>(dw, split8(a), bs);           // dV_new S^T
-        gfrag_row(dSg, DV, 16 * cb + lr, DK, 32 * u, b);
-        gfrag_row(Vnb, rs, 16 * i + lr, nvalid, 32 * u, a);
-        dkd = mm3<true, true>(dkd, split8(a), split8(b));  // V_new dS^T
-      }
       f32x4 gx, rr;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * i + 4 * lq + v, col = 16 * cb + lr;
-        x1[v] *= eg(row);                                  // X1 = diag(e^G) dO S^T
-        gx[v] = scale * ldx(sQ + row * LDK + col) * x1[v];
+        dq[kb][i][v] *= eg(row);                           // X1 = diag(e^G) dO S^T
+        gx[v] = scale * ldx(sQ + row * LDK + col) * dq[kb][i][v];
         const float e = el(row);
-        rr[v] = dkd[v] * ldx(sK + row * LDK + col) * e;    // dkdec * kdec
-        dkd[v] *= e;
-        sDW[row * LDW + col] = -dw[v];                     // dW = -dV_new S^T
+        rr[v] = dk[kb][i][v] * ldx(sK + row * LDK + col) * e;  // dkdec * kdec
+        dk[kb][i][v] *= e;
+        sDW[row * LDW + col] = -dw[kb][i][v];              // dW = -dV_new S^T
       }
-      dq[kb][i] = x1;
-      dk[kb][i] = dkd;
       add_rows(rowG, i, gx);
       add_rows(rP, i, rr);
     }
   }
-  // dP = (dO V_new^T) * tril, row block `wave`; dXa = dV_new v^T
-  f32x4 dxa[4];
-  {
-    const int bi = wave;
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
-      f32x4 dp = zero4(), xa = zero4();
+  for (int jj = 0; jj < 2; ++jj) {
+    const int bj = 2 * half + jj;
+    f32x4 pdp;
 #pragma unroll
-      for (int u = 0; u < DV / 32; ++u) {
-        float a[8], b[8];
-        gfrag_row(vb, rs, 16 * bj + lr, nvalid, 32 * u, b);
-        gfrag_row(dVnb, rs, 16 * bi + lr, nvalid, 32 * u, a);
-        xa = mm3<true, F32>(xa, split8(a), split8<F32>(b));
-        if (bj <= bi) {
-          gfrag_row(Vnb, rs, 16 * bj + lr, nvalid, 32 * u, b);
-          gfrag_row(dOb, rs, 16 * bi + lr, nvalid, 32 * u, a);
-          dp = mm3<true, true>(dp, split8(a), split8(b));
-        }
-      }
-      dxa[bj] = xa;
-      f32x4 pdp;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
-        const float d = row >= col ? dp[v] : 0.f;
-        pdp[v] = d * xb[kXlpgP + row * C + col];
-        sDP[row * LDF + col] = d * gam(row, col);          // dPg = dP * Gamma
-      }
-      add_rows(rowG, bi, pdp);
-      add_cols(colG, bj, -pdp);
+    for (int v = 0; v < 4; ++v) {
+      const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
+      const float d = row >= col ? dp[jj][v] : 0.f;
+      pdp[v] = d * xb[kXlpgP + row * C + col];
+      sDP[row * LDF + col] = d * gam(row, col);            // dPg = dP * Gamma
     }
+    add_rows(rowG, bi, pdp);
+    add_cols(colG, bj, -pdp);
   }
   // sum of dS_end * S over the state (the e^{G_last} S term of the state update)
   {
     float sds = 0.f;
-    for (int it = tid; it < DK * DV / 4; it += NT) {
+    for (int it = tid; it < DK * DV / 4; it += CNT) {
       const float4 a = ((const float4*)Sg)[it], b = ((const float4*)dSg)[it];
       sds += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
     }
@@ -530,9 +612,9 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
 
   // ---------------------------------------------------------------- dX = dU vb^T + dW kbe^T
   {
-    const int bi = wave;
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int bj = 2 * half + jj;
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
@@ -546,7 +628,7 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * bi + 4 * lq + v;
-        sDX[row * LDF + col] = bc * (dxa[bj][v] + ec * acc[v]);
+        sDX[row * LDF + col] = bc * (dxa[jj][v] + ec * acc[v]);
       }
     }
   }
@@ -555,7 +637,7 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   // ---------------------------------------------------------------- dvb = X^T dU, dkbe = X^T dW
 #pragma unroll
   for (int kv = 0; kv < NVW; ++kv) {
-    const int cv = wave + 4 * kv;
+    const int cv = wave + CW * kv;
     if (cv >= NVB) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -584,7 +666,7 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   }
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    const int cb = wave + 4 * kb;
+    const int cb = wave + CW * kb;
     if (cb >= NCB) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -606,11 +688,11 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
       add_rows(rowT, i, kt);
     }
   }
-  // M1 = X^T dX, row block `wave` (read back only by this wavefront)
+  // M1 = X^T dX
   {
-    const int bi = wave;
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int bj = 2 * half + jj;
       f32x4 acc = zero4();
       for (int p2 = bi / 2; p2 < 2; ++p2) {  // X^T is upper triangular
         float a[8], b[8];
@@ -622,13 +704,13 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
       for (int v = 0; v < 4; ++v) sM[(16 * bi + 4 * lq + v) * LDF + 16 * bj + lr] = acc[v];
     }
   }
-  wave_lds_fence();
+  __syncthreads();  // M1 complete (a row block's two halves come from two wavefronts)
   // ---------------------------------------------------------------- dL = -strict_lower(M1 X^T)
   {
-    const int bi = wave;
-    f32x4 dl[4];
+    f32x4 dl[2];
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int bj = 2 * half + jj;
       f32x4 acc = zero4();
       if (bj <= bi) {
 #pragma unroll
@@ -639,16 +721,17 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
           acc = mm3<true, true>(acc, split8(a), split8(b));
         }
       }
-      dl[bj] = acc;
+      dl[jj] = acc;
     }
-    wave_lds_fence();  // every read of M1 is complete before its rows are overwritten
+    __syncthreads();  // every read of M1 is complete before its rows are overwritten
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int jj = 0; jj < 2; ++jj) {
+      const int bj = 2 * half + jj;
       f32x4 lb, ld;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
-        const float d = row > col ? -dl[bj][v] : 0.f;
+        const float d = row > col ? -dl[jj][v] : 0.f;
         const float lg = xb[kXlpgLg + row * C + col];
         lb[v] = d * lg;
         ld[v] = d * sBt[row] * lg;                      // dL * L
@@ -664,7 +747,7 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
   // ---------------------------------------------------------------- (Qm + Qm^T) k, dPg^T qs, dPg k
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
-    const int cb = wave + 4 * kb;
+    const int cb = wave + CW * kb;
     if (cb >= NCB) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -712,7 +795,7 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
     const int i = l;
     float rg = 0.f, rt = 0.f, rb = 0.f, rp = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < CW; ++w) {
       rg += sRowG[w][i] + sColG[w][i] - sRP[w][i];
       rt += sRowT[w][i];
       rb += sRowB[w][i];
@@ -722,7 +805,9 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
     float dG = rg + sBt[i] * t;
     const float db = rb + t;
     const float rsum = wave_sum(rp);
-    const float sds = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+    float sds = 0.f;
+#pragma unroll
+    for (int w = 0; w < CW; ++w) sds += sRed[w];
     if (i == C - 1) dG += rsum + __expf(Gl) * sds;
     // dg_t = sum_{i >= t} dG_i (G = cumsum(g), deltanet.py:98)
     float x = dG;
@@ -740,48 +825,47 @@ __global__ __launch_bounds__(NT) void cgrad_kernel(BwdParams p) {
 
 // ============================================================================ q/k finalisation
 
-// One wavefront per (token, key head) row of dq or dk: the sum over the key head's value
-// heads, then (qk_l2norm) the L2-norm backward dx = r (dy - y (y . dy)), y = x r,
-// r = rsqrt(sum x^2 + 1e-6) (deltanet.py:30-32; the bf16 rounding of y is differentiated
-// as the identity, as autodiff does for a dtype cast).
+// dk / 4 consecutive threads per (token, key head) row of dq or dk, 4 elements each: the
+// sum over the key head's value heads, then (qk_l2norm) the L2-norm backward
+// dx = r (dy - y (y . dy)), y = x r, r = rsqrt(sum x^2 + 1e-6) (deltanet.py:30-32; the bf16
+// rounding of y is differentiated as the identity, as autodiff does for a dtype cast).
 template <bool F32>
 __global__ __launch_bounds__(NT) void qk_final_kernel(BwdParams p, long long rows) {
   using In = typename std::conditional<F32, float, bf16_t>::type;
-  const int l = threadIdx.x & 63;
-  const long long rid = (long long)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
-  if (rid >= 2 * rows) return;
+  const int dk = p.dk, tpr = dk / 4, gqa = p.Hv / p.Hk;
+  const long long gid = (long long)blockIdx.x * NT + threadIdx.x;
+  const long long rid = gid / tpr;
+  const int c4 = 4 * (int)(gid % tpr);
+  if (rid >= 2 * rows) return;  // whole rows drop out together (tpr divides 64)
   const int which = (int)(rid / rows);
   const long long row = rid % rows;
   const long long token = row / p.Hk;
-  const int hk = (int)(row % p.Hk), dk = p.dk, gqa = p.Hv / p.Hk;
-  const float* src = (which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk;
-  const In* x_in = (const In*)(which ? p.k : p.q) + row * dk;
-  float d[2], x[2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int a = l + 64 * e;
-    d[e] = 0.f;
-    x[e] = 0.f;
-    if (a < dk) {
-      for (int g = 0; g < gqa; ++g) d[e] += src[(long long)g * dk + a];
-      x[e] = ldx(x_in + a);
-    }
+  const int hk = (int)(row % p.Hk);
+  const float* src = (which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk + c4;
+  float d[4] = {0.f, 0.f, 0.f, 0.f}, x[4];
+  for (int g = 0; g < gqa; ++g) {
+    const float4 w = *(const float4*)(src + (long long)g * dk);
+    d[0] += w.x; d[1] += w.y; d[2] += w.z; d[3] += w.w;
   }
+  const In* x_in = (const In*)(which ? p.k : p.q) + row * dk + c4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = ldx(x_in + e);
   if (p.qk_l2norm) {
-    const float r = rsqrtf(wave_sum(x[0] * x[0] + x[1] * x[1]) + 1e-6f);
-    const float y0 = x[0] * r, y1 = x[1] * r;
-    const float yd = wave_sum(y0 * d[0] + y1 * d[1]);
-    d[0] = r * (d[0] - y0 * yd);
-    d[1] = r * (d[1] - y1 * yd);
-  }
-  In* out = (In*)(which ? p.dk_out : p.dq) + row * dk;
+    float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+    for (int o = 1; o < tpr; o <<= 1) ss += __shfl_xor(ss, o);
+    const float r = rsqrtf(ss + 1e-6f);
+    float yd = 0.f;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    const int a = l + 64 * e;
-    if (a < dk) {
-      if constexpr (F32) out[a] = d[e];
-      else out[a] = f2bf(d[e]);
-    }
+    for (int e = 0; e < 4; ++e) yd += x[e] * r * d[e];
+    for (int o = 1; o < tpr; o <<= 1) yd += __shfl_xor(yd, o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[e] = r * (d[e] - x[e] * r * yd);
+  }
+  In* out = (In*)(which ? p.dk_out : p.dq) + row * dk + c4;
+  if constexpr (F32) {
+    *(float4*)out = float4{d[0], d[1], d[2], d[3]};
+  } else {
+    *(u32x2*)out = u32x2{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
   }
 }
 
@@ -794,15 +878,16 @@ hipError_t launch_bwd_dk(const BwdParams& p, hipStream_t stream) {
   const unsigned grid = (unsigned)((long long)p.n_rec * p.Hv);
   if (grid > 0) {
     if (p.DV == 128)
-      hipLaunchKernelGGL((cgrad_kernel<DK, 128, F32>), dim3(grid), dim3(NT), 0, stream, p);
+      hipLaunchKernelGGL((cgrad_kernel<DK, 128, F32>), dim3(grid), dim3(CNT), 0, stream, p);
     else
-      hipLaunchKernelGGL((cgrad_kernel<DK, 64, F32>), dim3(grid), dim3(NT), 0, stream, p);
+      hipLaunchKernelGGL((cgrad_kernel<DK, 64, F32>), dim3(grid), dim3(CNT), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   const long long rows = (long long)p.T * (p.cu_seqlens ? 1 : p.N) * p.Hk;
   if (rows > 0) {
-    const unsigned g2 = (unsigned)((2 * rows + NT / 64 - 1) / (NT / 64));
+    const long long threads = 2 * rows * (p.dk / 4);
+    const unsigned g2 = (unsigned)((threads + NT - 1) / NT);
     hipLaunchKernelGGL((qk_final_kernel<F32>), dim3(g2), dim3(NT), 0, stream, p, rows);
     e = hipGetLastError();
   }
