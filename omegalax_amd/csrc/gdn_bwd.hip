@@ -292,11 +292,10 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 
     // gradient of the state leaving chunk j, for the chunk-local gradients
     {
-      float* dd = p.dstates + ((size_t)slot * p.Hv + h) * DK * DV + col0 + c + lr;
+      // column-major per state ([dv][dk]): a lane's 4 rows of a tile are contiguous
+      float* dd = p.dstates + ((size_t)slot * p.Hv + h) * DK * DV + (size_t)(col0 + c + lr) * DK;
 #pragma unroll
-      for (int t = 0; t < DK / 16; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) dd[(size_t)(16 * t + 4 * lq + v) * DV] = dS[t][v];
+      for (int t = 0; t < DK / 16; ++t) *(f32x4*)(dd + 16 * t + 4 * lq) = dS[t];
     }
 
     // ---------------------------------------------------------------- K dS
@@ -526,9 +525,10 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       const int cb = wave + CW * kb;
       if (cb >= NCB) continue;
       float b[8];
-      gfrag_row(Sg, DV, 16 * cb + lr, DK, 32 * u, b);
+      // the states are column-major ([dv][dk]): row 16 cb + lr is a column there
+      gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, DV, b);
       bs[kb] = split8(b);
-      gfrag_row(dSg, DV, 16 * cb + lr, DK, 32 * u, b);
+      gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, DV, b);
       bd[kb] = split8(b);
     }
     Op ow, vw;  // dO and dV_new rows of block bi

@@ -429,11 +429,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     if constexpr (BWD) {
       // the state entering chunk j, for the backward pass
       const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
-      float* sd = p.states + ((size_t)slot * p.Hv + h) * DK * DV + col0 + 16 * wave + lr;
+      // column-major per state ([dv][dk]): a lane's 4 rows of a tile are contiguous
+      float* sd = p.states + ((size_t)slot * p.Hv + h) * DK * DV + (size_t)(col0 + 16 * wave + lr) * DK;
 #pragma unroll
-      for (int t = 0; t < DK / 16; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) sd[(size_t)state_row(t, lq, v) * DV] = S[t][v];
+      for (int t = 0; t < DK / 16; ++t) *(f32x4*)(sd + state_row(t, lq, 0)) = S[t];
     }
     // ------------------------------------------------------------ K S, Q S, right-hand side
     // The B operand of K S and Q S over dk block s2 is the state itself: lane (q, r)
@@ -548,12 +547,22 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
       __builtin_amdgcn_sched_group_barrier(0x008, 18, 1);
     }
     if constexpr (BWD) {
-      float* vd = p.vnew + ((size_t)t0 * p.Hv + h) * DV + col0 + 16 * wave + lr;
+      // V_new for the backward pass, formed transposed (V_new^T = R^T (T diag(beta))^T:
+      // the packed R serves as A operand and the record's T fragments as B operands), so
+      // a lane holds 4 consecutive columns of one token row: one 16-byte store per row block
+      float* vd = p.vnew + ((size_t)t0 * p.Hv + h) * DV + col0 + 16 * wave + 4 * lq;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 4; ++i) {
+        f32x4 ut = zero4();
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (16 * i + 4 * lq + v < nvalid) vd[(size_t)(16 * i + 4 * lq + v) * p.Hv * DV] = U[i][v];
+        for (int pp = 0; pp <= i / 2; ++pp) {
+          const int x = pair_index(i, pp);
+          ut = mma16(Rh[pp], th[x], ut);
+          ut = mma16(Rl[pp], th[x], ut);
+          ut = mma16(Rh[pp], tl[x], ut);
+        }
+        if (16 * i + lr < nvalid) *(f32x4*)(vd + (size_t)(16 * i + lr) * p.Hv * DV) = ut;
+      }
     }
     u32x4 Uh[2], Ul[2];  // bf16 hi/lo of V_new block pairs as B operands
 #pragma unroll

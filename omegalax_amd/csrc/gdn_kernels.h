@@ -80,7 +80,7 @@ struct ChunkParams {
   long long ks_ld, qs_ld, vs_ld;
   // backward pass only (the backward variants of the two kernels write them)
   float* xlpg;                 // prep: per (chunk slot, value head) X, Lg, P [64][64], G [64]
-  float* states;               // scan: the state entering each chunk [slot][Hv][dk][DV]
+  float* states;               // scan: the state entering each chunk [slot][Hv][DV][dk]
   float* vnew;                 // scan: V_new [tokens][Hv][DV]
 };
 
@@ -95,9 +95,9 @@ struct BwdParams {
   const float* dht;            // [N][Hv][dk][DV] or null
   const unsigned char* rec;    // prep records
   const float* xlpg;           // prep backward extras
-  const float* states;         // state entering each chunk
+  const float* states;         // state entering each chunk [slot][Hv][DV][dk]
   const float* vnew;           // V_new
-  float* dstates;              // gradient of the state leaving each chunk [slot][Hv][dk][DV]
+  float* dstates;              // gradient of the state leaving each chunk [slot][Hv][DV][dk]
   float* dvnew;                // gradient of V_new [tokens][Hv][DV]
   float* dh0;                  // [N][Hv][dk][DV] or null
   float* dqh;                  // per value head gradient of the normalised q [tokens][Hv][dk]
