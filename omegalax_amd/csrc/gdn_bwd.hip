@@ -140,6 +140,11 @@ __device__ __forceinline__ u32x2 load4(const bf16_t* src, bool valid) {
   return valid ? *(const u32x2*)src : u32x2{0u, 0u};
 }
 __device__ __forceinline__ void store4(float* dst, float4 x) { *(float4*)dst = x; }
+__device__ __forceinline__ float4 to_f4(float4 x) { return x; }
+__device__ __forceinline__ float4 to_f4(u32x2 x) {
+  return float4{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xffff0000u),
+                __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xffff0000u)};
+}
 __device__ __forceinline__ void store4(bf16_t* dst, u32x2 x) { *(u32x2*)dst = x; }
 
 // 4 elements at src (zero when !valid) into LDS
@@ -418,11 +423,13 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   constexpr int NVB = DV / 16, NVW = (NVB + CW - 1) / CW;  // dv column blocks; per wavefront
   __shared__ __align__(16) KT sK[C * LDK];
   __shared__ __align__(16) KT sQ[C * LDK];
-  __shared__ __align__(16) float sX[C * LDF];
   __shared__ __align__(16) float sDW[C * LDW];
-  __shared__ __align__(16) float sDX[C * LDF];
   __shared__ __align__(16) float sDP[C * LDF];
-  __shared__ __align__(16) float sM[C * LDF];
+  // X, dX and M1 / Qm; during the products over dv the region stages their operand rows
+  __shared__ __align__(16) float sR[3 * C * LDF];
+  float* const sX = sR;
+  float* const sDX = sR + C * LDF;
+  float* const sM = sR + 2 * C * LDF;
   __shared__ float sG[C], sBt[C];
   // per-wavefront partial row / column sums (deterministic: one writer per entry at a time)
   __shared__ float sRowG[CW][C], sColG[CW][C], sRowB[CW][C], sRowT[CW][C], sRP[CW][C];
@@ -471,10 +478,6 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
                     (long long)hk * DK + c4;
     copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
   }
-  for (int it = tid; it < C * 16; it += CNT) {
-    const int row = it >> 4, c4 = 4 * (it & 15);
-    copy4(sX + row * LDF + c4, xb + kXlpgX + row * C + c4, true);
-  }
   if (tid < C) {
     sG[tid] = xb[kXlpgG + tid];
     sBt[tid] = ((const float*)(p.rec + ((size_t)ci * Hv + h) * rec_stride + kRecG))[kGateBeta * C + tid];
@@ -505,10 +508,48 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   f32x4 dq[NKB][4], dk[NKB][4];
 
   // ---------------------------------------------------------------- products over dv
-  // One pass over dv in 32-column steps; every fragment is loaded once per wavefront and
-  // serves all of the wavefront's products:
-  //   X1 = diag(e^G) dO S^T, dW = -dV_new S^T, dkdec = V_new dS^T (its dk column blocks),
-  //   dP = (dO V_new^T) * tril and dXa = dV_new v^T (its row block bi = wave).
+  // One pass over dv in 32-column steps:
+  //   X1 = diag(e^G) dO S^T, dW = -dV_new S^T, dkdec = V_new dS^T (the wavefront's dk
+  //   column blocks), dP = (dO V_new^T) * tril and dXa = dV_new v^T (its row block bi,
+  //   column blocks 2 half, 2 half + 1).
+  // The step's dO, dV_new, V_new and v rows are staged in LDS (one coalesced float4 per
+  // thread each) and the state fragments come straight from global memory; both are
+  // loaded into registers one step ahead.
+  constexpr int LDR = 36;  // row stride of a staged 32-column slice
+  static_assert(4 * C * LDR <= 3 * C * LDF, "the staged slices fit the X / dX / M1 region");
+  float* const sDOs = sR;
+  float* const sDVs = sR + C * LDR;
+  float* const sVNs = sR + 2 * C * LDR;
+  float* const sVs = sR + 3 * C * LDR;
+  const int srow = tid >> 3, sc4 = 4 * (tid & 7);  // this thread's staged item
+  const bool srv = srow < nvalid;
+  float4 pf_do, pf_dv, pf_vn;
+  typename Vec4<In>::type pf_v;
+  auto load_rows = [&](int u) {
+    const long long off = (long long)(srv ? srow : 0) * rs + 32 * u + sc4;
+    pf_do = load4(dOb + off, srv);
+    pf_dv = load4(dVnb + off, srv);
+    pf_vn = load4(Vnb + off, srv);
+    pf_v = load4(vb + off, srv);
+  };
+  auto store_rows = [&]() {
+    const int o = srow * LDR + sc4;
+    store4(sDOs + o, pf_do);
+    store4(sDVs + o, pf_dv);
+    store4(sVNs + o, pf_vn);
+    store4(sVs + o, to_f4(pf_v));
+  };
+  float sfr[NKB][8], dfr[NKB][8];  // state fragments (the states are column-major)
+  auto load_state = [&](int u) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int cb = wave + CW * kb;
+      if (cb >= NCB) continue;
+      gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, DV, sfr[kb]);
+      gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, DV, dfr[kb]);
+    }
+  };
+  float4 pf_x[C * 16 / CNT];  // X, staged after the last step
   f32x4 dw[NKB][4], dp[2], dxa[2];
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb)
@@ -517,39 +558,46 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) dp[j] = dxa[j] = zero4();
   const int bi = wave & 3, half = wave >> 2;  // row block and column-block pair
+  load_rows(0);
+  load_state(0);
 #pragma unroll
   for (int u = 0; u < DV / 32; ++u) {
+    __syncthreads();  // the previous step's readers are done
+    store_rows();
     Op bs[NKB], bd[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      const int cb = wave + CW * kb;
-      if (cb >= NCB) continue;
-      float b[8];
-      // the states are column-major ([dv][dk]): row 16 cb + lr is a column there
-      gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, DV, b);
-      bs[kb] = split8(b);
-      gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, DV, b);
-      bd[kb] = split8(b);
+      bs[kb] = split8(sfr[kb]);
+      bd[kb] = split8(dfr[kb]);
     }
+    if (u + 1 < DV / 32) {
+      load_rows(u + 1);
+      load_state(u + 1);
+    } else {
+#pragma unroll
+      for (int m = 0; m < C * 16 / CNT; ++m) {
+        const int it = tid + m * CNT;
+        pf_x[m] = load4(xb + kXlpgX + (it >> 4) * C + 4 * (it & 15), true);
+      }
+    }
+    __syncthreads();
     Op ow, vw;  // dO and dV_new rows of block bi
     {
       float a[8];
-      gfrag_row(dOb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+      frag_row<false>(sDOs, LDR, 16 * bi + lr, 0, a);
       ow = split8(a);
-      gfrag_row(dVnb, rs, 16 * bi + lr, nvalid, 32 * u, a);
+      frag_row<false>(sDVs, LDR, 16 * bi + lr, 0, a);
       vw = split8(a);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float a[8];
-      gfrag_row(dOb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      frag_row<false>(sDOs, LDR, 16 * i + lr, 0, a);
       const Op ao = split8(a);
-      gfrag_row(dVnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      frag_row<false>(sDVs, LDR, 16 * i + lr, 0, a);
       const Op adv = split8(a);
-      gfrag_row(Vnb, rs, 16 * i + lr, nvalid, 32 * u, a);
+      frag_row<false>(sVNs, LDR, 16 * i + lr, 0, a);
       const Op avn = split8(a);
-      gfrag_row(vb, rs, 16 * i + lr, nvalid, 32 * u, a);
-      const Op av = split8<F32>(a);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         if (wave + CW * kb >= NCB) continue;
@@ -558,10 +606,18 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         dk[kb][i] = mm3<true, true>(dk[kb][i], avn, bd[kb]);   // V_new dS^T
       }
       if ((i >> 1) == half) {
+        frag_row<false>(sVs, LDR, 16 * i + lr, 0, a);
+        const Op av = split8<F32>(a);
         dxa[i & 1] = mm3<true, F32>(dxa[i & 1], vw, av);              // dV_new v^T
         if (i <= bi) dp[i & 1] = mm3<true, true>(dp[i & 1], ow, avn);  // dO V_new^T
       }
     }
+  }
+  __syncthreads();  // every read of the staged slices is done: the region now holds X
+#pragma unroll
+  for (int m = 0; m < C * 16 / CNT; ++m) {
+    const int it = tid + m * CNT;
+    store4(sX + (it >> 4) * LDF + 4 * (it & 15), pf_x[m]);
   }
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
