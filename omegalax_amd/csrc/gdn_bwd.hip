@@ -98,6 +98,49 @@ __device__ __forceinline__ void frag_col(const T* m, int ld, int col, int k0, fl
   for (int e = 0; e < 8; ++e) x[e] = ldx(m + (k0 + kslot<PAIR>(q, e)) * ld + col);
 }
 
+// K / Q operand fragments from the staged rows: bf16 rows are exact bf16 (one vector or
+// two transposed LDS reads, no lo part); fp32 rows are read element-wise and split.
+// kq_row: row row0 + lane%16, slots over columns from k0; kq_col: column col0 + lane%16,
+// slots over rows from k0.
+template <bool PAIR>
+__device__ __forceinline__ Op kq_row(const float* m, int ld, int row0, int k0) {
+  float x[8];
+  frag_row<PAIR>(m, ld, row0 + (lane_id() & 15), k0, x);
+  return split8(x);
+}
+template <bool PAIR>
+__device__ __forceinline__ Op kq_row(const bf16_t* m, int ld, int row0, int k0) {
+  const int l = lane_id(), q = l >> 4;
+  const bf16_t* pr = m + (row0 + (l & 15)) * ld + k0;
+  Op o;
+  if constexpr (PAIR) {
+    const u32x2 a = *(const u32x2*)(pr + 4 * q), b = *(const u32x2*)(pr + 16 + 4 * q);
+    o.h = u32x4{a[0], a[1], b[0], b[1]};
+  } else {
+    o.h = *(const u32x4*)(pr + 8 * q);
+  }
+  o.l = o.h;
+  return o;
+}
+template <bool PAIR>
+__device__ __forceinline__ Op kq_col(const float* m, int ld, int col0, int k0) {
+  float x[8];
+  frag_col<PAIR>(m, ld, col0 + (lane_id() & 15), k0, x);
+  return split8(x);
+}
+template <bool PAIR>
+__device__ __forceinline__ Op kq_col(const bf16_t* m, int ld, int col0, int k0) {
+  Op o;
+  if constexpr (PAIR) {
+    const u32x2 a = rows4_tr(m, ld, k0, col0), b = rows4_tr(m, ld, k0 + 16, col0);
+    o.h = u32x4{a[0], a[1], b[0], b[1]};
+  } else {
+    o.h = frag_tr(m, ld, k0, col0);
+  }
+  o.l = o.h;
+  return o;
+}
+
 // global: 8 consecutive values of row `row` from column k0 + 8q (zero when row >= nvalid)
 template <class T>
 __device__ __forceinline__ void gfrag_row(const T* base, long long ld, int row, int nvalid, int k0,
@@ -313,9 +356,7 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
-        float x[8];
-        frag_row<true>(sK, LDK, 16 * i + lr, 32 * s, x);
-        acc = mm3<F32, true>(acc, split8<F32>(x), dsb[s]);
+        acc = mm3<F32, true>(acc, kq_row<true>(sK, LDK, 16 * i, 32 * s), dsb[s]);
       }
       kds[i] = acc;
     }
@@ -388,11 +429,8 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       for (int v = 0; v < 4; ++v) acc[v] = egl * dS[t][v];
 #pragma unroll
       for (int p2 = 0; p2 < 2; ++p2) {
-        float a[8];
-        frag_col<false>(sQ, LDK, 16 * t + lr, 32 * p2, a);
-        acc = mm3<F32, true>(acc, split8<F32>(a), b1[p2]);
-        frag_col<true>(sK, LDK, 16 * t + lr, 32 * p2, a);
-        acc = mm3<F32, true>(acc, split8<F32>(a), b2[p2]);
+        acc = mm3<F32, true>(acc, kq_col<false>(sQ, LDK, 16 * t, 32 * p2), b1[p2]);
+        acc = mm3<F32, true>(acc, kq_col<true>(sK, LDK, 16 * t, 32 * p2), b2[p2]);
       }
       dS[t] = acc;
     }
@@ -674,10 +712,9 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 acc = zero4();
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
-        float a[8], b[8];
+        float a[8];
         frag_row<false>(sDW, LDW, 16 * bi + lr, 32 * s, a);
-        frag_row<false>(sK, LDK, 16 * bj + lr, 32 * s, b);
-        acc = mm3<true, F32>(acc, split8(a), split8<F32>(b));
+        acc = mm3<true, F32>(acc, split8(a), kq_row<false>(sK, LDK, 16 * bj, 32 * s));
       }
       const int col = 16 * bj + lr;
       const float bc = sBt[col], ec = eg(col);
@@ -695,21 +732,38 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   for (int kv = 0; kv < NVW; ++kv) {
     const int cv = wave + CW * kv;
     if (cv >= NVB) continue;
+    // the column's dV_new fragments (one per 32-token half, shared by every row block)
+    // and v values, loaded in one batch
+    Op bo[2];
+    float vvs[4][4];
+    {
+      float b[8];
+      gfrag_col(dVnb, rs, 16 * cv + lr, 0, nvalid, b);
+      bo[0] = split8(b);
+      gfrag_col(dVnb, rs, 16 * cv + lr, 32, nvalid, b);
+      bo[1] = split8(b);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * i + 4 * lq + v;
+          vvs[i][v] = row < nvalid ? ldx(vb + (long long)row * rs + 16 * cv + lr) : 0.f;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
       for (int p2 = i / 2; p2 < 2; ++p2) {
-        float a[8], b[8];
+        float a[8];
         frag_col<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
-        gfrag_col(dVnb, rs, 16 * cv + lr, 32 * p2, nvalid, b);
-        acc = mm3<true, true>(acc, split8(a), split8(b));
+        acc = mm3<true, true>(acc, split8(a), bo[p2]);
       }
       f32x4 vd;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * i + 4 * lq + v, col = 16 * cv + lr;
-        const float vv = row < nvalid ? ldx(vb + (long long)row * rs + col) : 0.f;
+        const float vv = vvs[i][v];
         vd[v] = vv * acc[v];
         const float dvv = sBt[row] * acc[v];
         if (row < nvalid) {
@@ -810,9 +864,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 a_k = dk[kb][i], a_q = dq[kb][i], a_t = zero4();
 #pragma unroll
       for (int p2 = 0; p2 < 2; ++p2) {
-        float a[8], b[8];
-        frag_col<false>(sK, LDK, 16 * cb + lr, 32 * p2, b);
-        const Op bk = split8<F32>(b);
+        float a[8];
+        const Op bk = kq_col<false>(sK, LDK, 16 * cb, 32 * p2);
         // symmetric Qm + Qm^T
         {
           float x[8], y[8];
@@ -828,8 +881,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         }
         if (p2 >= i / 2) {  // dPg^T is upper triangular
           frag_col<false>(sDP, LDF, 16 * i + lr, 32 * p2, a);
-          frag_col<false>(sQ, LDK, 16 * cb + lr, 32 * p2, b);
-          a_t = mm3<true, F32>(a_t, split8(a), split8<F32>(b));
+          a_t = mm3<true, F32>(a_t, split8(a), kq_col<false>(sQ, LDK, 16 * cb, 32 * p2));
         }
       }
       float* dqo = p.dqh + (t0 * Hv + h) * (long long)DK;
