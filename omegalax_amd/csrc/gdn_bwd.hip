@@ -398,7 +398,7 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 #pragma unroll
       for (int p2 = i / 2; p2 < 2; ++p2) {  // X^T is upper triangular
         float a[8];
-        frag_col<true>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        frag_row<true>(sX, LDF, 16 * i + lr, 32 * p2, a);  // X^T rows (stored transposed)
         acc = mm3<true, true>(acc, split8(a), dvp[p2]);
       }
 #pragma unroll
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   __shared__ __align__(16) KT sQ[C * LDK];
   __shared__ __align__(16) float sDW[C * LDW];
   __shared__ __align__(16) float sDP[C * LDF];
-  // X, dX and M1 / Qm; during the products over dv the region stages their operand rows
+  // X^T, dX and M1 / Qm; during the products over dv the region stages their operand rows
   __shared__ __align__(16) float sR[3 * C * LDF];
   float* const sX = sR;
   float* const sDX = sR + C * LDF;
@@ -578,6 +578,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     store4(sVs + o, to_f4(pf_v));
   };
   float sfr[NKB][8], dfr[NKB][8];  // state fragments (the states are column-major)
+  float sds = 0.f;  // sum of dS_end * S over the state (each element is loaded once here)
   auto load_state = [&](int u) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -596,6 +597,16 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) dp[j] = dxa[j] = zero4();
   const int bi = wave & 3, half = wave >> 2;  // row block and column-block pair
+  // P and Lg at this wavefront's tiles (bi, 2 half + jj), read elementwise later
+  float pP[2][4], pLg[2][4];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int o = (16 * bi + 4 * lq + v) * C + 16 * (2 * half + jj) + lr;
+      pP[jj][v] = xb[kXlpgP + o];
+      pLg[jj][v] = xb[kXlpgLg + o];
+    }
   load_rows(0);
   load_state(0);
 #pragma unroll
@@ -607,6 +618,10 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int kb = 0; kb < NKB; ++kb) {
       bs[kb] = split8(sfr[kb]);
       bd[kb] = split8(dfr[kb]);
+      if (wave + CW * kb < NCB) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sds += sfr[kb][e] * dfr[kb][e];
+      }
     }
     if (u + 1 < DV / 32) {
       load_rows(u + 1);
@@ -686,22 +701,15 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int v = 0; v < 4; ++v) {
       const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
       const float d = row >= col ? dp[jj][v] : 0.f;
-      pdp[v] = d * xb[kXlpgP + row * C + col];
+      pdp[v] = d * pP[jj][v];
       sDP[row * LDF + col] = d * gam(row, col);            // dPg = dP * Gamma
     }
     add_rows(rowG, bi, pdp);
     add_cols(colG, bj, -pdp);
   }
   // sum of dS_end * S over the state (the e^{G_last} S term of the state update)
-  {
-    float sds = 0.f;
-    for (int it = tid; it < DK * DV / 4; it += CNT) {
-      const float4 a = ((const float4*)Sg)[it], b = ((const float4*)dSg)[it];
-      sds += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
-    }
-    sds = wave_sum(sds);
-    if (l == 0) sRed[wave] = sds;
-  }
+  sds = wave_sum(sds);
+  if (l == 0) sRed[wave] = sds;
   __syncthreads();
 
   // ---------------------------------------------------------------- dX = dU vb^T + dW kbe^T
@@ -732,23 +740,23 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   for (int kv = 0; kv < NVW; ++kv) {
     const int cv = wave + CW * kv;
     if (cv >= NVB) continue;
-    // the column's dV_new fragments (one per 32-token half, shared by every row block)
-    // and v values, loaded in one batch
+    // the column's dV_new fragments (one per 32-token half, shared by every row block).
+    // dvb is formed transposed, dvb^T = dV_new^T X (the fragments serve as A operands and
+    // the X^T rows as B operands), so a lane holds 4 consecutive columns of one row: v is
+    // read and dv written 4 columns at a time.
     Op bo[2];
-    float vvs[4][4];
     {
       float b[8];
       gfrag_col(dVnb, rs, 16 * cv + lr, 0, nvalid, b);
       bo[0] = split8(b);
       gfrag_col(dVnb, rs, 16 * cv + lr, 32, nvalid, b);
       bo[1] = split8(b);
+    }
+    typename Vec4<In>::type vv4[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = 16 * i + 4 * lq + v;
-          vvs[i][v] = row < nvalid ? ldx(vb + (long long)row * rs + 16 * cv + lr) : 0.f;
-        }
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * i + lr;
+      vv4[i] = load4(vb + (long long)(row < nvalid ? row : 0) * rs + 16 * cv + 4 * lq, row < nvalid);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -756,22 +764,19 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
       for (int p2 = i / 2; p2 < 2; ++p2) {
         float a[8];
-        frag_col<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
-        acc = mm3<true, true>(acc, split8(a), bo[p2]);
+        frag_row<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        acc = mm3<true, true>(acc, bo[p2], split8(a));
       }
-      f32x4 vd;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * i + 4 * lq + v, col = 16 * cv + lr;
-        const float vv = vvs[i][v];
-        vd[v] = vv * acc[v];
-        const float dvv = sBt[row] * acc[v];
-        if (row < nvalid) {
-          if constexpr (F32) ((float*)p.dv)[(t0 + row) * rs + (long long)h * DV + col] = dvv;
-          else ((bf16_t*)p.dv)[(t0 + row) * rs + (long long)h * DV + col] = f2bf(dvv);
-        }
+      const int row = 16 * i + lr;
+      const float4 vf = to_f4(vv4[i]);
+      const f32x4 vd = f32x4{vf.x * acc[0], vf.y * acc[1], vf.z * acc[2], vf.w * acc[3]};
+      const float bt = sBt[row];
+      if (row < nvalid) {
+        In* dvo = (In*)p.dv + (t0 + row) * rs + (long long)h * DV + 16 * cv + 4 * lq;
+        if constexpr (F32) *(float4*)dvo = float4{bt * acc[0], bt * acc[1], bt * acc[2], bt * acc[3]};
+        else *(u32x2*)dvo = u32x2{pack_bf16(bt * acc[0], bt * acc[1]), pack_bf16(bt * acc[2], bt * acc[3])};
       }
-      add_rows(rowB, i, vd);
+      add_cols(rowB, i, vd);  // row 16 i + r of the chunk: the transposed tile's column r
     }
   }
 #pragma unroll
@@ -784,7 +789,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
       for (int p2 = i / 2; p2 < 2; ++p2) {
         float a[8], b[8];
-        frag_col<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
+        frag_row<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
         frag_col<false>(sDW, LDW, 16 * cb + lr, 32 * p2, b);
         acc = mm3<true, true>(acc, split8(a), split8(b));
       }
@@ -806,7 +811,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 acc = zero4();
       for (int p2 = bi / 2; p2 < 2; ++p2) {  // X^T is upper triangular
         float a[8], b[8];
-        frag_col<false>(sX, LDF, 16 * bi + lr, 32 * p2, a);
+        frag_row<false>(sX, LDF, 16 * bi + lr, 32 * p2, a);
         frag_col<false>(sDX, LDF, 16 * bj + lr, 32 * p2, b);
         acc = mm3<true, true>(acc, split8(a), split8(b));
       }
@@ -827,7 +832,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         for (int p2 = 0; p2 <= bj / 2; ++p2) {
           float a[8], b[8];
           frag_row<false>(sM, LDF, 16 * bi + lr, 32 * p2, a);
-          frag_row<false>(sX, LDF, 16 * bj + lr, 32 * p2, b);
+          frag_col<false>(sX, LDF, 16 * bj + lr, 32 * p2, b);  // rows of X
           acc = mm3<true, true>(acc, split8(a), split8(b));
         }
       }
@@ -842,7 +847,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
         const float d = row > col ? -dl[jj][v] : 0.f;
-        const float lg = xb[kXlpgLg + row * C + col];
+        const float lg = pLg[jj][v];
         lb[v] = d * lg;
         ld[v] = d * sBt[row] * lg;                      // dL * L
         sM[row * LDF + col] = sBt[row] * d * gam(row, col);  // Qm = diag(beta) (dL * Gamma)

@@ -79,7 +79,7 @@ struct ChunkParams {
   const void* vs;
   long long ks_ld, qs_ld, vs_ld;
   // backward pass only (the backward variants of the two kernels write them)
-  float* xlpg;                 // prep: per (chunk slot, value head) X, Lg, P [64][64], G [64]
+  float* xlpg;                 // prep: per (chunk slot, value head) X^T, Lg, P [64][64], G [64]
   float* states;               // scan: the state entering each chunk [slot][Hv][DV][dk]
   float* vnew;                 // scan: V_new [tokens][Hv][DV]
 };

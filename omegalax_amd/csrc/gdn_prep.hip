@@ -331,7 +331,8 @@ __device__ __forceinline__ void put_f32_tile(float* m, int bi, int bj, f32x4 a) 
 }
 
 // BWD: also writes, per (chunk, value head), the fp32 matrices the backward pass reads
-// (X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in gdn_chunk.h).
+// (X^T with X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in
+// gdn_chunk.h).
 template <int DK, int MODE, bool BWD = false>
 __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
@@ -478,12 +479,13 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
       const auto rec = buf_rsrc(p.rec + ((size_t)ci * p.Hv + h) * rec_stride, (unsigned)rec_stride);
       float* xb = BWD ? p.xlpg + ((size_t)ci * p.Hv + h) * kXlpgFloats : nullptr;
       if constexpr (BWD) {
-        // the upper tiles of X, Lg and P are zero
+        // the lower tiles of X^T and the upper tiles of Lg and P are zero
         for (int z = wave; z < 18; z += 4) {
           const int mat = z / 6, u = z % 6;
           const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2);
           const int bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
-          put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
+          if (mat == 0) put_f32_tile(xb + kXlpgX, bj, bi, zero4());
+          else put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
         }
       }
 
@@ -610,7 +612,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
             // the record holds T diag(beta): column 16 bi + 4 lq + v scaled by its beta
             const f32x4 Tb = Ta * col_beta(gw, bi);
             put_tile(rec, rec_t_off(bi, bi), pack_hi4(Tb));
-            if constexpr (BWD) put_f32_tile(xb + kXlpgX, bi, bi, Ta);
+            if constexpr (BWD) put_f32_tile(xb + kXlpgX, bi, bi, Tc);  // X^T: the C layout
             put_tile(rec, rec_t_off(bi, bi) + kPairBytes, pack_lo4(Tb));
             if ((bi & 1) == 0) {
               // the zero upper tile (bi, bi + 1) that completes row block bi's last pair
@@ -671,7 +673,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
           Tl[i] = pack_lo4(Tij);
           const f32x4 Tb = TijT * col_beta(gw, j);  // T_ij diag(beta), A layout
           put_tile(rec, rec_t_off(i, j), pack_hi4(Tb));
-          if constexpr (BWD) put_f32_tile(xb + kXlpgX, i, j, TijT);
+          if constexpr (BWD) put_f32_tile(xb + kXlpgX, j, i, Tij);  // X^T: the C layout
           put_tile(rec, rec_t_off(i, j) + kPairBytes, pack_lo4(Tb));
         }
       }
