@@ -162,3 +162,10 @@ def test_bwd_long_memory_gates():
     g = np.log(np.random.default_rng(3).uniform(0.9, 0.9999, beta.shape)).astype(np.float32)
     check(run_gpu(q, k, v, g, beta, S0, do, dht, "bf16"),
           run_ref(q, k, v, g, beta, S0, do, dht, "bf16"), "bf16")
+
+
+def test_bwd_4096_tokens_gqa():
+    """64 chunks (C1's sequence length) with GQA and both state cotangents."""
+    say("bwd T=4096")
+    args = make(41, 1, 4096, 2, 4, 128, 128, "bf16")
+    check(run_gpu(*args, "bf16"), run_ref(*args, "bf16"), "bf16")

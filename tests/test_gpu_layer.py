@@ -133,3 +133,34 @@ def test_layer_c1_shape_batch_slice():
           for k_, v_ in t.items()}
     out3, S3, _ = gpu_prefill(t3, dims)
     assert torch.equal(out3, out[3:4]) and torch.equal(S3, S[3:4])
+
+
+def test_layer_c3_full_size_packed_equals_separate():
+    """Config C3 at full size: T=32768 packed as 8 Dirichlet-length sequences with carried
+    initial states (C1 heads, B=1).  Each sequence's output, final state and conv cache from
+    the packed call equal a separate call on that sequence (GPU vs GPU), and the shortest
+    sequence matches the oracle."""
+    say("layer C3 full size")
+    dims = dict(Hk=16, dk=128, Hv=32, dv=128)
+    d = W.varlen_inputs()
+    cu = d["cu_seqlens"]
+    S0 = d["initial_state"]
+    t = W.to_device({k_: v_ for k_, v_ in d.items() if k_ not in ("cu_seqlens", "initial_state")})
+    out, S, conv = gpu_prefill(t, dims, cu, S0)
+    lens = np.diff(cu)
+    for n in range(len(lens)):
+        s, e = int(cu[n]), int(cu[n + 1])
+        tn = {k_: (v_[:, s:e].contiguous() if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+              for k_, v_ in t.items()}
+        o_n, S_n, c_n = gpu_prefill(tn, dims, None, S0[n:n + 1])
+        assert rel(np_(o_n), np_(out[:, s:e])) < 1e-6, f"sequence {n}"
+        assert rel(np_(S_n), np_(S[n:n + 1])) < 1e-6, f"sequence {n}"
+        assert torch.equal(c_n, conv[n:n + 1])
+    n = int(np.argmin(lens))
+    s, e = int(cu[n]), int(cu[n + 1])
+    dn = {k_: (v_[:, s:e] if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+          for k_, v_ in d.items() if k_ not in ("cu_seqlens", "initial_state")}
+    ref, S_ref, conv_ref = ref_prefill(dn, dims, None, S0[n:n + 1])
+    assert rel(np_(out[:, s:e]), ref) < BF16_TOL
+    assert rel(np_(S[n:n + 1]), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv[n:n + 1]), conv_ref)

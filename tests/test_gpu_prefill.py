@@ -150,3 +150,34 @@ def test_chunk_split_sequence_equals_whole():
     o2, S2 = run_gpu(q[:, n:], k[:, n:], v[:, n:], g[:, n:], beta[:, n:], S1, "bf16")
     assert rel(np.concatenate([o1, o2], axis=1), o) < 1e-4
     assert rel(S2, S) < 1e-4
+
+
+def test_chunk_c4_full_size():
+    """Config C4 at full size (B=1, T=65536, Hk=16, Hv=64, bf16 N(0,1) q/k/v, e^g ~
+    U(0.9, 0.9999), beta = sigmoid(N(0,1))), drawn on the GPU from a seeded generator: the
+    call split at T/2 with the state carried equals the whole call, and a causal prefix
+    (T=4096) of key head 0's four value heads matches the oracle."""
+    from omegalax_amd import chunk_gated_delta_rule
+    say("chunk C4 full size")
+    T, Hk, Hv, d = 65536, 16, 64, 128
+    gen = torch.Generator(device="cuda").manual_seed(1004)
+    q = torch.randn((1, T, Hk, d), generator=gen, device="cuda").bfloat16()
+    k = torch.randn((1, T, Hk, d), generator=gen, device="cuda").bfloat16()
+    v = torch.randn((1, T, Hv, d), generator=gen, device="cuda").bfloat16()
+    g = torch.log(0.9 + 0.0999 * torch.rand((1, T, Hv), generator=gen, device="cuda"))
+    beta = torch.sigmoid(torch.randn((1, T, Hv), generator=gen, device="cuda")).bfloat16().float()
+    o, S = chunk_gated_delta_rule(q, k, v, g, beta, 64, output_final_state=True)
+    n = T // 2
+    o1, S1 = chunk_gated_delta_rule(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], 64,
+                                    output_final_state=True)
+    o2, S2 = chunk_gated_delta_rule(q[:, n:], k[:, n:], v[:, n:], g[:, n:], beta[:, n:], 64,
+                                    initial_state=S1, output_final_state=True)
+    torch.cuda.synchronize()
+    def trel(a, b):  # on the GPU: the full-size outputs are 2 GiB
+        return float((a - b).abs().max() / b.abs().max())
+    assert trel(o1, o[:, :n]) < 1e-6 and trel(o2, o[:, n:]) < 1e-6
+    assert trel(S2, S) < 1e-6
+    P = 4096
+    o_ref, _ = run_ref(np_(q[:, :P, :1]), np_(k[:, :P, :1]), np_(v[:, :P, :4]),
+                       np_(g[:, :P, :4]), np_(beta[:, :P, :4]), None, "bf16")
+    assert rel(np_(o[:, :P, :4]), o_ref) < BF16_TOL
