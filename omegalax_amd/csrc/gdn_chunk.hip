@@ -441,6 +441,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     // does not depend on S is read from LDS in one batch while the state update of
     // the previous chunk drains.
     constexpr int NSK = DK / 32;
+    // On the direct-load path Q S is formed after the state update: it is off the chain
+    // K S -> R -> T R -> S, and deferring its fragment reads halves the LDS traffic the
+    // chunk's first products wait for.
+    constexpr bool DEFER_QS = DIRECT && !IS;
     u32x4 kh[4][NSK], kl[4][NSK], qh[4][NSK], ql[4][NSK];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -448,7 +452,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
       for (int s2 = 0; s2 < NSK; ++s2) {
         if constexpr (DIRECT) {
           kh[i][s2] = kl[i][s2] = swz_frag(sK, 16 * i, 32 * s2);
-          qh[i][s2] = ql[i][s2] = swz_frag(sQ, 16 * i, 32 * s2);
+          if constexpr (!DEFER_QS) qh[i][s2] = ql[i][s2] = swz_frag(sQ, 16 * i, 32 * s2);
         } else {
           frag2<IS>(sK, K_LO, LDK, 16 * i, 32 * s2, kh[i][s2], kl[i][s2]);
           frag2<IS>(sQ, K_LO, LDK, 16 * i, 32 * s2, qh[i][s2], ql[i][s2]);
@@ -488,14 +492,14 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
 #pragma unroll
       for (int i = 0; i < 4; ++i) {  // eight independent accumulation chains
         KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
-        QS[i] = mm<IS, IS>(QS[i], sh[s2], sl[s2], qh[i][s2], ql[i][s2]);  // (Q S)^T
+        if constexpr (!DEFER_QS) QS[i] = mm<IS, IS>(QS[i], sh[s2], sl[s2], qh[i][s2], ql[i][s2]);  // (Q S)^T
       }
     if constexpr (DIRECT && !IS) {
       // all fragment reads go out back to back, then the state packs, then the
       // products: one LDS round trip for the phase instead of one per few products
-      __builtin_amdgcn_sched_group_barrier(0x100, 8 * NSK + 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4 * NSK + 4, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 4 * NSK, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 8 * NSK, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * NSK, 0);
     }
     // T operands of V_new = T R, one per block pair (read while the products run)
     u32x4 th[kNPairs], tl[kNPairs];
@@ -636,6 +640,17 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     // holds token 16i + r, columns 16w + 4q .. +3 of the wave's slice: one 16-byte (fp32)
     // or 8-byte (bf16) store per row block, and one gate factor per lane.
     if constexpr (BWD) return;
+    if constexpr (DEFER_QS) {
+      // (Q S)^T from the chunk's entering state, still held packed in sh
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int s2 = 0; s2 < NSK; ++s2) qh[i][s2] = swz_frag(sQ, 16 * i, 32 * s2);
+#pragma unroll
+      for (int s2 = 0; s2 < NSK; ++s2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) QS[i] = mma16(sh[s2], qh[i][s2], QS[i]);
+    }
     f32x4 o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
