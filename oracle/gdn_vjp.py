@@ -31,9 +31,10 @@ from __future__ import annotations
 
 import numpy as np
 
+from . import gdn_oracle as O
 from .gdn_oracle import _gqa_expand, _ident
 
-__all__ = ["chunk_gated_delta_rule_bwd", "chunk_bwd_core"]
+__all__ = ["chunk_gated_delta_rule_bwd", "chunk_bwd_core", "gdn_prefill_layer_bwd"]
 
 
 def _l2norm_fwd(x, eps, act_round):
@@ -244,3 +245,93 @@ def chunk_gated_delta_rule_bwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, do_BTHU,
     if keep:
         return out + (keeps,)
     return out
+
+
+# ----------------------------------------------------------------------------- layer VJP
+
+def _silu_grad(u):
+    s = 1.0 / (1.0 + np.exp(-u))
+    return s * (1.0 + u * (1.0 - s))
+
+
+def gdn_prefill_layer_bwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, dout, *, Hk, dk, Hv,
+                          dv, eps=1e-6, chunk_size=64, cu_seqlens=None, initial_state=None,
+                          d_final_state=None, act_round=_ident):
+    """VJP of ``gdn_oracle.gdn_prefill_layer`` (deltanet.py:243-293 between the projections
+    and out_proj) for the cotangent ``dout`` [B,T,Hv*dv] of its output and ``d_final_state``
+    of the final state.  Dtype casts are differentiated as the identity, as autodiff does.
+
+    Steps, in reverse of the forward:
+      gated RMSNorm (deltanet.py:282-293): n = o r, r = (mean(o^2) + eps)^-1/2,
+        out = w n silu(z): dn = dout w silu(z), dz = dout w n silu'(z),
+        dw = sum dout n silu(z), do = r (dn - n mean(dn n));
+      the chunked rule (:261-281): ``chunk_gated_delta_rule_bwd``;
+      gates (:248-250): beta = sigmoid(b) -> db = dbeta beta (1 - beta);
+        g = A softplus(a + dt_bias), A = -exp(A_log) -> da = dg A sigmoid(a + dt_bias),
+        d dt_bias = sum da, dA_log = sum dg g;
+      conv + SiLU (:35-50, 243): y = silu(u), u = sum_k w[c,k] x[t-K+1+k] ->
+        du = dy silu'(u), dx[s] = sum_k w[c,k] du[s+K-1-k], dw[c,k] = sum_t du[t] x[t-K+1+k],
+        each sequence on its own (zero history).
+    Returns (d_mixed_qkv, dz, da, db, d_conv_w, dA_log, d_dt_bias, d_norm_w, d_initial_state).
+    """
+    x = np.asarray(mixed_qkv, np.float64)
+    B, T, Cd = x.shape
+    w = act_round(np.asarray(conv_w, np.float32)).astype(np.float64)  # as the forward (:243)
+    K = w.shape[1]
+    seqs = ([(bb, 0, T) for bb in range(B)] if cu_seqlens is None else
+            [(0, int(s), int(e)) for s, e in zip(cu_seqlens[:-1], cu_seqlens[1:])])
+    # forward: conv pre-activation u and the rule's inputs
+    u = np.zeros_like(x)
+    for bb, s, e in seqs:
+        if e > s:
+            u[bb:bb + 1, s:e] = O.causal_depthwise_conv1d(x[bb:bb + 1, s:e], w)
+    u = act_round(u)
+    y = act_round(O.silu(u))
+    q, k, v = O.split_mixed_qkv(y, Hk, dk, Hv, dv)
+    g, beta = O.gates(a, b, A_log, dt_bias, act_round)
+    o, _ = O.chunk_gated_delta_rule(q, k, v, g, beta, chunk_size, initial_state=initial_state,
+                                    output_final_state=True, cu_seqlens=cu_seqlens,
+                                    act_round=act_round)
+    # gated RMSNorm
+    o2 = o.reshape(-1, dv)
+    z2 = np.asarray(z, np.float64).reshape(-1, dv)
+    wn = np.asarray(norm_w, np.float64)
+    d2 = np.asarray(dout, np.float64).reshape(-1, dv)
+    r = 1.0 / np.sqrt(np.mean(o2 * o2, axis=-1, keepdims=True) + eps)
+    n = o2 * r
+    sz = O.silu(z2)
+    dn = d2 * wn * sz
+    dz = (d2 * wn * n * _silu_grad(z2)).reshape(np.shape(z))
+    dnw = (d2 * n * sz).sum(0)
+    do = r * (dn - n * np.mean(dn * n, axis=-1, keepdims=True))
+    # the chunked rule
+    dq, dk_, dv_, dg, dbeta, dh0 = chunk_gated_delta_rule_bwd(
+        q, k, v, g, beta, do.reshape(B, T, Hv, dv), chunk_size, initial_state=initial_state,
+        dht=d_final_state, cu_seqlens=cu_seqlens, act_round=act_round)
+    # gates
+    a64 = np.asarray(a, np.float64)
+    b64 = np.asarray(b, np.float64)
+    sb = O.sigmoid(b64)
+    db = dbeta * sb * (1.0 - sb)
+    A = -np.exp(np.asarray(A_log, np.float64))
+    da = dg * A * O.sigmoid(a64 + np.asarray(dt_bias, np.float64))
+    d_dt_bias = da.sum((0, 1))
+    dA_log = (dg * g).sum((0, 1))
+    # conv + SiLU
+    dy = np.concatenate([dq.reshape(B, T, -1), dk_.reshape(B, T, -1), dv_.reshape(B, T, -1)], -1)
+    du = dy * _silu_grad(u)
+    dx = np.zeros_like(x)
+    dw = np.zeros_like(w)
+    for bb, s, e in seqs:
+        L = e - s
+        if L <= 0:
+            continue
+        xs, dus = x[bb, s:e], du[bb, s:e]
+        xp = np.concatenate([np.zeros((K - 1, Cd)), xs], 0)      # x[t - K + 1 + k] = xp[t + k]
+        for kk in range(K):
+            dw[:, kk] += (dus * xp[kk:kk + L]).sum(0)
+            # u[t] += w[k] x[t - K + 1 + k]: x[s'] feeds u[s' + K - 1 - k]
+            sh = K - 1 - kk
+            if sh < L:
+                dx[bb, s:e - sh] += w[:, kk] * dus[sh:]
+    return dx, dz, da, db, dw, dA_log, d_dt_bias, dnw, dh0

@@ -130,3 +130,55 @@ def test_vjp_oracle_single_token_closed_form():
     assert np.allclose(got[2], b * qk * c["do"], rtol=1e-12, atol=1e-14)
     assert np.allclose(got[4].ravel(), qk * float((c["v"] * c["do"]).sum()), rtol=1e-12)
     assert np.allclose(got[3], 0.0, atol=1e-14)  # S0 = 0: the decay multiplies nothing
+
+
+# ----------------------------------------------------------------------------- layer VJP
+
+def layer_case(seed, B=1, T=13, Hk=1, dk=4, Hv=2, dv=4, K=4):
+    rng = np.random.default_rng(seed)
+    Cd = 2 * Hk * dk + Hv * dv
+    return dict(
+        x=rng.standard_normal((B, T, Cd)), z=rng.standard_normal((B, T, Hv, dv)),
+        a=rng.standard_normal((B, T, Hv)), b=rng.standard_normal((B, T, Hv)),
+        # conv weights with at most 10 fractional bits: the forward casts them to float32,
+        # and w +- 2^-20 d with d = +-1 then stays exact there
+        w=np.round(512 * rng.standard_normal((Cd, K))) / 1024, A_log=rng.uniform(-1.5, 0.5, Hv),
+        dt=rng.uniform(-2, 0, Hv), nw=rng.uniform(0.5, 1.5, dv),
+        S0=0.3 * rng.standard_normal((B, Hv, dk, dv)),
+        dout=rng.standard_normal((B, T, Hv * dv)), dS=0.3 * rng.standard_normal((B, Hv, dk, dv)),
+        dims=dict(Hk=Hk, dk=dk, Hv=Hv, dv=dv))
+
+
+def layer_loss(c, C, cu=None, **over):
+    x = {**c, **over}
+    out, S, _ = O.gdn_prefill_layer(x["x"], x["z"], x["a"], x["b"], x["w"], x["A_log"], x["dt"],
+                                    x["nw"], **c["dims"], chunk_size=C, cu_seqlens=cu,
+                                    initial_state=x["S0"], act_round=lambda y: y)
+    return float((out * c["dout"]).sum() + (S * c["dS"]).sum())
+
+
+@pytest.mark.parametrize("C,cu", [(4, None), (64, None), (4, [0, 5, 5, 13])])
+def test_layer_vjp_oracle_matches_finite_differences(C, cu):
+    """Every input of the layer VJP against central differences of the pinned layer forward
+    (conv_w goes through the forward's float32 cast, so its direction is +-1 with a 2^-20
+    step, exact in float32)."""
+    c = layer_case(3)
+    if cu is not None:
+        cu = np.asarray(cu)
+        c["S0"] = 0.3 * np.random.default_rng(5).standard_normal((len(cu) - 1, 2, 4, 4))
+        c["dS"] = 0.3 * np.random.default_rng(6).standard_normal((len(cu) - 1, 2, 4, 4))
+    dx, dz, da, db, dw, dA, ddt, dnw, dh0 = V.gdn_prefill_layer_bwd(
+        c["x"], c["z"], c["a"], c["b"], c["w"], c["A_log"], c["dt"], c["nw"], c["dout"],
+        **c["dims"], chunk_size=C, cu_seqlens=cu, initial_state=c["S0"], d_final_state=c["dS"])
+    grads = dict(x=dx, z=dz, a=da, b=db, w=dw, A_log=dA, dt=ddt, nw=dnw, S0=dh0)
+    rng = np.random.default_rng(9)
+    for name, grad in grads.items():
+        eps, tol = (2.0 ** -20, 1e-7) if name == "w" else (1e-5, 1e-7)
+        for _ in range(2):
+            d = rng.standard_normal(np.shape(c[name]))
+            if name == "w":
+                d = np.sign(d)
+            fd = (layer_loss(c, C, cu, **{name: c[name] + eps * d})
+                  - layer_loss(c, C, cu, **{name: c[name] - eps * d})) / (2 * eps)
+            an = float((grad * d).sum())
+            assert abs(fd - an) <= tol * max(1.0, abs(fd)), (name, fd, an)
