@@ -187,6 +187,41 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
 size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
                                         int64_t dk, int64_t dv, int64_t N, int in_dtype);
 
+/*
+ * Backward pass (VJP) of omx_gdn_prefill: the gradients the reference's SFT step takes
+ * through GatedDeltaNet.__call__ between its projections and out_proj (deltanet.py:243-293,
+ * differentiated by jax.value_and_grad in trainers/vlm.py:157-195), for the cotangent
+ * d_out of the output (and d_final_state of the final state).  Inputs have the meaning and
+ * layout of omx_gdn_prefill (no conv history: conv windows start from zeros); the forward
+ * is recomputed inside.
+ *
+ *   d_out          [B, T, Hv*dv] bf16
+ *   d_final_state  [N, Hv, dk, dv] f32 or NULL (zeros)
+ *   d_mixed_qkv    [B, T, conv_dim] bf16;  dz [B, T, Hv, dv] bf16;  da, db [B, T, Hv] bf16
+ *   d_conv_w       [conv_dim, K] f32;  dA_log, d_dt_bias [Hv] f32;  d_norm_w [dv] f32
+ *   d_initial_state [N, Hv, dk, dv] f32 or NULL
+ * Compiled shapes: K = 4, dk 64/128, dv 64/128, Hv <= 256.
+ */
+int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                        const float* conv_w, const float* A_log, const float* dt_bias,
+                        const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                        const float* initial_state, const void* d_out,
+                        const float* d_final_state, void* d_mixed_qkv, void* dz, void* da,
+                        void* db, float* d_conv_w, float* dA_log, float* d_dt_bias,
+                        float* d_norm_w, float* d_initial_state, int64_t B, int64_t T,
+                        int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t K,
+                        int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Bytes of device workspace omx_gdn_prefill_bwd needs (16-byte aligned): that of
+ * omx_gdn_chunk_bwd for bf16 inputs, plus the recomputed conv output, gates, the rule's
+ * fp32 output and its cotangent, the rule's input gradients and partial sums of the
+ * parameter gradients.
+ */
+size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                                          int64_t dk, int64_t dv, int64_t N);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,10 @@ SIGNATURES = {
                                _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _sz,
                                _p]),
     "omx_gdn_chunk_bwd_workspace_size": (_sz, [_i64] * 7 + [_i]),
+    "omx_gdn_prefill_bwd": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _i64, _p, _p, _p, _p, _p,
+                                 _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _i64, _i64, _p, _sz, _p]),
+    "omx_gdn_prefill_bwd_workspace_size": (_sz, [_i64] * 7),
 }
 
 

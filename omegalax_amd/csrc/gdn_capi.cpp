@@ -136,7 +136,7 @@ extern "C" {
 
 const char* omx_gdn_last_error(void) { return g_last_error.c_str(); }
 
-int omx_gdn_abi_version(void) { return 102; }
+int omx_gdn_abi_version(void) { return 103; }
 
 int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
                         const float* conv_w, const float* A_log, const float* dt_bias,
@@ -457,6 +457,166 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
   b.nch = p.nch; b.n_rec = p.n_rec; b.in_f32 = f32 ? 1 : 0; b.qk_l2norm = p.qk_l2norm;
   b.scale = scale;
   return launch_status(omx::launch_bwd(b, st), fn);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------- layer backward
+namespace {
+
+// Workspace of the layer backward: the rule's backward workspace, then the recomputed
+// conv + SiLU output (q, k, v rows), g and beta, the rule's fp32 o and its cotangent, the
+// rule's gradients of q, k, v, g and beta, and the partial sums of the parameter gradients.
+struct LayerBwdWs {
+  BwdWs c;
+  size_t q, k, v, g, beta, o, dO, gq, gk, gv, dg, dbeta, pn, pg, pc, total;
+};
+
+LayerBwdWs layer_bwd_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                        int64_t N) {
+  LayerBwdWs w{};
+  w.c = bwd_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeBF16);
+  if (B < 0 || T < 0 || Hk < 0 || Hv < 0 || dk < 0 || dv < 0 || N < 0) return w;
+  const size_t tokens = (size_t)(B * T);
+  const size_t kd = (size_t)(Hk * dk), vd = (size_t)(Hv * dv), conv_dim = 2 * kd + vd;
+  size_t o = w.c.total;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += align_up(bytes, 256);
+    return at;
+  };
+  w.q = take(tokens * kd * 2);
+  w.k = take(tokens * kd * 2);
+  w.v = take(tokens * vd * 2);
+  w.g = take(tokens * (size_t)Hv * 4);
+  w.beta = take(tokens * (size_t)Hv * 4);
+  w.o = take(tokens * vd * 4);
+  w.dO = take(tokens * vd * 4);
+  w.gq = take(tokens * kd * 2);
+  w.gk = take(tokens * kd * 2);
+  w.gv = take(tokens * vd * 2);
+  w.dg = take(tokens * (size_t)Hv * 4);
+  w.dbeta = take(tokens * (size_t)Hv * 4);
+  w.pn = take((size_t)omx::layer_bwd_norm_blocks() * (size_t)dv * 4);
+  w.pg = take((size_t)omx::layer_bwd_gate_blocks((long long)tokens) * 2 * (size_t)Hv * 4);
+  w.pc = take((size_t)omx::layer_bwd_conv_blocks((long long)tokens) * conv_dim * 4 * 4);
+  w.total = o;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                          int64_t dv, int64_t N) {
+  return layer_bwd_ws(B, T, Hk, Hv, dk, dv, N).total;
+}
+
+int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                        const float* conv_w, const float* A_log, const float* dt_bias,
+                        const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                        const float* initial_state, const void* d_out,
+                        const float* d_final_state, void* d_mixed_qkv, void* dz, void* da,
+                        void* db, float* d_conv_w, float* dA_log, float* d_dt_bias,
+                        float* d_norm_w, float* d_initial_state, int64_t B, int64_t T,
+                        int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t K,
+                        int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const char* fn = "omx_gdn_prefill_bwd";
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
+  REQUIRE(K == 4, "%s: conv kernel size must be 4 (got %lld)", fn, (long long)K);
+  REQUIRE(B >= 0 && T >= 0, "%s: negative shape (B=%lld, T=%lld)", fn, (long long)B, (long long)T);
+  REQUIRE(B * T <= (int64_t)1 << 31, "%s: too many tokens (%lld)", fn, (long long)(B * T));
+  REQUIRE(eps >= 0.f && eps < 1.f, "%s: eps %g out of range", fn, (double)eps);
+  if (cu_seqlens) {
+    REQUIRE(B == 1, "%s: cu_seqlens requires batch 1 (got %lld)", fn, (long long)B);
+    REQUIRE(N >= 1 && N <= (1 << 20), "%s: sequence count %lld out of range", fn, (long long)N);
+  } else {
+    REQUIRE(N == B, "%s: without cu_seqlens N must equal B (%lld vs %lld)", fn, (long long)N,
+            (long long)B);
+  }
+  if (!omx::bwd_dims_supported((int)dk, (int)dv, false) || Hv > 256)
+    return fail(OMX_GDN_EUNSUPPORTED,
+                "%s: dk=%lld dv=%lld Hv=%lld not compiled (dk 64/128, dv 64/128, Hv <= 256)", fn,
+                (long long)dk, (long long)dv, (long long)Hv);
+  const LayerBwdWs ws = layer_bwd_ws(B, T, Hk, Hv, dk, dv, N);
+  REQUIRE(workspace_bytes >= ws.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, ws.total);
+  if (N == 0) return ok();
+  const int64_t tokens = B * T;
+  REQUIRE(conv_w && A_log && dt_bias && norm_w && d_conv_w && dA_log && d_dt_bias && d_norm_w,
+          "%s: a parameter or parameter-gradient pointer is NULL", fn);
+  if (tokens > 0)
+    REQUIRE(mixed_qkv && z && a && b && d_out && d_mixed_qkv && dz && da && db,
+            "%s: an activation or activation-gradient pointer is NULL", fn);
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(d_mixed_qkv, 16)),
+          "%s: mixed_qkv and d_mixed_qkv must be 16-byte aligned", fn);
+  REQUIRE(aligned(conv_w, 16), "%s: conv_w must be 16-byte aligned", fn);
+  char* base = (char*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  omx::LayerBwdParams lp{};
+  lp.x = (const uint16_t*)mixed_qkv; lp.conv_w = conv_w; lp.a = (const uint16_t*)a;
+  lp.b = (const uint16_t*)b; lp.A_log = A_log; lp.dt_bias = dt_bias; lp.z = (const uint16_t*)z;
+  lp.norm_w = norm_w; lp.dout = (const uint16_t*)d_out; lp.eps = eps;
+  lp.q = (uint16_t*)(base + ws.q); lp.k = (uint16_t*)(base + ws.k); lp.v = (uint16_t*)(base + ws.v);
+  lp.g = (float*)(base + ws.g); lp.beta = (float*)(base + ws.beta);
+  lp.o = (const float*)(base + ws.o); lp.dO = (float*)(base + ws.dO);
+  lp.grad_q = (uint16_t*)(base + ws.gq); lp.grad_k = (uint16_t*)(base + ws.gk);
+  lp.grad_v = (uint16_t*)(base + ws.gv);
+  lp.dg = (const float*)(base + ws.dg); lp.dbeta = (const float*)(base + ws.dbeta);
+  lp.part_norm = (float*)(base + ws.pn); lp.part_gates = (float*)(base + ws.pg);
+  lp.part_conv = (float*)(base + ws.pc);
+  lp.dx = (uint16_t*)d_mixed_qkv; lp.dz = (uint16_t*)dz; lp.da = (uint16_t*)da;
+  lp.db = (uint16_t*)db; lp.d_conv_w = d_conv_w; lp.dA_log = dA_log; lp.d_dt_bias = d_dt_bias;
+  lp.d_norm_w = d_norm_w; lp.cu_seqlens = cu_seqlens; lp.tokens = tokens;
+  lp.N = (int)N; lp.T = (int)T; lp.Hk = (int)Hk; lp.Hv = (int)Hv; lp.dk = (int)dk; lp.dv = (int)dv;
+  lp.conv_dim = (int)(2 * Hk * dk + Hv * dv);
+  // forward recompute: conv + SiLU, gates, then the rule's prep and scan (keeping o)
+  hipError_t e = omx::launch_layer_fwd_pieces(lp, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  omx::ChunkParams p{};
+  p.q = lp.q; p.k = lp.k; p.v = lp.v;
+  p.q_ld = Hk * dk; p.k_ld = Hk * dk; p.v_ld = Hv * dv;
+  p.g = lp.g; p.beta = lp.beta; p.o = (float*)(base + ws.o);
+  p.initial_state = initial_state; p.final_state = nullptr; p.cu_seqlens = cu_seqlens;
+  p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.DV = (int)dv;
+  p.nb = (int)(dv / omx::chunk_block_cols());
+  p.scale = 1.0f / sqrtf((float)dk); p.qk_l2norm = 1;
+  REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
+  REQUIRE(((B * T + 63) / 64 + N) * Hv <= INT32_MAX, "%s: grid too large", fn);
+  setup_chunked(p, ws.c.f, workspace, omx::kModeBF16);
+  p.xlpg = (float*)(base + ws.c.xlpg);
+  p.states = (float*)(base + ws.c.states);
+  p.vnew = (float*)(base + ws.c.vnew);
+  if (p.cu_seqlens) e = omx::launch_chunk_plan(p, st);
+  if (e == hipSuccess) e = omx::launch_prep_bwd(p, omx::kModeBF16, st);
+  if (e == hipSuccess) e = omx::launch_scan_bwd(p, omx::kModeBF16, st);
+  // the gated norm's adjoint gives the rule's cotangent
+  if (e == hipSuccess) e = omx::launch_layer_norm_bwd(lp, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  omx::BwdParams bp{};
+  bp.ks = p.ks; bp.qs = p.qs; bp.ks_ld = p.ks_ld; bp.qs_ld = p.qs_ld;
+  bp.v = lp.v; bp.dO = lp.dO; bp.dht = d_final_state; bp.rec = p.rec; bp.xlpg = p.xlpg;
+  bp.states = p.states; bp.vnew = p.vnew;
+  bp.dstates = (float*)(base + ws.c.dstates);
+  bp.dvnew = (float*)(base + ws.c.dvnew);
+  bp.dh0 = d_initial_state;
+  bp.dqh = (float*)(base + ws.c.dqh);
+  bp.dkh = (float*)(base + ws.c.dkh);
+  bp.dv = lp.grad_v; bp.dg = (float*)(base + ws.dg); bp.dbeta = (float*)(base + ws.dbeta);
+  bp.q = lp.q; bp.k = lp.k; bp.dq = lp.grad_q; bp.dk_out = lp.grad_k;
+  bp.cu_seqlens = cu_seqlens; bp.chunk_off = p.chunk_off;
+  bp.N = p.N; bp.T = p.T; bp.Hk = p.Hk; bp.Hv = p.Hv; bp.dk = p.dk; bp.DV = p.DV; bp.nb = p.nb;
+  bp.nch = p.nch; bp.n_rec = p.n_rec; bp.in_f32 = 0; bp.qk_l2norm = 1; bp.scale = p.scale;
+  e = omx::launch_bwd(bp, st);
+  // gates and conv + SiLU adjoints
+  if (e == hipSuccess) e = omx::launch_layer_tail_bwd(lp, st);
+  return launch_status(e, fn);
 }
 
 }  // extern "C"

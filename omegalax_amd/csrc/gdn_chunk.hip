@@ -262,8 +262,8 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                      (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
 }
 
-// BWD (the backward pass's recompute): stores the state entering every chunk and V_new
-// instead of o.
+// BWD (the backward pass's recompute): stores the state entering every chunk and V_new,
+// and o only when p.o is set.
 template <int DK, int MODE, bool BWD = false>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
@@ -639,7 +639,9 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     // both operand layouts hold "row r, contraction slots 8q .. 8q+7".  Lane (q, r) then
     // holds token 16i + r, columns 16w + 4q .. +3 of the wave's slice: one 16-byte (fp32)
     // or 8-byte (bf16) store per row block, and one gate factor per lane.
-    if constexpr (BWD) return;
+    if constexpr (BWD) {
+      if (!p.o) return;  // the layer backward also needs o (for its norm's adjoint)
+    }
     if constexpr (DEFER_QS) {
       // (Q S)^T from the chunk's entering state, still held packed in sh
 #pragma unroll

@@ -136,6 +136,56 @@ hipError_t launch_scan_bwd(const ChunkParams& p, int mode, hipStream_t stream);
 bool bwd_dims_supported(int dk, int dv, bool f32_inputs);
 hipError_t launch_bwd(const BwdParams& p, hipStream_t stream);
 
+// Backward of the layer prefill around the chunked rule's backward (gdn_layer_bwd.hip).
+// bf16 arrays are raw uint16_t.
+struct LayerBwdParams {
+  // forward inputs
+  const uint16_t* x;           // mixed_qkv [tokens][conv_dim]
+  const float* conv_w;         // [conv_dim][4]
+  const uint16_t* a;           // [tokens][Hv]
+  const uint16_t* b;
+  const float* A_log;          // [Hv]
+  const float* dt_bias;
+  const uint16_t* z;           // [tokens][Hv][dv]
+  const float* norm_w;         // [dv]
+  const uint16_t* dout;        // [tokens][Hv*dv], cotangent of the output
+  float eps;
+  // workspace: recomputed forward values and the rule's gradients
+  uint16_t* q;                 // conv + SiLU output split: q, k [tokens][Hk*dk], v [tokens][Hv*dv]
+  uint16_t* k;
+  uint16_t* v;
+  float* g;                    // [tokens][Hv]
+  float* beta;
+  const float* o;              // the rule's fp32 output [tokens][Hv][dv]
+  float* dO;                   // its cotangent
+  uint16_t* grad_q;            // gradients of q, k, v (bf16)
+  uint16_t* grad_k;
+  uint16_t* grad_v;
+  const float* dg;             // [tokens][Hv]
+  const float* dbeta;
+  float* part_norm;            // partial sums [norm blocks][dv]
+  float* part_gates;           // [gate blocks][2 Hv]
+  float* part_conv;            // [conv blocks][conv_dim][4]
+  // outputs
+  uint16_t* dx;                // d mixed_qkv
+  uint16_t* dz;
+  uint16_t* da;
+  uint16_t* db;
+  float* d_conv_w;             // [conv_dim][4]
+  float* dA_log;               // [Hv]
+  float* d_dt_bias;            // [Hv]
+  float* d_norm_w;             // [dv]
+  const int32_t* cu_seqlens;
+  long long tokens;
+  int N, T, Hk, Hv, dk, dv, conv_dim;
+};
+int layer_bwd_norm_blocks();
+long long layer_bwd_conv_blocks(long long tokens);
+int layer_bwd_gate_blocks(long long tokens);
+hipError_t launch_layer_fwd_pieces(const LayerBwdParams& p, hipStream_t stream);
+hipError_t launch_layer_norm_bwd(const LayerBwdParams& p, hipStream_t stream);
+hipError_t launch_layer_tail_bwd(const LayerBwdParams& p, hipStream_t stream);
+
 // Gated RMSNorm of the layer prefill from bf16 o: out = w * o * rsqrt(mean(o^2) + eps)
 // * silu(z) per (token, value head) row of dv (dv / 8 at most 32).
 hipError_t launch_norm_epilogue(const void* o_part, const void* z, const float* norm_w, void* out,

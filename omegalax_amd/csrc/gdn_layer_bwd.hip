@@ -1,0 +1,405 @@
+// Backward pass of the GatedDeltaNet layer prefill (omx_gdn_prefill_bwd): the parts
+// around the chunked rule's backward (gdn_bwd.hip).
+//
+// Forward (deltanet.py:243-293, between the projections and out_proj):
+//   u = conv(x, w) (causal depthwise, K = 4, bf16), y = silu(u) (bf16), y = [q | k | v];
+//   beta = sigmoid(b) (bf16), g = -exp(A_log) softplus(a + dt_bias);
+//   o = chunk_gated_delta_rule(q, k, v, g, beta) (fp32);
+//   out = w_n * o * rsqrt(mean(o^2) + eps) * silu(z).
+// Kernels here, in the order the backward runs them:
+//   conv_silu_split_kernel  y from x and w, as the forward's prep computes it, into
+//                           separate q, k, v rows for the rule's backward;
+//   gates_kernel            g and beta per (token, value head);
+//   norm_bwd_kernel         the gated RMSNorm's adjoint: do, dz and per-workgroup partial
+//                           sums of dw_n (o comes from the rule's recompute scan);
+//   gates_bwd_kernel        da, db and per-workgroup partial sums of dA_log, d dt_bias;
+//   conv_bwd_kernel         du = dy silu'(u), dx (the transposed conv) and per-token-block
+//                           partial sums of dw;
+//   col_reduce_kernel       the partial sums in a fixed order (deterministic results).
+// Dtype casts are differentiated as the identity, as autodiff does.
+#include "gdn_chunk.h"
+#include "gdn_kernels.h"
+
+namespace omx {
+
+namespace {
+
+constexpr int NT = 256;
+
+// Sequence bounds of token t: packed sequences (cu_seqlens, clamped by seq_range) or batch
+// rows of length T.
+__device__ __forceinline__ void token_seq(const int32_t* cu, int N, int T, long long t,
+                                          long long& s0, long long& s1) {
+  if (cu) {
+    int lo = 0, hi = N;  // the last n with cu[n] <= t
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cu[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    seq_range(cu, lo, T, s0, s1);
+  } else {
+    s0 = (t / T) * T;
+    s1 = s0 + T;
+  }
+}
+
+// conv weights of channels c0 .. c0+7 cast to bf16 (deltanet.py:243): wt[e][d] multiplies
+// the input d tokens back (tap K-1-d); K = 4
+__device__ __forceinline__ void conv_w8(const float* w, int c0, float (*wt)[4]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float4 x = *(const float4*)(w + (size_t)(c0 + e) * 4);
+    wt[e][0] = round_bf(x.w);
+    wt[e][1] = round_bf(x.z);
+    wt[e][2] = round_bf(x.y);
+    wt[e][3] = round_bf(x.x);
+  }
+}
+
+__device__ __forceinline__ void load8(const bf16_t* p, float* x) {
+  const u32x4 w = *(const u32x4*)p;
+  unpack8<false>(&w, x);
+}
+
+__device__ __forceinline__ void zero8(float* x) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = 0.f;
+}
+
+// the forward's conv pre-activation, rounded to bf16 as there
+__device__ __forceinline__ float conv_u(const float* wt, float x0, float x1, float x2, float x3) {
+  return round_bf(wt[0] * x0 + wt[1] * x1 + wt[2] * x2 + wt[3] * x3);
+}
+
+// d silu(u) / du
+__device__ __forceinline__ float silu_grad(float u) {
+  const float s = 1.0f / (1.0f + __expf(-u));
+  return s * (1.0f + u * (1.0f - s));
+}
+
+// ---------------------------------------------------------------------------- forward pieces
+
+// one thread per (token, 8-channel group)
+__global__ __launch_bounds__(NT) void conv_silu_split_kernel(LayerBwdParams p) {
+  const int G = p.conv_dim / 8;
+  const long long idx = (long long)blockIdx.x * NT + threadIdx.x;
+  if (idx >= p.tokens * G) return;
+  const long long t = idx / G;
+  const int c0 = 8 * (int)(idx % G);
+  long long s0, s1;
+  token_seq(p.cu_seqlens, p.N, p.T, t, s0, s1);
+  float wt[8][4];
+  conv_w8(p.conv_w, c0, wt);
+  float xs[4][8];  // inputs d tokens back
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (t - d >= s0) load8(p.x + (t - d) * p.conv_dim + c0, xs[d]);
+    else zero8(xs[d]);
+  }
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    y[e] = round_bf(silu_fast(conv_u(wt[e], xs[0][e], xs[1][e], xs[2][e], xs[3][e])));
+  const int kd = p.Hk * p.dk;
+  bf16_t* dst;
+  if (c0 < kd) dst = p.q + t * kd + c0;
+  else if (c0 < 2 * kd) dst = p.k + t * kd + (c0 - kd);
+  else dst = p.v + t * (long long)(p.Hv * p.dv) + (c0 - 2 * kd);
+  *(u32x4*)dst = pack8(y);
+}
+
+// one thread per (token, value head): g and beta as the forward's prep forms them
+__global__ __launch_bounds__(NT) void gates_kernel(LayerBwdParams p) {
+  const long long idx = (long long)blockIdx.x * NT + threadIdx.x;
+  if (idx >= p.tokens * p.Hv) return;
+  const int h = (int)(idx % p.Hv);
+  p.g[idx] = -expf(p.A_log[h]) * softplusf_(bf2f(p.a[idx]) + p.dt_bias[h]);
+  p.beta[idx] = round_bf(sigmoidf_(bf2f(p.b[idx])));
+}
+
+// ---------------------------------------------------------------------------- gated RMSNorm
+
+// Persistent: each wavefront walks (token, value head) rows of dv <= 128 (lane: columns l and
+// l + 64).  n = o r, r = (mean(o^2) + eps)^-1/2, out = w n silu(z):
+//   dn = dout w silu(z), dz = dout w n silu'(z), dw = sum dout n silu(z),
+//   do = r (dn - n mean(dn n)).
+__global__ __launch_bounds__(NT) void norm_bwd_kernel(LayerBwdParams p) {
+  __shared__ float sdw[NT / 64][128];
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int dv = p.dv;
+  const long long rows = p.tokens * p.Hv;
+  const long long nw = (long long)gridDim.x * (NT / 64);
+  float w[2], dw[2] = {0.f, 0.f};
+#pragma unroll
+  for (int e = 0; e < 2; ++e) w[e] = l + 64 * e < dv ? p.norm_w[l + 64 * e] : 0.f;
+  for (long long r = (long long)blockIdx.x * (NT / 64) + wave; r < rows; r += nw) {
+    float o[2], z[2], go[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = l + 64 * e;
+      const bool in = c < dv;
+      o[e] = in ? p.o[r * dv + c] : 0.f;
+      z[e] = in ? bf2f(p.z[r * dv + c]) : 0.f;
+      go[e] = in ? bf2f(p.dout[r * dv + c]) : 0.f;
+    }
+    float ss = o[0] * o[0] + o[1] * o[1];
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) ss += __shfl_xor(ss, s);
+    const float rr = rsqrtf(ss / (float)dv + p.eps);
+    float n[2], dn[2], dnn = 0.f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      n[e] = o[e] * rr;
+      const float sz = siluf_(z[e]);
+      dn[e] = go[e] * w[e] * sz;
+      dnn += dn[e] * n[e];
+      dw[e] += go[e] * n[e] * sz;
+      const int c = l + 64 * e;
+      if (c < dv) p.dz[r * dv + c] = f2bf(go[e] * w[e] * n[e] * silu_grad(z[e]));
+    }
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) dnn += __shfl_xor(dnn, s);
+    const float m = dnn / (float)dv;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = l + 64 * e;
+      if (c < dv) p.dO[r * dv + c] = rr * (dn[e] - n[e] * m);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+    if (l + 64 * e < dv) sdw[wave][l + 64 * e] = dw[e];
+  __syncthreads();
+  if (threadIdx.x < dv) {
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < NT / 64; ++v) s += sdw[v][threadIdx.x];
+    p.part_norm[(size_t)blockIdx.x * dv + threadIdx.x] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------- gates
+
+// Workgroup w takes a contiguous token range; thread (j, h) = (tid / Hv, tid % Hv) walks its
+// tokens j, j + R, ... (R = 256 / Hv) for value head h.
+//   da = dg A sigmoid(a + dt_bias), A = -exp(A_log); db = dbeta sigmoid(b)(1 - sigmoid(b));
+//   dA_log = sum dg g, d dt_bias = sum da.
+__global__ __launch_bounds__(NT) void gates_bwd_kernel(LayerBwdParams p, long long per) {
+  __shared__ float sacc[NT][2];
+  const int Hv = p.Hv, tid = threadIdx.x;
+  const int R = NT / Hv;
+  const int h = tid % Hv, j = tid / Hv;
+  float sA = 0.f, sdt = 0.f;
+  if (j < R) {
+    const float A = -expf(p.A_log[h]), dtb = p.dt_bias[h];
+    const long long t0 = (long long)blockIdx.x * per;
+    const long long t1 = t0 + per < p.tokens ? t0 + per : p.tokens;
+    for (long long t = t0 + j; t < t1; t += R) {
+      const long long i = t * Hv + h;
+      const float dgv = p.dg[i];
+      const float da = dgv * A * sigmoidf_(bf2f(p.a[i]) + dtb);
+      const float sb = sigmoidf_(bf2f(p.b[i]));
+      p.da[i] = f2bf(da);
+      p.db[i] = f2bf(p.dbeta[i] * sb * (1.f - sb));
+      sA += dgv * p.g[i];
+      sdt += da;
+    }
+  }
+  sacc[tid][0] = sA;
+  sacc[tid][1] = sdt;
+  __syncthreads();
+  if (tid < Hv) {
+    float a0 = 0.f, a1 = 0.f;
+    for (int jj = 0; jj < R; ++jj) {
+      a0 += sacc[jj * Hv + tid][0];
+      a1 += sacc[jj * Hv + tid][1];
+    }
+    p.part_gates[(size_t)blockIdx.x * 2 * Hv + tid] = a0;
+    p.part_gates[(size_t)blockIdx.x * 2 * Hv + Hv + tid] = a1;
+  }
+}
+
+// ---------------------------------------------------------------------------- conv + SiLU
+
+// One thread per (64-token block, 8-channel group).  du = dy silu'(u) with u recomputed;
+// dx[s] = sum_d wt[d] du[s + d] over s + d inside s's sequence (the transposed conv);
+// dwt[d] = sum_t du[t] x[t - d] (x = 0 before the sequence start), written per token block.
+constexpr int kConvTB = 64;
+
+__global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
+  const int G = p.conv_dim / 8;
+  const long long nblk = (p.tokens + kConvTB - 1) / kConvTB;
+  const long long idx = (long long)blockIdx.x * NT + threadIdx.x;
+  if (idx >= nblk * G) return;
+  const long long blk = idx / G;
+  const int c0 = 8 * (int)(idx % G);
+  const int kd = p.Hk * p.dk;
+  const long long vd = (long long)p.Hv * p.dv;
+  const bf16_t* dys;
+  long long dy_ld;
+  int dy_c;
+  if (c0 < kd) { dys = p.grad_q; dy_ld = kd; dy_c = c0; }
+  else if (c0 < 2 * kd) { dys = p.grad_k; dy_ld = kd; dy_c = c0 - kd; }
+  else { dys = p.grad_v; dy_ld = vd; dy_c = c0 - 2 * kd; }
+  float wt[8][4];
+  conv_w8(p.conv_w, c0, wt);
+  const long long tb = blk * kConvTB;
+  const long long te = tb + kConvTB < p.tokens ? tb + kConvTB : p.tokens;
+  float dwt[8][4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) dwt[e][d] = 0.f;
+  // rolling windows: xs[d] = x[t - d]; dus[d] = du[t - d] (the last four du computed)
+  float xs[4][8], dus[4][8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    zero8(xs[d]);
+    zero8(dus[d]);
+  }
+  long long cs0, cs1;  // sequence of the current token t
+  token_seq(p.cu_seqlens, p.N, p.T, tb, cs0, cs1);
+#pragma unroll
+  for (int d = 1; d < 4; ++d)
+    if (tb - d >= cs0) load8(p.x + (tb - d) * p.conv_dim + c0, xs[d]);
+  const long long tend = te + 3 < p.tokens ? te + 3 : p.tokens;
+  for (long long t = tb; t < tend; ++t) {
+    if (t >= cs1) {  // a new sequence starts at t: no history
+      token_seq(p.cu_seqlens, p.N, p.T, t, cs0, cs1);
+#pragma unroll
+      for (int d = 1; d < 4; ++d) zero8(xs[d]);
+    }
+    load8(p.x + t * p.conv_dim + c0, xs[0]);
+    float dy[8];
+    load8(dys + t * dy_ld + dy_c, dy);
+    float du[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      du[e] = dy[e] * silu_grad(conv_u(wt[e], xs[0][e], xs[1][e], xs[2][e], xs[3][e]));
+    if (t < te) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) dwt[e][d] += du[e] * xs[d][e];
+    }
+    // shift the du window; a sequence boundary cuts it (du of another sequence is 0 here)
+#pragma unroll
+    for (int d = 3; d > 0; --d)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dus[d][e] = dus[d - 1][e];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dus[0][e] = du[e];
+    // dx[s] for s = t - 3 needs du[s .. s + 3] = dus[3 .. 0]; terms past s's sequence end
+    // are dropped (tokens s + d >= end(s) belong to the next sequence)
+    const long long s = t - 3;
+    if (s >= tb && s < te) {
+      long long ss0, ss1;
+      token_seq(p.cu_seqlens, p.N, p.T, s, ss0, ss1);
+      float dx[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          if (s + d < ss1) acc += wt[e][d] * dus[3 - d][e];
+        dx[e] = acc;
+      }
+      *(u32x4*)(p.dx + s * p.conv_dim + c0) = pack8(dx);
+    }
+#pragma unroll
+    for (int d = 3; d > 0; --d)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[d][e] = xs[d - 1][e];
+  }
+  // the block's last tokens whose du window runs past the end of all tokens
+  for (long long s = (te - 3 > tb ? te - 3 : tb); s < te; ++s) {
+    if (s + 3 < tend) continue;  // already written in the loop
+    long long ss0, ss1;
+    token_seq(p.cu_seqlens, p.N, p.T, s, ss0, ss1);
+    const long long last = tend - 1;  // dus[0] holds du[last]
+    float dx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = 0.f;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const long long tt = s + d;
+        const int back = (int)(last - tt);
+        if (tt < ss1 && tt <= last && back < 4) {
+          float v = 0.f;
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if (b == back) v = dus[b][e];
+          acc += wt[e][d] * v;
+        }
+      }
+      dx[e] = acc;
+    }
+    *(u32x4*)(p.dx + s * p.conv_dim + c0) = pack8(dx);
+  }
+  // partial dw in [c][k] order (k = 3 - d)
+  float* part = p.part_conv + (size_t)blk * p.conv_dim * 4 + (size_t)c0 * 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    *(float4*)(part + 4 * e) = float4{dwt[e][3], dwt[e][2], dwt[e][1], dwt[e][0]};
+}
+
+// out[c] = sum over rows r (in order) of part[r * stride + off + c], c < ncols
+__global__ __launch_bounds__(NT) void col_reduce_kernel(const float* part, long long nrows,
+                                                        int stride, int off, int ncols, float* out) {
+  const int c = blockIdx.x * NT + threadIdx.x;
+  if (c >= ncols) return;
+  float s = 0.f;
+  for (long long r = 0; r < nrows; ++r) s += part[r * stride + off + c];
+  out[c] = s;
+}
+
+}  // namespace
+
+int layer_bwd_norm_blocks() { return 1024; }
+
+long long layer_bwd_conv_blocks(long long tokens) { return (tokens + kConvTB - 1) / kConvTB; }
+
+int layer_bwd_gate_blocks(long long tokens) {
+  const long long b = (tokens + 255) / 256;
+  return (int)(b < 1024 ? (b < 1 ? 1 : b) : 1024);
+}
+
+hipError_t launch_layer_fwd_pieces(const LayerBwdParams& p, hipStream_t stream) {
+  const long long n1 = p.tokens * (p.conv_dim / 8);
+  if (n1 > 0) {
+    hipLaunchKernelGGL(conv_silu_split_kernel, dim3((unsigned)((n1 + NT - 1) / NT)), dim3(NT), 0,
+                       stream, p);
+    const long long n2 = p.tokens * p.Hv;
+    hipLaunchKernelGGL(gates_kernel, dim3((unsigned)((n2 + NT - 1) / NT)), dim3(NT), 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_layer_norm_bwd(const LayerBwdParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(norm_bwd_kernel, dim3(layer_bwd_norm_blocks()), dim3(NT), 0, stream, p);
+  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.dv + NT - 1) / NT), dim3(NT), 0, stream,
+                     (const float*)p.part_norm, (long long)layer_bwd_norm_blocks(), p.dv, 0, p.dv,
+                     p.d_norm_w);
+  return hipGetLastError();
+}
+
+hipError_t launch_layer_tail_bwd(const LayerBwdParams& p, hipStream_t stream) {
+  const int gb = layer_bwd_gate_blocks(p.tokens);
+  const long long per = (p.tokens + gb - 1) / gb;
+  hipLaunchKernelGGL(gates_bwd_kernel, dim3(gb), dim3(NT), 0, stream, p, per);
+  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.Hv + NT - 1) / NT), dim3(NT), 0, stream,
+                     (const float*)p.part_gates, (long long)gb, 2 * p.Hv, 0, p.Hv, p.dA_log);
+  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.Hv + NT - 1) / NT), dim3(NT), 0, stream,
+                     (const float*)p.part_gates, (long long)gb, 2 * p.Hv, p.Hv, p.Hv, p.d_dt_bias);
+  const long long nblk = layer_bwd_conv_blocks(p.tokens);
+  const long long n = nblk * (p.conv_dim / 8);
+  if (n > 0)
+    hipLaunchKernelGGL(conv_bwd_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, stream, p);
+  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.conv_dim * 4 + NT - 1) / NT), dim3(NT), 0, stream,
+                     (const float*)p.part_conv, nblk, p.conv_dim * 4, 0, p.conv_dim * 4, p.d_conv_w);
+  return hipGetLastError();
+}
+
+}  // namespace omx

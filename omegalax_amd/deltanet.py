@@ -18,7 +18,7 @@ from . import _lib
 
 __all__ = [
     "chunk_gated_delta_rule", "chunk_gated_delta_rule_bwd", "recurrent_gated_delta_rule_step",
-    "gdn_prefill",
+    "gdn_prefill", "gdn_prefill_bwd",
     "gdn_decode_step", "GDNError",
 ]
 
@@ -233,9 +233,9 @@ def recurrent_gated_delta_rule_step(q, k, v, g, beta, state, *, scale=None):
     return o
 
 
-def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_heads, head_k_dim,
-                num_v_heads, head_v_dim, eps=1e-6, chunk_size=64, cu_seqlens=None,
-                initial_state=None, conv_state=None, output_final_state=False):
+def _gdn_prefill_fwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_heads, head_k_dim,
+                     num_v_heads, head_v_dim, eps=1e-6, chunk_size=64, cu_seqlens=None,
+                     initial_state=None, conv_state=None, output_final_state=False):
     """Prefill from projection outputs to the gated-norm output (deltanet.py:243-293).
 
     mixed_qkv [B,T,conv_dim] bf16, z [B,T,Hv,dv] bf16 (or [B,T,Hv*dv]), a/b [B,T,Hv] bf16,
@@ -278,6 +278,115 @@ def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_hea
               _ptr(fs), _ptr(conv_state), _ptr(cs), _ptr(out), B, T, Hk, Hv, dk, dv, K,
               int(chunk_size), _ptr(ws), ws_bytes, _stream(dev))
     return (out, fs, cs) if output_final_state else out
+
+
+def gdn_prefill_bwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, d_out, *, num_k_heads,
+                    head_k_dim, num_v_heads, head_v_dim, eps=1e-6, chunk_size=64,
+                    cu_seqlens=None, initial_state=None, d_final_state=None):
+    """Gradients of ``gdn_prefill`` (deltanet.py:243-293 between the projections and
+    out_proj, as the reference's training step differentiates it) for the cotangent
+    ``d_out`` [B,T,Hv*dv] of its output and ``d_final_state`` of the final state.
+
+    Returns (d_mixed_qkv, dz, da, db) at the activations' bf16 and (d_conv_w, dA_log,
+    d_dt_bias, d_norm_w, d_initial_state) in fp32.  Conv windows start from zeros (no conv
+    history input).
+    """
+    Hk, dk, Hv, dv = num_k_heads, head_k_dim, num_v_heads, head_v_dim
+    x = mixed_qkv.contiguous()
+    z = z.contiguous()
+    a, b = a.contiguous(), b.contiguous()
+    d_out = d_out.to(torch.bfloat16).contiguous()
+    conv_w, A_log, dt_bias, norm_w = (_f32(t) for t in (conv_w, A_log, dt_bias, norm_w))
+    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, cu_seqlens, initial_state, d_out,
+               d_final_state)
+    for name, t in (("mixed_qkv", x), ("z", z), ("a", a), ("b", b)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bf16")
+    B, T, Cd = x.shape
+    K = conv_w.shape[1]
+    if Cd != 2 * Hk * dk + Hv * dv or conv_w.shape[0] != Cd:
+        raise ValueError("mixed_qkv / conv_w channel count does not match the head layout")
+    if z.numel() != B * T * Hv * dv or d_out.numel() != B * T * Hv * dv:
+        raise ValueError("z / d_out size does not match the head layout")
+    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
+    if initial_state is not None:
+        initial_state = _f32(initial_state)
+    if d_final_state is not None:
+        d_final_state = _f32(d_final_state)
+    dx = torch.empty_like(x)
+    dz = torch.empty_like(z)
+    da = torch.empty_like(a)
+    db = torch.empty_like(b)
+    dconv = torch.empty_like(conv_w)
+    dA = torch.empty_like(A_log)
+    ddt = torch.empty_like(dt_bias)
+    dnw = torch.empty_like(norm_w)
+    dh0 = torch.empty((N, Hv, dk, dv), dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    ws_bytes = L.omx_gdn_prefill_bwd_workspace_size(B, T, Hk, Hv, dk, dv, N)
+    ws = _workspace(ws_bytes, dev)
+    _lib.call("omx_gdn_prefill_bwd", _ptr(x), _ptr(z), _ptr(a), _ptr(b), _ptr(conv_w),
+              _ptr(A_log), _ptr(dt_bias), _ptr(norm_w), float(eps), _ptr(cu_seqlens), N,
+              _ptr(initial_state), _ptr(d_out), _ptr(d_final_state), _ptr(dx), _ptr(dz),
+              _ptr(da), _ptr(db), _ptr(dconv), _ptr(dA), _ptr(ddt), _ptr(dnw), _ptr(dh0),
+              B, T, Hk, Hv, dk, dv, K, int(chunk_size), _ptr(ws), ws_bytes, _stream(dev))
+    return dx, dz, da, db, dconv, dA, ddt, dnw, dh0
+
+
+class _GDNPrefill(torch.autograd.Function):
+    """Autograd node of the layer prefill: forward omx_gdn_prefill, backward
+    omx_gdn_prefill_bwd (which recomputes the forward)."""
+
+    @staticmethod
+    def forward(ctx, x, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state, cu_seqlens, cfg):
+        out, fs, cs = _gdn_prefill_fwd(x, z, a, b, conv_w, A_log, dt_bias, norm_w,
+                                       cu_seqlens=cu_seqlens, initial_state=initial_state,
+                                       output_final_state=True, **cfg)
+        ctx.save_for_backward(x, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state,
+                              cu_seqlens)
+        ctx.cfg = cfg
+        ctx.set_materialize_grads(False)
+        ctx.mark_non_differentiable(cs)
+        return out, fs, cs
+
+    @staticmethod
+    def backward(ctx, d_out, d_fs, _d_cs):
+        x, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state, cu_seqlens = ctx.saved_tensors
+        if d_out is None:
+            d_out = torch.zeros((x.shape[0], x.shape[1], ctx.cfg["num_v_heads"] * ctx.cfg["head_v_dim"]),
+                                dtype=torch.bfloat16, device=x.device)
+        dx, dz, da, db, dconv, dA, ddt, dnw, dh0 = gdn_prefill_bwd(
+            x, z, a, b, conv_w, A_log, dt_bias, norm_w, d_out, cu_seqlens=cu_seqlens,
+            initial_state=initial_state, d_final_state=d_fs, **ctx.cfg)
+        return (dx, dz.view(z.shape), da, db, dconv, dA, ddt, dnw,
+                dh0 if initial_state is not None else None, None, None)
+
+
+def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_heads, head_k_dim,
+                num_v_heads, head_v_dim, eps=1e-6, chunk_size=64, cu_seqlens=None,
+                initial_state=None, conv_state=None, output_final_state=False):
+    """Prefill from projection outputs to the gated-norm output (deltanet.py:243-293).
+
+    mixed_qkv [B,T,conv_dim] bf16, z [B,T,Hv,dv] bf16 (or [B,T,Hv*dv]), a/b [B,T,Hv] bf16,
+    conv_w [conv_dim,K], A_log/dt_bias [Hv], norm_w [dv].  Returns out [B,T,Hv*dv] bf16,
+    or (out, final_state, conv_state_out) when ``output_final_state``.  When gradients are
+    enabled and an input requires them (and no conv history is passed), the call is recorded
+    for autograd; its backward runs omx_gdn_prefill_bwd.
+    """
+    cfg = dict(num_k_heads=num_k_heads, head_k_dim=head_k_dim, num_v_heads=num_v_heads,
+               head_v_dim=head_v_dim, eps=eps, chunk_size=chunk_size)
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad
+        for t in (mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state))
+    if needs_grad:
+        if conv_state is not None:
+            raise ValueError("gdn_prefill: gradients through a conv history are not supported")
+        out, fs, cs = _GDNPrefill.apply(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
+                                        initial_state, cu_seqlens, cfg)
+        return (out, fs, cs) if output_final_state else out
+    return _gdn_prefill_fwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
+                            cu_seqlens=cu_seqlens, initial_state=initial_state,
+                            conv_state=conv_state, output_final_state=output_final_state, **cfg)
 
 
 def gdn_decode_step(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, conv_state, state, *,

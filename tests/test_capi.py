@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().omx_gdn_abi_version() == 102
+    assert _lib.lib().omx_gdn_abi_version() == 103
 
 
 def _decode(**over):
