@@ -12,6 +12,7 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
            (C1 by default; C4 is --batch 1 --seq-len 65536 --v-heads 64).
   bwd      one chunk_gated_delta_rule_bwd call (the VJP: forward recompute, reverse state-
            gradient scan, chunk-parallel gradients) at the core workload's shape.
+  layer_bwd one gdn_prefill_bwd call at C1 (the layer's VJP: conv, gates, rule, gated norm).
   copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
 rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
@@ -227,6 +228,27 @@ def bench_bwd(B, T, Hk, Hv, d, steps, warmup):
     }
 
 
+def bench_layer_bwd(steps, warmup, B=4, T=4096):
+    """One gdn_prefill_bwd call at C1 (bf16 activations, bf16 output cotangent)."""
+    import torch
+    from omegalax_amd import gdn_prefill_bwd, workloads as W
+    Hk, Hv, d = 16, 32, 128
+    arrs = W.layer_inputs(B, T, Hk, Hv, d, d)
+    t = W.to_device(arrs)
+    rng = np.random.default_rng(9)
+    dout = torch.from_numpy(rng.standard_normal((B, T, Hv * d), dtype=np.float32)).cuda().bfloat16()
+    dims = dict(num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+
+    def step():
+        gdn_prefill_bwd(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                        t["dt_bias"], t["norm_w"], dout, **dims)
+
+    _say(f"layer_bwd: B={B} T={T} timing {steps} calls")
+    wall, ms = time_launches(step, steps, warmup)
+    return {"ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+            "tokens_per_s": B * T * steps / wall}
+
+
 # ----------------------------------------------------------------------------- prefill (C1)
 
 def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
@@ -282,7 +304,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "copy"],
+    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "layer_bwd", "copy"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -313,6 +335,19 @@ def main():
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "f32", "data": "synthetic",
                           "config": {"workload": "256 MiB read + 256 MiB written"}}), flush=True)
+        return 0
+    if args.workload == "layer_bwd":
+        res = bench_layer_bwd(args.steps, args.warmup)
+        line = {
+            "metric": "gdn_prefill_bwd tokens/s (GDN layer backward, config C1)",
+            "value": res["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) activations and cotangent, random-init params)",
+            "config": {"workload": "C1 GDN layer backward B=4 T=4096 Hk=16 Hv=32 d=128"},
+            "kernel_ms": res["kernel_ms"],
+        }
+        print(json.dumps(line), flush=True)
         return 0
     if args.workload == "bwd":
         B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads

@@ -80,33 +80,52 @@ __device__ __forceinline__ float silu_grad(float u) {
 
 // ---------------------------------------------------------------------------- forward pieces
 
-// one thread per (token, 8-channel group)
+// One thread per (16-token block, 8-channel group): the weights and the last three inputs
+// stay in registers while it streams down the block's tokens (every input read once plus a
+// 3-token halo).
+constexpr int kConvFwdTB = 16;
+
 __global__ __launch_bounds__(NT) void conv_silu_split_kernel(LayerBwdParams p) {
   const int G = p.conv_dim / 8;
+  const long long nblk = (p.tokens + kConvFwdTB - 1) / kConvFwdTB;
   const long long idx = (long long)blockIdx.x * NT + threadIdx.x;
-  if (idx >= p.tokens * G) return;
-  const long long t = idx / G;
+  if (idx >= nblk * G) return;
+  const long long tb = (idx / G) * kConvFwdTB;
+  const long long te = tb + kConvFwdTB < p.tokens ? tb + kConvFwdTB : p.tokens;
   const int c0 = 8 * (int)(idx % G);
-  long long s0, s1;
-  token_seq(p.cu_seqlens, p.N, p.T, t, s0, s1);
   float wt[8][4];
   conv_w8(p.conv_w, c0, wt);
-  float xs[4][8];  // inputs d tokens back
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    if (t - d >= s0) load8(p.x + (t - d) * p.conv_dim + c0, xs[d]);
-    else zero8(xs[d]);
-  }
-  float y[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e)
-    y[e] = round_bf(silu_fast(conv_u(wt[e], xs[0][e], xs[1][e], xs[2][e], xs[3][e])));
   const int kd = p.Hk * p.dk;
   bf16_t* dst;
-  if (c0 < kd) dst = p.q + t * kd + c0;
-  else if (c0 < 2 * kd) dst = p.k + t * kd + (c0 - kd);
-  else dst = p.v + t * (long long)(p.Hv * p.dv) + (c0 - 2 * kd);
-  *(u32x4*)dst = pack8(y);
+  long long ld;
+  if (c0 < kd) { dst = p.q + c0; ld = kd; }
+  else if (c0 < 2 * kd) { dst = p.k + (c0 - kd); ld = kd; }
+  else { dst = p.v + (c0 - 2 * kd); ld = (long long)p.Hv * p.dv; }
+  long long s0, s1;
+  token_seq(p.cu_seqlens, p.N, p.T, tb, s0, s1);
+  float xs[4][8];  // inputs d tokens back
+#pragma unroll
+  for (int d = 1; d < 4; ++d) {
+    if (tb - d >= s0) load8(p.x + (tb - d) * p.conv_dim + c0, xs[d]);
+    else zero8(xs[d]);
+  }
+  for (long long t = tb; t < te; ++t) {
+    if (t >= s1) {  // a new sequence starts at t: no history
+      token_seq(p.cu_seqlens, p.N, p.T, t, s0, s1);
+#pragma unroll
+      for (int d = 1; d < 4; ++d) zero8(xs[d]);
+    }
+    load8(p.x + t * p.conv_dim + c0, xs[0]);
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      y[e] = round_bf(silu_fast(conv_u(wt[e], xs[0][e], xs[1][e], xs[2][e], xs[3][e])));
+    *(u32x4*)(dst + t * ld) = pack8(y);
+#pragma unroll
+    for (int d = 3; d > 0; --d)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xs[d][e] = xs[d - 1][e];
+  }
 }
 
 // one thread per (token, value head): g and beta as the forward's prep forms them
@@ -264,15 +283,26 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
   for (int d = 1; d < 4; ++d)
     if (tb - d >= cs0) load8(p.x + (tb - d) * p.conv_dim + c0, xs[d]);
   const long long tend = te + 3 < p.tokens ? te + 3 : p.tokens;
+  // the next token's x and dy rows are loaded one iteration ahead
+  u32x4 nx = {0u, 0u, 0u, 0u}, ndy = {0u, 0u, 0u, 0u};
+  if (tb < tend) {
+    nx = *(const u32x4*)(p.x + tb * p.conv_dim + c0);
+    ndy = *(const u32x4*)(dys + tb * dy_ld + dy_c);
+  }
   for (long long t = tb; t < tend; ++t) {
+    const u32x4 cx = nx, cdy = ndy;
+    if (t + 1 < tend) {
+      nx = *(const u32x4*)(p.x + (t + 1) * p.conv_dim + c0);
+      ndy = *(const u32x4*)(dys + (t + 1) * dy_ld + dy_c);
+    }
     if (t >= cs1) {  // a new sequence starts at t: no history
       token_seq(p.cu_seqlens, p.N, p.T, t, cs0, cs1);
 #pragma unroll
       for (int d = 1; d < 4; ++d) zero8(xs[d]);
     }
-    load8(p.x + t * p.conv_dim + c0, xs[0]);
+    unpack8<false>(&cx, xs[0]);
     float dy[8];
-    load8(dys + t * dy_ld + dy_c, dy);
+    unpack8<false>(&cdy, dy);
     float du[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
@@ -345,19 +375,49 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
     *(float4*)(part + 4 * e) = float4{dwt[e][3], dwt[e][2], dwt[e][1], dwt[e][0]};
 }
 
-// out[c] = sum over rows r (in order) of part[r * stride + off + c], c < ncols
+// out[c] = sum over rows r of part[r * stride + off + c], c < ncols: COLS columns per
+// workgroup and NT / COLS row groups (rows r = rg mod NT/COLS), each summing its rows into
+// four accumulators; the partial sums are combined in a fixed order, so the result does not
+// depend on timing.
+template <int COLS>
 __global__ __launch_bounds__(NT) void col_reduce_kernel(const float* part, long long nrows,
                                                         int stride, int off, int ncols, float* out) {
-  const int c = blockIdx.x * NT + threadIdx.x;
-  if (c >= ncols) return;
-  float s = 0.f;
-  for (long long r = 0; r < nrows; ++r) s += part[r * stride + off + c];
-  out[c] = s;
+  constexpr int RG = NT / COLS;
+  __shared__ float s_part[RG][COLS];
+  const int cl = threadIdx.x % COLS, rg = threadIdx.x / COLS;
+  const int c = blockIdx.x * COLS + cl;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  if (c < ncols) {
+    long long r = rg;
+    for (; r + 3 * RG < nrows; r += 4 * RG) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += part[(r + u * RG) * stride + off + c];
+    }
+    for (; r < nrows; r += RG) acc[0] += part[r * stride + off + c];
+  }
+  s_part[rg][cl] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (rg == 0 && c < ncols) {
+    float t = 0.f;
+    for (int g = 0; g < RG; ++g) t += s_part[g][cl];
+    out[c] = t;
+  }
+}
+
+// narrow column groups (more row groups) for the few-column reductions
+void launch_col_reduce(const float* part, long long nrows, int stride, int off, int ncols,
+                       float* out, hipStream_t stream) {
+  if (ncols <= 2048)
+    hipLaunchKernelGGL((col_reduce_kernel<8>), dim3((ncols + 7) / 8), dim3(NT), 0, stream, part,
+                       nrows, stride, off, ncols, out);
+  else
+    hipLaunchKernelGGL((col_reduce_kernel<32>), dim3((ncols + 31) / 32), dim3(NT), 0, stream, part,
+                       nrows, stride, off, ncols, out);
 }
 
 }  // namespace
 
-int layer_bwd_norm_blocks() { return 1024; }
+int layer_bwd_norm_blocks() { return 4096; }
 
 long long layer_bwd_conv_blocks(long long tokens) { return (tokens + kConvTB - 1) / kConvTB; }
 
@@ -367,7 +427,7 @@ int layer_bwd_gate_blocks(long long tokens) {
 }
 
 hipError_t launch_layer_fwd_pieces(const LayerBwdParams& p, hipStream_t stream) {
-  const long long n1 = p.tokens * (p.conv_dim / 8);
+  const long long n1 = (p.tokens + kConvFwdTB - 1) / kConvFwdTB * (p.conv_dim / 8);
   if (n1 > 0) {
     hipLaunchKernelGGL(conv_silu_split_kernel, dim3((unsigned)((n1 + NT - 1) / NT)), dim3(NT), 0,
                        stream, p);
@@ -379,9 +439,7 @@ hipError_t launch_layer_fwd_pieces(const LayerBwdParams& p, hipStream_t stream) 
 
 hipError_t launch_layer_norm_bwd(const LayerBwdParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(norm_bwd_kernel, dim3(layer_bwd_norm_blocks()), dim3(NT), 0, stream, p);
-  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.dv + NT - 1) / NT), dim3(NT), 0, stream,
-                     (const float*)p.part_norm, (long long)layer_bwd_norm_blocks(), p.dv, 0, p.dv,
-                     p.d_norm_w);
+  launch_col_reduce(p.part_norm, layer_bwd_norm_blocks(), p.dv, 0, p.dv, p.d_norm_w, stream);
   return hipGetLastError();
 }
 
@@ -389,16 +447,13 @@ hipError_t launch_layer_tail_bwd(const LayerBwdParams& p, hipStream_t stream) {
   const int gb = layer_bwd_gate_blocks(p.tokens);
   const long long per = (p.tokens + gb - 1) / gb;
   hipLaunchKernelGGL(gates_bwd_kernel, dim3(gb), dim3(NT), 0, stream, p, per);
-  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.Hv + NT - 1) / NT), dim3(NT), 0, stream,
-                     (const float*)p.part_gates, (long long)gb, 2 * p.Hv, 0, p.Hv, p.dA_log);
-  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.Hv + NT - 1) / NT), dim3(NT), 0, stream,
-                     (const float*)p.part_gates, (long long)gb, 2 * p.Hv, p.Hv, p.Hv, p.d_dt_bias);
+  launch_col_reduce(p.part_gates, gb, 2 * p.Hv, 0, p.Hv, p.dA_log, stream);
+  launch_col_reduce(p.part_gates, gb, 2 * p.Hv, p.Hv, p.Hv, p.d_dt_bias, stream);
   const long long nblk = layer_bwd_conv_blocks(p.tokens);
   const long long n = nblk * (p.conv_dim / 8);
   if (n > 0)
     hipLaunchKernelGGL(conv_bwd_kernel, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, stream, p);
-  hipLaunchKernelGGL(col_reduce_kernel, dim3((p.conv_dim * 4 + NT - 1) / NT), dim3(NT), 0, stream,
-                     (const float*)p.part_conv, nblk, p.conv_dim * 4, 0, p.conv_dim * 4, p.d_conv_w);
+  launch_col_reduce(p.part_conv, nblk, p.conv_dim * 4, 0, p.conv_dim * 4, p.d_conv_w, stream);
   return hipGetLastError();
 }
 
