@@ -17,7 +17,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
 rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
 shapes: the chunk-parallel preparation kernel and the state scan), and carries the
-decode step's HBM roofline as "decode" and the backward pass (VJP) at C1 as "backward".  Only one GPU is
+decode step's HBM roofline as "decode", the rule's backward pass (VJP) at C1 as
+"backward" and the layer's backward as "layer_backward".  Only one GPU is
 used: --gpus above 1 exits with a message.
 
 Kernel durations come from HIP events recorded on the stream the kernels run on
@@ -397,6 +398,7 @@ def main():
     pre = bench_prefill(args.steps, args.warmup, cpu)
     dec = bench_decode(args.decode_batch, max(args.steps, 20), args.warmup, False)
     bwd = bench_bwd(4, 4096, 16, 32, 128, max(args.steps // 2, 5), args.warmup)
+    lbwd = bench_layer_bwd(max(args.steps // 2, 5), args.warmup)
     line = {
         "metric": "GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
         "value": pre["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -412,6 +414,8 @@ def main():
         "prefill_detail": {k_: pre[k_] for k_ in ("step_event_ms", "core_kernel_ms")},
         "backward": {"config": "chunk_gated_delta_rule_bwd at C1 (B=4 T=4096 Hk=16 Hv=32 d=128)",
                      "kernel_ms": bwd["kernel_ms"], "roofline": bwd["roofline"]},
+        "layer_backward": {"config": "gdn_prefill_bwd at C1", "kernel_ms": lbwd["kernel_ms"],
+                           "tokens_per_s": lbwd["tokens_per_s"]},
     }
     if cpu:
         line["cpu_baseline"] = pre["cpu_baseline"]

@@ -116,3 +116,63 @@ def test_layer_autograd_routes_through_the_bwd_entry_point():
     ref = run_gpu(d, dims)
     for g_, r_ in zip(grads, ref):
         assert np.array_equal(np_(g_).reshape(r_.shape), r_)
+
+
+def test_layer_module_trains_end_to_end():
+    """Gradients of every parameter and of the input through the layer module's forward
+    (projections -> gdn_prefill -> out_proj, deltanet.py:226-306) under torch.autograd,
+    against the chain rule around the fp64 layer VJP oracle."""
+    say("layer module training step")
+    from omegalax_amd import GDNConfig, GDNParams, gated_deltanet_forward
+    Hk, dk, Hv, dv, D, B, T = 2, 128, 4, 128, 64, 1, 100
+    cfg = GDNConfig(hidden_size=D, num_k_heads=Hk, head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv)
+    rng = np.random.default_rng(21)
+    Cd = 2 * Hk * dk + Hv * dv
+    w = {
+        "in_proj_qkv": O.round_bf16(0.1 * rng.standard_normal((Cd, D))),
+        "in_proj_z": O.round_bf16(0.1 * rng.standard_normal((Hv * dv, D))),
+        "in_proj_b": O.round_bf16(0.1 * rng.standard_normal((Hv, D))),
+        "in_proj_a": O.round_bf16(0.1 * rng.standard_normal((Hv, D))),
+        "conv_w": (0.1 * rng.standard_normal((Cd, 4))).astype(np.float32),
+        "dt_bias": rng.uniform(-2, 0, Hv).astype(np.float32),
+        "A_log": rng.uniform(0, np.log(16), Hv).astype(np.float32),
+        "norm_w": rng.uniform(0.5, 1.5, dv).astype(np.float32),
+        "out_proj": O.round_bf16(0.05 * rng.standard_normal((D, Hv * dv))),
+    }
+    h = O.round_bf16(rng.standard_normal((B, T, D)))
+    R = O.round_bf16(rng.standard_normal((B, T, D)))
+    bf = ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj")
+    tw = {n: torch.from_numpy(v).cuda().to(torch.bfloat16 if n in bf else torch.float32)
+          .requires_grad_() for n, v in w.items()}
+    th = torch.from_numpy(h).cuda().bfloat16().requires_grad_()
+    out = gated_deltanet_forward(GDNParams(**tw), cfg, th)
+    (out.float() * torch.from_numpy(R).cuda()).sum().backward()
+    # reference: forward with bf16-rounded projection outputs, then the chain rule
+    f64 = {n: np.asarray(v, np.float64) for n, v in w.items()}
+    mixed = O.round_bf16(h @ f64["in_proj_qkv"].T)
+    z = O.round_bf16(h @ f64["in_proj_z"].T).reshape(B, T, Hv, dv)
+    b = O.round_bf16(h @ f64["in_proj_b"].T)
+    a = O.round_bf16(h @ f64["in_proj_a"].T)
+    core, _, _ = O.gdn_prefill_layer(mixed, z, a, b, w["conv_w"], w["A_log"], w["dt_bias"],
+                                     w["norm_w"], Hk=Hk, dk=dk, Hv=Hv, dv=dv)
+    d_core = R @ f64["out_proj"]
+    dmix, dz, da, db, dconv, dA, ddt, dnw, _ = V.gdn_prefill_layer_bwd(
+        mixed, z, a, b, w["conv_w"], w["A_log"], w["dt_bias"], w["norm_w"], d_core, Hk=Hk,
+        dk=dk, Hv=Hv, dv=dv, act_round=O.round_bf16)
+    flat = lambda x: x.reshape(-1, x.shape[-1]) if x.ndim > 2 else x
+    hf = h.reshape(-1, D)
+    ref = {
+        "out_proj": flat(R).T @ core.reshape(-1, Hv * dv),
+        "in_proj_qkv": flat(dmix).T @ hf,
+        "in_proj_z": dz.reshape(-1, Hv * dv).T @ hf,
+        "in_proj_a": flat(da).T @ hf,
+        "in_proj_b": flat(db).T @ hf,
+        "conv_w": dconv, "A_log": dA, "dt_bias": ddt, "norm_w": dnw,
+    }
+    dh = (flat(dmix) @ f64["in_proj_qkv"] + dz.reshape(-1, Hv * dv) @ f64["in_proj_z"]
+          + flat(da) @ f64["in_proj_a"] + flat(db) @ f64["in_proj_b"])
+    errs = {n: rel(np_(tw[n].grad), r) for n, r in ref.items()}
+    errs["hidden"] = rel(np_(th.grad).reshape(-1, D), dh)
+    say("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    for n, e in errs.items():
+        assert e < BF16_TOL, (n, e)
