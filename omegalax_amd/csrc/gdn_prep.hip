@@ -263,13 +263,15 @@ template <int MODE>
 constexpr bool prep_persistent() { return MODE != MODE_LAYER; }
 
 // Per-thread register prefetch of one task's inputs: raw q/k rows (core modes)
-// and the gate inputs of the first kGatePf value heads (lane = token).
+// and the gate inputs of value head w of the task's first kGatePf (wavefront w,
+// lane = token).
 template <int DK, int MODE>
 struct PrepPf {
   static constexpr int NRAW = MODE == MODE_LAYER ? 1 : PrepCfg<DK, MODE>::NI_KQ * PrepCfg<DK, MODE>::RAWW;
   u32x4 raw[NRAW];
-  float ga[kGatePf], gb[kGatePf];
+  float ga, gb;
 };
+static_assert(kGatePf == NT / 64, "one prefetched value head per wavefront");
 
 template <int DK, int MODE>
 __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTask& t,
@@ -300,20 +302,18 @@ __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTa
     }
   }
   const int gqa = p.Hv / p.Hk;
+  const int gg = tid >> 6;  // this wavefront's value head within the key head
   const long long g0 = t.t0 * p.Hv + (long long)t.hk * gqa;  // token t0, first value head
-#pragma unroll
-  for (int gg = 0; gg < kGatePf; ++gg) {
-    pf.ga[gg] = 0.f;
-    pf.gb[gg] = 0.f;
-    if (gg < gqa && l < t.nvalid) {
-      const unsigned lo = (unsigned)l * (unsigned)p.Hv;  // lane = token
-      if constexpr (MODE == MODE_LAYER) {
-        pf.ga[gg] = bf2f(*at_bytes((const bf16_t*)p.a + g0 + gg, 2u * lo));
-        pf.gb[gg] = bf2f(*at_bytes((const bf16_t*)p.b + g0 + gg, 2u * lo));
-      } else {
-        pf.ga[gg] = *at_bytes(p.g + g0 + gg, 4u * lo);
-        pf.gb[gg] = *at_bytes(p.beta + g0 + gg, 4u * lo);
-      }
+  pf.ga = 0.f;
+  pf.gb = 0.f;
+  if (gg < gqa && l < t.nvalid) {
+    const unsigned lo = (unsigned)l * (unsigned)p.Hv;  // lane = token
+    if constexpr (MODE == MODE_LAYER) {
+      pf.ga = bf2f(*at_bytes((const bf16_t*)p.a + g0 + gg, 2u * lo));
+      pf.gb = bf2f(*at_bytes((const bf16_t*)p.b + g0 + gg, 2u * lo));
+    } else {
+      pf.ga = *at_bytes(p.g + g0 + gg, 4u * lo);
+      pf.gb = *at_bytes(p.beta + g0 + gg, 4u * lo);
     }
   }
 }
@@ -404,6 +404,12 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         }
       }
     } else {
+      // Every prefetched register is consumed before the task's first global store:
+      // the memory counter retires operations in issue order, so a register read after
+      // a store would also wait for that store to complete.
+      sGin[wave * 2 * C + l] = pf.ga;
+      sGin[wave * 2 * C + C + l] = pf.gb;
+      u32x4 hwk[Q_::NI_KQ];
 #pragma unroll
       for (int k = 0; k < Q_::NI_KQ; ++k) {
         constexpr int PER = C * SEGS;
@@ -423,28 +429,39 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         bf16_t* dst = (which == 0 ? sK : sQ) + r * LDK + seg * 8;
         const u32x4 hw = pack8(x);
         *(u32x4*)dst = hw;
+        hwk[k] = hw;
         if constexpr (IS) *(u32x4*)(dst + K_LO) = pack8_lo(x);
-        void* out = which == 0 ? p.kn : p.qn;
-        if (out && (nvalid == C || r < nvalid)) {
-          // row t0 of this key head (uniform) plus the lane's byte offset
-          const long long o0 = t0 * (long long)p.Hk * DK + (long long)hk * DK;
-          const unsigned lo = (unsigned)r * (unsigned)(p.Hk * DK) + 8u * seg;
-          if constexpr (F32) {
+        if constexpr (F32) {  // fp32 rows are stored as they form (no register copy)
+          void* out = which == 0 ? p.kn : p.qn;
+          if (out && (nvalid == C || r < nvalid)) {
+            const long long o0 = t0 * (long long)p.Hk * DK + (long long)hk * DK;
+            const unsigned lo = (unsigned)r * (unsigned)(p.Hk * DK) + 8u * seg;
             float4* d4 = (float4*)at_bytes((float*)out + o0, 4u * lo);
             d4[0] = float4{x[0], x[1], x[2], x[3]};
             d4[1] = float4{x[4], x[5], x[6], x[7]};
-          } else {
-            *(u32x4*)at_bytes((bf16_t*)out + o0, 2u * lo) = hw;
+          }
+        }
+      }
+      if constexpr (!F32) {
+#pragma unroll
+        for (int k = 0; k < Q_::NI_KQ; ++k) {
+          constexpr int PER = C * SEGS;
+          const int which = (k * NT) / PER;
+          const int rem = (k * NT) % PER + tid;
+          const int r = rem / SEGS, seg = rem % SEGS;
+          void* out = which == 0 ? p.kn : p.qn;
+          if (out && (nvalid == C || r < nvalid)) {
+            // row t0 of this key head (uniform) plus the lane's byte offset
+            const long long o0 = t0 * (long long)p.Hk * DK + (long long)hk * DK;
+            const unsigned lo = (unsigned)r * (unsigned)(p.Hk * DK) + 8u * seg;
+            *(u32x4*)at_bytes((bf16_t*)out + o0, 2u * lo) = hwk[k];
           }
         }
       }
     }
-    if (wave == 0) {
-#pragma unroll
-      for (int gg = 0; gg < kGatePf; ++gg) {
-        sGin[gg * 2 * C + l] = pf.ga[gg];
-        sGin[gg * 2 * C + C + l] = pf.gb[gg];
-      }
+    if constexpr (MODE == MODE_LAYER) {
+      sGin[wave * 2 * C + l] = pf.ga;
+      sGin[wave * 2 * C + C + l] = pf.gb;
     }
     // the next task's loads land while this one computes (the barrier below does not
     // wait for them, nor for the normalised rows' stores)
@@ -489,23 +506,35 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         }
       }
 
-      // gates of value head h, one token per lane; every wave scans its own copy
-      {
-        float g = 0.f, bt = 0.f;
-        if (gg < kGatePf) {
-          g = sGin[gg * 2 * C + l];
-          bt = sGin[gg * 2 * C + C + l];
-        } else if (l < nvalid) {
-          const long long i0 = t0 * p.Hv + h;
-          const unsigned lo = (unsigned)l * (unsigned)p.Hv;
-          if constexpr (MODE == MODE_LAYER) {
-            g = bf2f(*at_bytes((const bf16_t*)p.a + i0, 2u * lo));
-            bt = bf2f(*at_bytes((const bf16_t*)p.b + i0, 2u * lo));
-          } else {
-            g = *at_bytes(p.g + i0, 4u * lo);
-            bt = *at_bytes(p.beta + i0, 4u * lo);
+      // gates of value head h, one token per lane; every wave scans its own copy.  The
+      // inputs come from LDS only: a global load here, whose register the loop reuses,
+      // would make every value head wait for all of the wavefront's outstanding memory
+      // operations (the next task's prefetch and this task's record stores).
+      if (gg >= kGatePf && gg % kGatePf == 0) {  // uniform; only when gqa > kGatePf
+        // the next kGatePf heads' gate inputs replace the prefetched ones (every wave has
+        // passed the previous head's last barrier, so sGin is free)
+        if (wave < kGatePf) {
+          float ga = 0.f, gb = 0.f;
+          if (gg + wave < gqa && l < nvalid) {
+            const long long i0 = t0 * p.Hv + h + wave;
+            const unsigned lo = (unsigned)l * (unsigned)p.Hv;
+            if constexpr (MODE == MODE_LAYER) {
+              ga = bf2f(*at_bytes((const bf16_t*)p.a + i0, 2u * lo));
+              gb = bf2f(*at_bytes((const bf16_t*)p.b + i0, 2u * lo));
+            } else {
+              ga = *at_bytes(p.g + i0, 4u * lo);
+              gb = *at_bytes(p.beta + i0, 4u * lo);
+            }
           }
+          sGin[wave * 2 * C + l] = ga;
+          sGin[wave * 2 * C + C + l] = gb;
         }
+        lds_barrier();
+      }
+      {
+        const int slot = gg % kGatePf;
+        float g = sGin[slot * 2 * C + l];
+        float bt = sGin[slot * 2 * C + C + l];
         if constexpr (MODE == MODE_LAYER) {
           // deltanet.py:248-250: beta in bf16, g in fp32 (padded tokens: both 0)
           const float keep = (float)(l < nvalid);

@@ -102,6 +102,7 @@ CASES = [
     (1, 200, 1, 1, 128, 64, "bf16"),
     (2, 150, 1, 2, 64, 64, "f32"),
     (1, 70, 2, 2, 32, 128, "f32"),
+    (1, 120, 1, 6, 128, 64, "bf16"),  # gqa 6
 ]
 
 

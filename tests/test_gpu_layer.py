@@ -60,6 +60,7 @@ def ref_prefill(d, dims, cu=None, S0=None, conv0=None):
     (2, 3, 1, 2, 64, 64),       # shorter than the conv window
     (1, 200, 2, 2, 64, 128),
     (1, 130, 1, 2, 128, 64),
+    (1, 100, 1, 6, 128, 64),    # gqa 6: gate inputs restaged past the prefetched four
 ])
 def test_layer_prefill_matches_oracle(B, T, Hk, Hv, dk, dv):
     say(f"layer B={B} T={T} Hk={Hk} Hv={Hv} dk={dk} dv={dv}")

@@ -81,6 +81,7 @@ def check(got, ref):
     (1, 200, 1, 2, 64, 64),
     (1, 130, 2, 2, 64, 128),
     (2, 3, 1, 2, 128, 64),
+    (1, 100, 1, 6, 128, 64),
 ])
 def test_layer_bwd_matches_oracle(B, T, Hk, Hv, dk, dv):
     say(f"layer bwd B={B} T={T} Hk={Hk} Hv={Hv} dk={dk} dv={dv}")

@@ -86,6 +86,8 @@ CASES = [
     (1, 200, 1, 1, 128, 64, "bf16"),
     (2, 150, 1, 2, 64, 64, "f32"),
     (1, 70, 2, 2, 32, 128, "f32"),
+    (1, 150, 1, 6, 128, 64, "bf16"),  # more value heads per key head than the prep prefetches
+    (1, 90, 1, 8, 64, 64, "f32"),
 ]
 
 
