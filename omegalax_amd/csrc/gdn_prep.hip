@@ -216,8 +216,16 @@ struct PrepTask {
   long long s0, t0;
 };
 
+// Entry i of a small read-only table (chunk offsets, sequence bounds) at a uniform
+// index, read through the scalar unit: a constant-address-space load is a scalar load,
+// which neither adds to nor waits on the vector memory counter (the table was written
+// before this kernel started).
+__device__ __forceinline__ int uniform_ld(const int32_t* a, int i) {
+  return ((const __attribute__((address_space(4))) int32_t*)a)[i];
+}
+
 // Task index -> task.  Tasks are key-head major (task = hk * n_ci + ci), so the
-// consecutive tasks a workgroup walks share the key head and its conv weights.
+// consecutive workgroups share the key head and its conv weights.
 __device__ __forceinline__ PrepTask prep_task(const ChunkParams& p, int task, int n_ci) {
   PrepTask t;
   t.hk = task / n_ci;
@@ -227,17 +235,23 @@ __device__ __forceinline__ PrepTask prep_task(const ChunkParams& p, int task, in
     int lo = 0, hi = p.N;  // chunk_off[lo] <= ci < chunk_off[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (p.chunk_off[mid] <= t.ci) lo = mid;
+      if (uniform_ld(p.chunk_off, mid) <= t.ci) lo = mid;
       else hi = mid;
     }
     t.n = lo;
-    c = t.ci - p.chunk_off[lo];
+    c = t.ci - uniform_ld(p.chunk_off, lo);
   } else {
     t.n = t.ci / p.nch;
     c = t.ci % p.nch;
   }
   long long s1;
-  seq_range(p.cu_seqlens, t.n, p.T, t.s0, s1);
+  if (p.cu_seqlens) {  // as seq_range, from scalar loads
+    const long long lo = uniform_ld(p.cu_seqlens, t.n), hi = uniform_ld(p.cu_seqlens, t.n + 1);
+    t.s0 = lo < 0 ? 0 : (lo > p.T ? p.T : lo);
+    s1 = hi < t.s0 ? t.s0 : (hi > p.T ? p.T : hi);
+  } else {
+    seq_range(nullptr, t.n, p.T, t.s0, s1);
+  }
   t.t0 = t.s0 + (long long)c * C;
   t.nvalid = (int)((s1 - t.t0) < C ? (s1 - t.t0) : C);
   // the task is uniform over the workgroup: keep it in scalar registers (values read
@@ -253,29 +267,22 @@ __device__ __forceinline__ PrepTask prep_task(const ChunkParams& p, int task, in
   return t;
 }
 
-constexpr int kGatePf = 4;  // value heads per key head whose gate inputs are prefetched
+constexpr int kGatePf = 4;  // value heads per key head whose gate inputs load with the rows
 
-// Core modes run persistent workgroups that prefetch their next task while
-// computing the current one.  The layer mode's conv window would need about 110
-// more registers across the compute phase, halving occupancy, so there each
-// workgroup runs a single task (the grid covers all tasks).
-template <int MODE>
-constexpr bool prep_persistent() { return MODE != MODE_LAYER; }
-
-// Per-thread register prefetch of one task's inputs: raw q/k rows (core modes)
+// Per-thread register load of the task's inputs: raw q/k rows (core modes)
 // and the gate inputs of value head w of the task's first kGatePf (wavefront w,
 // lane = token).
 template <int DK, int MODE>
-struct PrepPf {
+struct PrepIn {
   static constexpr int NRAW = MODE == MODE_LAYER ? 1 : PrepCfg<DK, MODE>::NI_KQ * PrepCfg<DK, MODE>::RAWW;
   u32x4 raw[NRAW];
   float ga, gb;
 };
-static_assert(kGatePf == NT / 64, "one prefetched value head per wavefront");
+static_assert(kGatePf == NT / 64, "one value head's gate inputs per wavefront");
 
 template <int DK, int MODE>
-__device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTask& t,
-                                              PrepPf<DK, MODE>& pf) {
+__device__ __forceinline__ void load_task_inputs(const ChunkParams& p, const PrepTask& t,
+                                                 PrepIn<DK, MODE>& pf) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int SEGS = Q_::SEGS;
   constexpr bool F32 = MODE == MODE_F32;
@@ -318,10 +325,11 @@ __device__ __forceinline__ void prep_prefetch(const ChunkParams& p, const PrepTa
   }
 }
 
-// Workgroups per CU the register budget is set for: the layer mode's single task per
-// workgroup waits on its conv inputs, so more resident workgroups hide that latency.
-template <int MODE>
-constexpr int prep_min_blocks() { return MODE == MODE_LAYER ? 3 : 2; }
+// Each workgroup runs one task, whose first phase waits on its global loads; three
+// resident workgroups per CU (the LDS limit) hide that latency.  A persistent variant
+// that prefetched the next task into registers needed about 80 more registers, so
+// only two fitted, and was slower.
+constexpr int kPrepBlocksPerCU = 3;
 
 // A-layout 16x16 fp32 tile (lane (q, r) holds M[16 bi + r][16 bj + 4q .. +3]) into a
 // row-major 64x64 matrix
@@ -334,7 +342,7 @@ __device__ __forceinline__ void put_f32_tile(float* m, int bi, int bj, f32x4 a) 
 // (X^T with X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in
 // gdn_chunk.h).
 template <int DK, int MODE, bool BWD = false>
-__global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(ChunkParams p) {
+__global__ __launch_bounds__(NT, kPrepBlocksPerCU) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, F32 = MODE == MODE_F32;
@@ -343,27 +351,22 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
   __shared__ __align__(16) u32x2 sLf[10 * 2 * 64];        // L blocks as A fragments (hi, lo)
   __shared__ __align__(16) u32x2 sTd[4 * 2 * 64];         // diagonal inverses as A fragments (hi, lo)
   __shared__ __align__(16) float sGw[4 * 2 * C];          // per wave: G log2(e), beta
-  __shared__ __align__(16) float sGin[kGatePf * 2 * C];   // the task's prefetched gate inputs
+  __shared__ __align__(16) float sGin[kGatePf * 2 * C];   // gate inputs of kGatePf value heads
   constexpr int K_LO = C * LDK;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gqa = p.Hv / p.Hk;
-  // tasks: (chunk, key head) pairs; workgroup b takes a contiguous block of them
-  const int n_ci = p.chunk_off ? p.chunk_off[p.N] : p.n_rec;
+  // tasks: (chunk, key head) pairs, one per workgroup (the grid may hold spare ones)
+  const int n_ci = p.chunk_off ? uniform_ld(p.chunk_off, p.N) : p.n_rec;
   const int total = n_ci * p.Hk;
-  const int per = (total + (int)gridDim.x - 1) / (int)gridDim.x;
-  const int first = (int)blockIdx.x * per;
-  const int last = first + per < total ? first + per : total;
+  const int task = (int)blockIdx.x;
+  if (task >= total) return;  // uniform
 
-  PrepPf<DK, MODE> pf;
-  if constexpr (prep_persistent<MODE>())
-    if (first < last) prep_prefetch<DK, MODE>(p, prep_task(p, first, n_ci), pf);
-
-  for (int task = first; task < (prep_persistent<MODE>() ? last : first + 1); ++task) {
-    if (!prep_persistent<MODE>() && task >= last) break;
+  PrepIn<DK, MODE> pf;
+  {
     const PrepTask tk = prep_task(p, task, n_ci);
-    if constexpr (!prep_persistent<MODE>()) prep_prefetch<DK, MODE>(p, tk, pf);
+    load_task_inputs<DK, MODE>(p, tk, pf);
     const int hk = tk.hk, ci = tk.ci, n = tk.n, nvalid = tk.nvalid;
     const long long s0 = tk.s0, t0 = tk.t0;
 
@@ -404,7 +407,7 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
         }
       }
     } else {
-      // Every prefetched register is consumed before the task's first global store:
+      // Every loaded register is consumed before the task's first global store:
       // the memory counter retires operations in issue order, so a register read after
       // a store would also wait for that store to complete.
       sGin[wave * 2 * C + l] = pf.ga;
@@ -463,10 +466,6 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
       sGin[wave * 2 * C + l] = pf.ga;
       sGin[wave * 2 * C + C + l] = pf.gb;
     }
-    // the next task's loads land while this one computes (the barrier below does not
-    // wait for them, nor for the normalised rows' stores)
-    if constexpr (prep_persistent<MODE>())
-      if (task + 1 < last) prep_prefetch<DK, MODE>(p, prep_task(p, task + 1, n_ci), pf);
     lds_barrier();
 
     // -------------------------------------------------------------- Gram tiles
@@ -509,9 +508,9 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
       // gates of value head h, one token per lane; every wave scans its own copy.  The
       // inputs come from LDS only: a global load here, whose register the loop reuses,
       // would make every value head wait for all of the wavefront's outstanding memory
-      // operations (the next task's prefetch and this task's record stores).
+      // operations (this task's row and record stores).
       if (gg >= kGatePf && gg % kGatePf == 0) {  // uniform; only when gqa > kGatePf
-        // the next kGatePf heads' gate inputs replace the prefetched ones (every wave has
+        // the next kGatePf heads' gate inputs replace the staged ones (every wave has
         // passed the previous head's last barrier, so sGin is free)
         if (wave < kGatePf) {
           float ga = 0.f, gb = 0.f;
@@ -711,28 +710,12 @@ __global__ __launch_bounds__(NT, prep_min_blocks<MODE>()) void prep_kernel(Chunk
   }
 }
 
-// Compute units of the current device (queried once per device).
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
-      v = 256;
-    cus[dev] = v;
-  }
-  return cus[dev];
-}
-
 template <int DK, int MODE, bool BWD = false>
 hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
-  // persistent (core modes): two workgroups per compute unit walk the tasks, each
-  // prefetching its next task while it computes the current one
+  // one workgroup per (chunk slot, key head)
   const long long tasks = (long long)p.n_rec * p.Hk;
   if (tasks == 0) return hipSuccess;
-  const long long cap = prep_persistent<MODE>() ? (long long)prep_min_blocks<MODE>() * device_cus() : tasks;
-  const unsigned grid = (unsigned)(tasks < cap ? tasks : cap);
+  const unsigned grid = (unsigned)tasks;
   hipLaunchKernelGGL((prep_kernel<DK, MODE, BWD>), dim3(grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
 }
