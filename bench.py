@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the MI355X GatedDeltaNet path on one GPU; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload prefill|decode|core]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   prefill  config C1: GDN layer prefill from projection outputs (mixed_qkv, z, a, b)
@@ -13,12 +13,16 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   bwd      one chunk_gated_delta_rule_bwd call (the VJP: forward recompute, reverse state-
            gradient scan, chunk-parallel gradients) at the core workload's shape.
   layer_bwd one gdn_prefill_bwd call at C1 (the layer's VJP: conv, gates, rule, gated norm).
+  layer_module the whole GatedDeltaNet layer at C1 with D=2048 (projection GEMMs included):
+           a forward, and a training step (forward + gradients of every parameter and the
+           input); the line's value is the training step's tokens/s.
   copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
 The headline line reports prefill tokens/s with the MFMA roofline of the chunked
 rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
 shapes: the chunk-parallel preparation kernel and the state scan), and carries the
 decode step's HBM roofline as "decode", the rule's backward pass (VJP) at C1 as
-"backward" and the layer's backward as "layer_backward".  Only one GPU is
+"backward", the layer's backward as "layer_backward" and the whole layer with its
+projections (forward and training step) as "layer_module".  Only one GPU is
 used: --gpus above 1 exits with a message.
 
 Kernel durations come from HIP events recorded on the stream the kernels run on
@@ -250,6 +254,48 @@ def bench_layer_bwd(steps, warmup, B=4, T=4096):
             "tokens_per_s": B * T * steps / wall}
 
 
+# ----------------------------------------------------------------------------- layer module (C1)
+
+def bench_layer_module(steps, warmup, B=4, T=4096, D=2048):
+    """GatedDeltaNet.__call__ (deltanet.py:226-306) at C1 with its projections, which run as
+    hipBLASLt GEMMs through F.linear: the forward hidden -> out, and a training step (the
+    forward plus the gradients of every parameter and of the input for a fixed output
+    cotangent)."""
+    import torch
+    from omegalax_amd import GDNConfig, GDNParams, gated_deltanet_forward, workloads as W
+    Hk, Hv, d = 16, 32, 128
+    cfg = GDNConfig(hidden_size=D, num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+    _say(f"layer module: B={B} T={T} D={D} generating parameters and inputs")
+    arrs = W.module_params(D, Hk, Hv, d, d)
+    lin = {"in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a", "out_proj"}
+    params = GDNParams(**{k_: torch.from_numpy(v_).cuda().to(torch.bfloat16 if k_ in lin else torch.float32)
+                          for k_, v_ in arrs.items()})
+    gen = torch.Generator(device="cuda").manual_seed(1001)
+    h = torch.randn((B, T, D), generator=gen, device="cuda").bfloat16()
+    R = torch.randn((B, T, D), generator=gen, device="cuda").bfloat16()
+
+    def fwd():
+        with torch.no_grad():
+            gated_deltanet_forward(params, cfg, h)
+
+    leaves = [getattr(params, f).requires_grad_() for f in params.__dataclass_fields__]
+    hx = h.clone().requires_grad_()
+
+    def train():
+        out = gated_deltanet_forward(params, cfg, hx)
+        torch.autograd.grad(out, leaves + [hx], R)
+
+    _say(f"layer module: timing {steps} forwards and {max(steps // 2, 5)} training steps")
+    wall_f, ms_f = time_launches(fwd, steps, warmup)
+    n_t = max(steps // 2, 5)
+    wall_t, ms_t = time_launches(train, n_t, warmup)
+    for leaf in leaves:
+        leaf.requires_grad_(False)
+    return {"config": f"GatedDeltaNet forward / training step at C1 with projections (D={D})",
+            "forward_ms": ms_f, "forward_tokens_per_s": B * T * steps / wall_f,
+            "train_step_ms": ms_t, "train_tokens_per_s": B * T * n_t / wall_t}
+
+
 # ----------------------------------------------------------------------------- prefill (C1)
 
 def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
@@ -305,7 +351,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "layer_bwd", "copy"],
+    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "layer_bwd",
+                                           "layer_module", "copy"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -336,6 +383,19 @@ def main():
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                           "dtype": "f32", "data": "synthetic",
                           "config": {"workload": "256 MiB read + 256 MiB written"}}), flush=True)
+        return 0
+    if args.workload == "layer_module":
+        res = bench_layer_module(args.steps, args.warmup)
+        line = {
+            "metric": "GatedDeltaNet training-step tokens/s (projections included, config C1)",
+            "value": res["train_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+            "steps": max(args.steps // 2, 5), "warmup": args.warmup,
+            "ms_per_step": res["train_step_ms"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) hidden states and output cotangent, random-init params)",
+            "config": {"workload": res["config"]}, "layer_module": res,
+        }
+        print(json.dumps(line), flush=True)
         return 0
     if args.workload == "layer_bwd":
         res = bench_layer_bwd(args.steps, args.warmup)
@@ -399,6 +459,7 @@ def main():
     dec = bench_decode(args.decode_batch, max(args.steps, 20), args.warmup, False)
     bwd = bench_bwd(4, 4096, 16, 32, 128, max(args.steps // 2, 5), args.warmup)
     lbwd = bench_layer_bwd(max(args.steps // 2, 5), args.warmup)
+    mod = bench_layer_module(args.steps, args.warmup)
     line = {
         "metric": "GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
         "value": pre["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -416,6 +477,7 @@ def main():
                      "kernel_ms": bwd["kernel_ms"], "roofline": bwd["roofline"]},
         "layer_backward": {"config": "gdn_prefill_bwd at C1", "kernel_ms": lbwd["kernel_ms"],
                            "tokens_per_s": lbwd["tokens_per_s"]},
+        "layer_module": mod,
     }
     if cpu:
         line["cpu_baseline"] = pre["cpu_baseline"]

@@ -74,6 +74,19 @@ def layer_params(rng, Hk, Hv, dk, dv, K=CONV_K):
     return dict(conv_w=conv_w, A_log=A_log, dt_bias=dt_bias, norm_w=norm_w)
 
 
+def module_params(D, Hk=16, Hv=32, dk=128, dv=128, seed=1001, K=CONV_K):
+    """GatedDeltaNet parameters at hidden size D (config C1's draws): the projection
+    weights N(0, 0.02) rounded to bf16, the conv, gate and norm parameters as layer_params.
+    Returns numpy arrays keyed by the GDNParams field names."""
+    rng = np.random.default_rng(seed)
+    conv_dim = 2 * Hk * dk + Hv * dv
+    w = lambda n, m: round_bf16(0.02 * rng.standard_normal((n, m), dtype=np.float32))
+    p = dict(in_proj_qkv=w(conv_dim, D), in_proj_z=w(Hv * dv, D), in_proj_b=w(Hv, D),
+             in_proj_a=w(Hv, D), out_proj=w(D, Hv * dv))
+    p.update(layer_params(rng, Hk, Hv, dk, dv, K))
+    return p
+
+
 def layer_inputs(B, T, Hk=16, Hv=32, dk=128, dv=128, seed=1001, act_scale=1.0):
     """Projection outputs for the layer-level prefill (C1 layout by default).
 
