@@ -190,14 +190,6 @@ __device__ __forceinline__ float4 to_f4(u32x2 x) {
 }
 __device__ __forceinline__ void store4(bf16_t* dst, u32x2 x) { *(u32x2*)dst = x; }
 
-// 4 elements at src (zero when !valid) into LDS
-__device__ __forceinline__ void copy4(float* dst, const float* src, bool valid) {
-  *(float4*)dst = valid ? *(const float4*)src : float4{0.f, 0.f, 0.f, 0.f};
-}
-__device__ __forceinline__ void copy4(bf16_t* dst, const bf16_t* src, bool valid) {
-  *(u32x2*)dst = valid ? *(const u32x2*)src : u32x2{0u, 0u};
-}
-
 // Row sums of a C-layout tile (rows 16 bi + 4q + v, summed over its 16 columns) added
 // into arr[row] (lanes r == 0 write; one lane per row); column sums likewise.
 __device__ __forceinline__ void add_rows(float* arr, int bi, f32x4 x) {
@@ -445,6 +437,43 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 
 // ============================================================================ chunk-local gradients
 
+// Split-matrix operands.  A 64-row fp32 matrix the gradient kernel reads as MFMA operands
+// is kept in LDS as bf16 hi and lo planes (hi + lo is the value to ~2^-16 relative), split
+// once when it is written, so no fragment read converts.  op_vec: lane (q, r) gets entries
+// k0 + 8q .. +7 of storage row r0 + r (one 16-byte read per plane); op_tr: entries
+// k0 + 8q .. +7 down storage column c0 + r (two transposed 8-byte reads per plane).
+template <bool LO = true>
+__device__ __forceinline__ Op op_vec(const bf16_t* h, const bf16_t* lo, int ld, int r0, int k0) {
+  const int l = lane_id();
+  const int off = (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
+  Op o;
+  o.h = *(const u32x4*)(h + off);
+  if constexpr (LO) o.l = *(const u32x4*)(lo + off);
+  else o.l = o.h;
+  return o;
+}
+template <bool LO = true>
+__device__ __forceinline__ Op op_tr(const bf16_t* h, const bf16_t* lo, int ld, int c0, int k0) {
+  Op o;
+  o.h = frag_tr(h, ld, k0, c0);
+  if constexpr (LO) o.l = frag_tr(lo, ld, k0, c0);
+  else o.l = o.h;
+  return o;
+}
+// A C-layout tile (lane (q, r): rows row0 + 4q .. +3 of column col0 + r) into column-major
+// planes (storage [col][row]): one 8-byte write per plane.
+__device__ __forceinline__ void put_ct(bf16_t* h, bf16_t* lo, int ld, int row0, int col0, f32x4 c) {
+  const int l = lane_id();
+  const int off = (col0 + (l & 15)) * ld + row0 + 4 * (l >> 4);
+  *(u32x2*)(h + off) = pack_hi4(c);
+  *(u32x2*)(lo + off) = pack_lo4(c);
+}
+// Four consecutive entries (one row, 4 columns from col) into row-major planes.
+__device__ __forceinline__ void put_row4(bf16_t* h, bf16_t* lo, int off, f32x4 c) {
+  *(u32x2*)(h + off) = pack_hi4(c);
+  *(u32x2*)(lo + off) = pack_lo4(c);
+}
+
 // Eight wavefronts (two per SIMD: the LDS holds one workgroup per CU).  Wavefront w owns
 // dk column blocks w + 8m and dv column blocks w + 8m of the (chunk x head) gradients,
 // and of the 64x64 chunk matrices row block w % 4, column blocks 2 (w / 4) and
@@ -456,18 +485,27 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   using KT = typename std::conditional<F32, float, bf16_t>::type;
   using In = KT;  // v has the input precision too
   constexpr int LDK = DK + (F32 ? 4 : 8);
-  constexpr int LDW = DK + 4;
+  constexpr int LDB = C + 8;  // stride (bf16) of a split plane: 64 entries and a pad
   constexpr int NCB = DK / 16, NKB = (NCB + CW - 1) / CW;  // dk column blocks; per wavefront
   constexpr int NVB = DV / 16, NVW = (NVB + CW - 1) / CW;  // dv column blocks; per wavefront
   __shared__ __align__(16) KT sK[C * LDK];
   __shared__ __align__(16) KT sQ[C * LDK];
-  __shared__ __align__(16) float sDW[C * LDW];
-  __shared__ __align__(16) float sDP[C * LDF];
-  // X^T, dX and M1 / Qm; during the products over dv the region stages their operand rows
-  __shared__ __align__(16) float sR[3 * C * LDF];
-  float* const sX = sR;
-  float* const sDX = sR + C * LDF;
-  float* const sM = sR + 2 * C * LDF;
+  // split planes (hi, lo): dW column-major [dk][token], dPg column-major
+  __shared__ __align__(16) bf16_t sDW[2 * DK * LDB];
+  __shared__ __align__(16) bf16_t sDP[2 * C * LDB];
+  // X (row-major), dX and M1 / Qm (column-major), split; during the products over dv the
+  // region stages their operand rows
+  __shared__ __align__(16) bf16_t sR[3 * 2 * C * LDB];
+  bf16_t* const sXh = sR;
+  bf16_t* const sXl = sR + C * LDB;
+  bf16_t* const sDXh = sR + 2 * C * LDB;
+  bf16_t* const sDXl = sR + 3 * C * LDB;
+  bf16_t* const sMh = sR + 4 * C * LDB;
+  bf16_t* const sMl = sR + 5 * C * LDB;
+  bf16_t* const sDWh = sDW;
+  bf16_t* const sDWl = sDW + DK * LDB;
+  bf16_t* const sDPh = sDP;
+  bf16_t* const sDPl = sDP + C * LDB;
   __shared__ float sG[C], sBt[C];
   // per-wavefront partial row / column sums (deterministic: one writer per entry at a time)
   __shared__ float sRowG[CW][C], sColG[CW][C], sRowB[CW][C], sRowT[CW][C], sRP[CW][C];
@@ -508,31 +546,10 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   const In* vb = (const In*)p.v + t0 * rs + (long long)h * DV;
   const float scale = p.scale;
 
-  // ---------------------------------------------------------------- stage
-  for (int it = tid; it < 2 * C * (DK / 4); it += CNT) {
-    const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
-    const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
-    const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
-                    (long long)hk * DK + c4;
-    copy4((which ? sQ : sK) + row * LDK + c4, src, row < nvalid);
-  }
-  if (tid < C) {
-    sG[tid] = xb[kXlpgG + tid];
-    sBt[tid] = ((const float*)(p.rec + ((size_t)ci * Hv + h) * rec_stride + kRecG))[kGateBeta * C + tid];
-  }
-  {
-    const int w = tid >> 6;
-    sRowG[w][l] = 0.f;
-    sColG[w][l] = 0.f;
-    sRowB[w][l] = 0.f;
-    sRowT[w][l] = 0.f;
-    sRP[w][l] = 0.f;
-  }
-  __syncthreads();
-
-  const float Gl = sG[C - 1];
+  // (the gates and the K, Q rows are staged just before the products over dv, together
+  // with the first step's loads)
   auto eg = [&](int row) { return __expf(sG[row]); };
-  auto el = [&](int row) { return row == C - 1 ? 1.f : __expf(Gl - sG[row]); };
+  auto el = [&](int row) { return row == C - 1 ? 1.f : __expf(sG[C - 1] - sG[row]); };
   auto gam = [&](int row, int col) {
     return row >= col ? __expf(fminf(sG[row] - sG[col], 0.f)) : 0.f;
   };
@@ -550,15 +567,19 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   //   X1 = diag(e^G) dO S^T, dW = -dV_new S^T, dkdec = V_new dS^T (the wavefront's dk
   //   column blocks), dP = (dO V_new^T) * tril and dXa = dV_new v^T (its row block bi,
   //   column blocks 2 half, 2 half + 1).
-  // The step's dO, dV_new, V_new and v rows are staged in LDS (one coalesced float4 per
-  // thread each) and the state fragments come straight from global memory; both are
-  // loaded into registers one step ahead.
-  constexpr int LDR = 36;  // row stride of a staged 32-column slice
-  static_assert(4 * C * LDR <= 3 * C * LDF, "the staged slices fit the X / dX / M1 region");
-  float* const sDOs = sR;
-  float* const sDVs = sR + C * LDR;
-  float* const sVNs = sR + 2 * C * LDR;
-  float* const sVs = sR + 3 * C * LDR;
+  // The step's dO, dV_new, V_new and v rows are staged in LDS as split planes (one
+  // coalesced float4 per thread each, split once) and the state fragments come straight
+  // from global memory; both are loaded into registers one step ahead.
+  constexpr int LDR = 40;  // stride (bf16) of a staged 32-column slice plane
+  static_assert(8 * C * LDR <= 6 * C * LDB, "the staged slices fit the X / dX / M1 region");
+  bf16_t* const sDOh = sR;
+  bf16_t* const sDOl = sR + C * LDR;
+  bf16_t* const sDVh = sR + 2 * C * LDR;
+  bf16_t* const sDVl = sR + 3 * C * LDR;
+  bf16_t* const sVNh = sR + 4 * C * LDR;
+  bf16_t* const sVNl = sR + 5 * C * LDR;
+  bf16_t* const sVh = sR + 6 * C * LDR;  // v: exact in bf16 unless the inputs are fp32
+  bf16_t* const sVl = sR + 7 * C * LDR;
   const int srow = tid >> 3, sc4 = 4 * (tid & 7);  // this thread's staged item
   const bool srv = srow < nvalid;
   float4 pf_do, pf_dv, pf_vn;
@@ -570,12 +591,14 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     pf_vn = load4(Vnb + off, srv);
     pf_v = load4(vb + off, srv);
   };
+  auto f4 = [](float4 x) { return f32x4{x.x, x.y, x.z, x.w}; };
   auto store_rows = [&]() {
     const int o = srow * LDR + sc4;
-    store4(sDOs + o, pf_do);
-    store4(sDVs + o, pf_dv);
-    store4(sVNs + o, pf_vn);
-    store4(sVs + o, to_f4(pf_v));
+    put_row4(sDOh, sDOl, o, f4(pf_do));
+    put_row4(sDVh, sDVl, o, f4(pf_dv));
+    put_row4(sVNh, sVNl, o, f4(pf_vn));
+    if constexpr (F32) put_row4(sVh, sVl, o, f4(to_f4(pf_v)));
+    else *(u32x2*)(sVh + o) = *(const u32x2*)&pf_v;
   };
   float sfr[NKB][8], dfr[NKB][8];  // state fragments (the states are column-major)
   float sds = 0.f;  // sum of dS_end * S over the state (each element is loaded once here)
@@ -607,9 +630,47 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       pP[jj][v] = xb[kXlpgP + o];
       pLg[jj][v] = xb[kXlpgLg + o];
     }
-  load_rows(0);
-  load_state(0);
+  // ---------------------------------------------------------------- stage
+  // K and Q rows in 16-byte items, every load issued (with the first step's) before any
+  // store, so the workgroup waits for one memory round trip rather than one per item
+  {
+    constexpr int EPI = 16 / (int)sizeof(KT);  // elements per item
+    constexpr int PER = C * DK / EPI;          // items per matrix
+    constexpr int NIT = 2 * PER / CNT;
+    static_assert(NIT * CNT == 2 * PER, "staging split");
+    u32x4 st[NIT];
 #pragma unroll
+    for (int m = 0; m < NIT; ++m) {
+      const int it = tid + m * CNT;
+      const int which = it / PER, rem = it % PER;
+      const int row = rem / (DK / EPI), c = EPI * (rem % (DK / EPI));
+      const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
+                      (long long)hk * DK + c;
+      st[m] = row < nvalid ? *(const u32x4*)src : u32x4{0u, 0u, 0u, 0u};
+    }
+    load_rows(0);
+    load_state(0);
+    if (tid < C) {
+      sG[tid] = xb[kXlpgG + tid];
+      sBt[tid] = ((const float*)(p.rec + ((size_t)ci * Hv + h) * rec_stride + kRecG))[kGateBeta * C + tid];
+    }
+    sRowG[wave][l] = 0.f;
+    sColG[wave][l] = 0.f;
+    sRowB[wave][l] = 0.f;
+    sRowT[wave][l] = 0.f;
+    sRP[wave][l] = 0.f;
+#pragma unroll
+    for (int m = 0; m < NIT; ++m) {
+      const int it = tid + m * CNT;
+      const int which = it / PER, rem = it % PER;
+      const int row = rem / (DK / EPI), c = EPI * (rem % (DK / EPI));
+      *(u32x4*)((which ? sQ : sK) + row * LDK + c) = st[m];
+    }
+  }
+  // (the barrier at the top of the first step orders the staging before every read)
+  // not unrolled: with every fragment a plain LDS read, an unrolled loop lets the
+  // scheduler hoist the reads of several steps and run out of registers
+#pragma unroll 1
   for (int u = 0; u < DV / 32; ++u) {
     __syncthreads();  // the previous step's readers are done
     store_rows();
@@ -634,23 +695,13 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       }
     }
     __syncthreads();
-    Op ow, vw;  // dO and dV_new rows of block bi
-    {
-      float a[8];
-      frag_row<false>(sDOs, LDR, 16 * bi + lr, 0, a);
-      ow = split8(a);
-      frag_row<false>(sDVs, LDR, 16 * bi + lr, 0, a);
-      vw = split8(a);
-    }
+    const Op ow = op_vec(sDOh, sDOl, LDR, 16 * bi, 0);  // dO and dV_new rows of block bi
+    const Op vw = op_vec(sDVh, sDVl, LDR, 16 * bi, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float a[8];
-      frag_row<false>(sDOs, LDR, 16 * i + lr, 0, a);
-      const Op ao = split8(a);
-      frag_row<false>(sDVs, LDR, 16 * i + lr, 0, a);
-      const Op adv = split8(a);
-      frag_row<false>(sVNs, LDR, 16 * i + lr, 0, a);
-      const Op avn = split8(a);
+      const Op ao = op_vec(sDOh, sDOl, LDR, 16 * i, 0);
+      const Op adv = op_vec(sDVh, sDVl, LDR, 16 * i, 0);
+      const Op avn = op_vec(sVNh, sVNl, LDR, 16 * i, 0);
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
         if (wave + CW * kb >= NCB) continue;
@@ -659,8 +710,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         dk[kb][i] = mm3<true, true>(dk[kb][i], avn, bd[kb]);   // V_new dS^T
       }
       if ((i >> 1) == half) {
-        frag_row<false>(sVs, LDR, 16 * i + lr, 0, a);
-        const Op av = split8<F32>(a);
+        const Op av = op_vec<F32>(sVh, sVl, LDR, 16 * i, 0);
         dxa[i & 1] = mm3<true, F32>(dxa[i & 1], vw, av);              // dV_new v^T
         if (i <= bi) dp[i & 1] = mm3<true, true>(dp[i & 1], ow, avn);  // dO V_new^T
       }
@@ -670,7 +720,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
   for (int m = 0; m < C * 16 / CNT; ++m) {
     const int it = tid + m * CNT;
-    store4(sX + (it >> 4) * LDF + 4 * (it & 15), pf_x[m]);
+    put_row4(sXh, sXl, (it >> 4) * LDB + 4 * (it & 15), f4(pf_x[m]));
   }
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
@@ -687,8 +737,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         const float e = el(row);
         rr[v] = dk[kb][i][v] * ldx(sK + row * LDK + col) * e;  // dkdec * kdec
         dk[kb][i][v] *= e;
-        sDW[row * LDW + col] = -dw[kb][i][v];              // dW = -dV_new S^T
       }
+      put_ct(sDWh, sDWl, LDB, 16 * i, 16 * cb, -dw[kb][i]);  // dW = -dV_new S^T
       add_rows(rowG, i, gx);
       add_rows(rP, i, rr);
     }
@@ -696,14 +746,15 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
   for (int jj = 0; jj < 2; ++jj) {
     const int bj = 2 * half + jj;
-    f32x4 pdp;
+    f32x4 pdp, dpg;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
       const float d = row >= col ? dp[jj][v] : 0.f;
       pdp[v] = d * pP[jj][v];
-      sDP[row * LDF + col] = d * gam(row, col);            // dPg = dP * Gamma
+      dpg[v] = d * gam(row, col);                          // dPg = dP * Gamma
     }
+    put_ct(sDPh, sDPl, LDB, 16 * bi, 16 * bj, dpg);
     add_rows(rowG, bi, pdp);
     add_cols(colG, bj, -pdp);
   }
@@ -719,18 +770,15 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       const int bj = 2 * half + jj;
       f32x4 acc = zero4();
 #pragma unroll
-      for (int s = 0; s < DK / 32; ++s) {
-        float a[8];
-        frag_row<false>(sDW, LDW, 16 * bi + lr, 32 * s, a);
-        acc = mm3<true, F32>(acc, split8(a), kq_row<false>(sK, LDK, 16 * bj, 32 * s));
-      }
+      for (int s = 0; s < DK / 32; ++s)
+        acc = mm3<true, F32>(acc, op_tr(sDWh, sDWl, LDB, 16 * bi, 32 * s),
+                             kq_row<false>(sK, LDK, 16 * bj, 32 * s));
       const int col = 16 * bj + lr;
       const float bc = sBt[col], ec = eg(col);
+      f32x4 dx;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 16 * bi + 4 * lq + v;
-        sDX[row * LDF + col] = bc * (dxa[jj][v] + ec * acc[v]);
-      }
+      for (int v = 0; v < 4; ++v) dx[v] = bc * (dxa[jj][v] + ec * acc[v]);
+      put_ct(sDXh, sDXl, LDB, 16 * bi, 16 * bj, dx);
     }
   }
   __syncthreads();
@@ -762,11 +810,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int p2 = i / 2; p2 < 2; ++p2) {
-        float a[8];
-        frag_row<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
-        acc = mm3<true, true>(acc, bo[p2], split8(a));
-      }
+      for (int p2 = i / 2; p2 < 2; ++p2)
+        acc = mm3<true, true>(acc, bo[p2], op_vec(sXh, sXl, LDB, 16 * i, 32 * p2));
       const int row = 16 * i + lr;
       const float4 vf = to_f4(vv4[i]);
       const f32x4 vd = f32x4{vf.x * acc[0], vf.y * acc[1], vf.z * acc[2], vf.w * acc[3]};
@@ -787,12 +832,9 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int p2 = i / 2; p2 < 2; ++p2) {
-        float a[8], b[8];
-        frag_row<false>(sX, LDF, 16 * i + lr, 32 * p2, a);
-        frag_col<false>(sDW, LDW, 16 * cb + lr, 32 * p2, b);
-        acc = mm3<true, true>(acc, split8(a), split8(b));
-      }
+      for (int p2 = i / 2; p2 < 2; ++p2)
+        acc = mm3<true, true>(acc, op_vec(sXh, sXl, LDB, 16 * i, 32 * p2),
+                              op_vec(sDWh, sDWl, LDB, 16 * cb, 32 * p2));
       f32x4 kt;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -809,14 +851,10 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int jj = 0; jj < 2; ++jj) {
       const int bj = 2 * half + jj;
       f32x4 acc = zero4();
-      for (int p2 = bi / 2; p2 < 2; ++p2) {  // X^T is upper triangular
-        float a[8], b[8];
-        frag_row<false>(sX, LDF, 16 * bi + lr, 32 * p2, a);
-        frag_col<false>(sDX, LDF, 16 * bj + lr, 32 * p2, b);
-        acc = mm3<true, true>(acc, split8(a), split8(b));
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v) sM[(16 * bi + 4 * lq + v) * LDF + 16 * bj + lr] = acc[v];
+      for (int p2 = bi / 2; p2 < 2; ++p2)  // X^T is upper triangular
+        acc = mm3<true, true>(acc, op_vec(sXh, sXl, LDB, 16 * bi, 32 * p2),
+                              op_vec(sDXh, sDXl, LDB, 16 * bj, 32 * p2));
+      put_ct(sMh, sMl, LDB, 16 * bi, 16 * bj, acc);
     }
   }
   __syncthreads();  // M1 complete (a row block's two halves come from two wavefronts)
@@ -829,12 +867,9 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 acc = zero4();
       if (bj <= bi) {
 #pragma unroll
-        for (int p2 = 0; p2 <= bj / 2; ++p2) {
-          float a[8], b[8];
-          frag_row<false>(sM, LDF, 16 * bi + lr, 32 * p2, a);
-          frag_col<false>(sX, LDF, 16 * bj + lr, 32 * p2, b);  // rows of X
-          acc = mm3<true, true>(acc, split8(a), split8(b));
-        }
+        for (int p2 = 0; p2 <= bj / 2; ++p2)  // B: rows of X
+          acc = mm3<true, true>(acc, op_tr(sMh, sMl, LDB, 16 * bi, 32 * p2),
+                                op_tr(sXh, sXl, LDB, 16 * bj, 32 * p2));
       }
       dl[jj] = acc;
     }
@@ -842,7 +877,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int bj = 2 * half + jj;
-      f32x4 lb, ld;
+      f32x4 lb, ld, qm;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
@@ -850,8 +885,9 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         const float lg = pLg[jj][v];
         lb[v] = d * lg;
         ld[v] = d * sBt[row] * lg;                      // dL * L
-        sM[row * LDF + col] = sBt[row] * d * gam(row, col);  // Qm = diag(beta) (dL * Gamma)
+        qm[v] = sBt[row] * d * gam(row, col);           // Qm = diag(beta) (dL * Gamma)
       }
+      put_ct(sMh, sMl, LDB, 16 * bi, 16 * bj, qm);
       add_rows(rowB, bi, lb);
       add_rows(rowG, bi, ld);
       add_cols(colG, bj, -ld);
@@ -869,25 +905,15 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 a_k = dk[kb][i], a_q = dq[kb][i], a_t = zero4();
 #pragma unroll
       for (int p2 = 0; p2 < 2; ++p2) {
-        float a[8];
         const Op bk = kq_col<false>(sK, LDK, 16 * cb, 32 * p2);
-        // symmetric Qm + Qm^T
-        {
-          float x[8], y[8];
-          frag_row<false>(sM, LDF, 16 * i + lr, 32 * p2, x);
-          frag_col<false>(sM, LDF, 16 * i + lr, 32 * p2, y);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a[e] = x[e] + y[e];
-          a_k = mm3<true, F32>(a_k, split8(a), bk);
-        }
-        if (p2 <= i / 2) {  // dPg is lower triangular
-          frag_row<false>(sDP, LDF, 16 * i + lr, 32 * p2, a);
-          a_q = mm3<true, F32>(a_q, split8(a), bk);
-        }
-        if (p2 >= i / 2) {  // dPg^T is upper triangular
-          frag_col<false>(sDP, LDF, 16 * i + lr, 32 * p2, a);
-          a_t = mm3<true, F32>(a_t, split8(a), kq_col<false>(sQ, LDK, 16 * cb, 32 * p2));
-        }
+        // (Qm + Qm^T) k as Qm k + Qm^T k
+        a_k = mm3<true, F32>(a_k, op_tr(sMh, sMl, LDB, 16 * i, 32 * p2), bk);
+        a_k = mm3<true, F32>(a_k, op_vec(sMh, sMl, LDB, 16 * i, 32 * p2), bk);
+        if (p2 <= i / 2)  // dPg is lower triangular
+          a_q = mm3<true, F32>(a_q, op_tr(sDPh, sDPl, LDB, 16 * i, 32 * p2), bk);
+        if (p2 >= i / 2)  // dPg^T is upper triangular
+          a_t = mm3<true, F32>(a_t, op_vec(sDPh, sDPl, LDB, 16 * i, 32 * p2),
+                               kq_col<false>(sQ, LDK, 16 * cb, 32 * p2));
       }
       float* dqo = p.dqh + (t0 * Hv + h) * (long long)DK;
       float* dko = p.dkh + (t0 * Hv + h) * (long long)DK;
@@ -921,7 +947,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     float sds = 0.f;
 #pragma unroll
     for (int w = 0; w < CW; ++w) sds += sRed[w];
-    if (i == C - 1) dG += rsum + __expf(Gl) * sds;
+    if (i == C - 1) dG += rsum + __expf(sG[C - 1]) * sds;
     // dg_t = sum_{i >= t} dG_i (G = cumsum(g), deltanet.py:98)
     float x = dG;
 #pragma unroll
