@@ -224,18 +224,84 @@ __device__ __forceinline__ float wave_sum(float s) {
 
 __device__ __forceinline__ int rec_mode(bool f32) { return f32 ? MODE_F32 : MODE_BF16; }
 
+// Split-matrix operands.  A 64-row fp32 matrix the backward kernels read as MFMA operands
+// is kept in LDS as bf16 hi and lo planes (hi + lo is the value to ~2^-16 relative), split
+// once when it is written, so no fragment read converts.  op_vec: lane (q, r) gets entries
+// k0 + 8q .. +7 of storage row r0 + r (one 16-byte read per plane); op_tr: entries
+// k0 + 8q .. +7 down storage column c0 + r (two transposed 8-byte reads per plane).
+template <bool LO = true>
+__device__ __forceinline__ Op op_vec(const bf16_t* h, const bf16_t* lo, int ld, int r0, int k0) {
+  const int l = lane_id();
+  const int off = (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
+  Op o;
+  o.h = *(const u32x4*)(h + off);
+  if constexpr (LO) o.l = *(const u32x4*)(lo + off);
+  else o.l = o.h;
+  return o;
+}
+template <bool LO = true>
+__device__ __forceinline__ Op op_tr(const bf16_t* h, const bf16_t* lo, int ld, int c0, int k0) {
+  Op o;
+  o.h = frag_tr(h, ld, k0, c0);
+  if constexpr (LO) o.l = frag_tr(lo, ld, k0, c0);
+  else o.l = o.h;
+  return o;
+}
+// A C-layout tile (lane (q, r): rows row0 + 4q .. +3 of column col0 + r) into column-major
+// planes (storage [col][row]): one 8-byte write per plane.
+__device__ __forceinline__ void put_ct(bf16_t* h, bf16_t* lo, int ld, int row0, int col0, f32x4 c) {
+  const int l = lane_id();
+  const int off = (col0 + (l & 15)) * ld + row0 + 4 * (l >> 4);
+  *(u32x2*)(h + off) = pack_hi4(c);
+  *(u32x2*)(lo + off) = pack_lo4(c);
+}
+// Four consecutive entries (one row, 4 columns from col) into row-major planes.
+__device__ __forceinline__ void put_row4(bf16_t* h, bf16_t* lo, int off, f32x4 c) {
+  *(u32x2*)(h + off) = pack_hi4(c);
+  *(u32x2*)(lo + off) = pack_lo4(c);
+}
+
+// op_vec in the block-pair contraction order (kslot<true>): entries k0 + 4q .. +3 and
+// k0 + 16 + 4q .. +3 of storage row r0 + r.
+__device__ __forceinline__ Op op_pair(const bf16_t* h, const bf16_t* lo, int ld, int r0, int k0) {
+  const int l = lane_id();
+  const int off = (r0 + (l & 15)) * ld + k0 + 4 * (l >> 4);
+  Op o;
+  const u32x2 a = *(const u32x2*)(h + off), b = *(const u32x2*)(h + off + 16);
+  const u32x2 c = *(const u32x2*)(lo + off), d = *(const u32x2*)(lo + off + 16);
+  o.h = u32x4{a[0], a[1], b[0], b[1]};
+  o.l = u32x4{c[0], c[1], d[0], d[1]};
+  return o;
+}
+// the fp32 values (hi + lo) of an operand's 8 slots
+__device__ __forceinline__ void op_values(const Op& o, float* x) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    x[2 * w] = __uint_as_float(o.h[w] << 16) + __uint_as_float(o.l[w] << 16);
+    x[2 * w + 1] = __uint_as_float(o.h[w] & 0xffff0000u) + __uint_as_float(o.l[w] & 0xffff0000u);
+  }
+}
+
 // ============================================================================ reverse scan
 
 template <int DK, bool F32>
 __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
   using KT = typename std::conditional<F32, float, bf16_t>::type;
   constexpr int LDK = DK + (F32 ? 4 : 8);
+  constexpr int LDB = C + 8;  // stride (bf16) of a split plane
   __shared__ __align__(16) KT sK[C * LDK];
   __shared__ __align__(16) KT sQ[C * LDK];
-  __shared__ __align__(16) float sDO[C * LDF];
-  __shared__ __align__(16) float sX[C * LDF];
-  __shared__ __align__(16) float sP[C * LDF];
+  // dO (this block's 64 columns), X^T and P, row-major, as bf16 hi / lo planes
+  __shared__ __align__(16) bf16_t sDO[2 * C * LDB];
+  __shared__ __align__(16) bf16_t sX[2 * C * LDB];
+  __shared__ __align__(16) bf16_t sP[2 * C * LDB];
   __shared__ __align__(16) float sGate[4 * C];
+  bf16_t* const sDOh = sDO;
+  bf16_t* const sDOl = sDO + C * LDB;
+  bf16_t* const sXh = sX;
+  bf16_t* const sXl = sX + C * LDB;
+  bf16_t* const sPh = sP;
+  bf16_t* const sPl = sP + C * LDB;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -305,13 +371,15 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
       const int it = tid + m * NT;
-      store4(sDO + (it >> 4) * LDF + 4 * (it & 15), pdo[m]);
+      put_row4(sDOh, sDOl, (it >> 4) * LDB + 4 * (it & 15), f32x4{pdo[m].x, pdo[m].y, pdo[m].z, pdo[m].w});
     }
 #pragma unroll
     for (int m = 0; m < 2 * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
-      store4((which ? sP : sX) + (rem >> 4) * LDF + 4 * (rem & 15), pxp[m]);
+      const f32x4 v = f32x4{pxp[m].x, pxp[m].y, pxp[m].z, pxp[m].w};
+      if (which) put_row4(sPh, sPl, (rem >> 4) * LDB + 4 * (rem & 15), v);
+      else put_row4(sXh, sXl, (rem >> 4) * LDB + 4 * (rem & 15), v);
     }
     sGate[tid] = pgate;
   };
@@ -358,12 +426,9 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int p2 = i / 2; p2 < 2; ++p2) {  // P^T is upper triangular
-        float a[8], b[8];
-        frag_col<false>(sP, LDF, 16 * i + lr, 32 * p2, a);
-        frag_col<false>(sDO, LDF, c + lr, 32 * p2, b);
-        acc = mm3<true, true>(acc, split8(a), split8(b));
-      }
+      for (int p2 = i / 2; p2 < 2; ++p2)  // P^T is upper triangular
+        acc = mm3<true, true>(acc, op_tr(sPh, sPl, LDB, 16 * i, 32 * p2),
+                              op_tr(sDOh, sDOl, LDB, c, 32 * p2));
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * i + 4 * lq + v;
@@ -388,11 +453,8 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int p2 = i / 2; p2 < 2; ++p2) {  // X^T is upper triangular
-        float a[8];
-        frag_row<true>(sX, LDF, 16 * i + lr, 32 * p2, a);  // X^T rows (stored transposed)
-        acc = mm3<true, true>(acc, split8(a), dvp[p2]);
-      }
+      for (int p2 = i / 2; p2 < 2; ++p2)  // X^T is upper triangular; X^T rows (stored transposed)
+        acc = mm3<true, true>(acc, op_pair(sXh, sXl, LDB, 16 * i, 32 * p2), dvp[p2]);
 #pragma unroll
       for (int v = 0; v < 4; ++v) y[i][v] = sB[16 * i + 4 * lq + v] * acc[v];
     }
@@ -401,7 +463,7 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 #pragma unroll
     for (int p2 = 0; p2 < 2; ++p2) {
       float x[8];
-      frag_col<false>(sDO, LDF, c + lr, 32 * p2, x);
+      op_values(op_tr(sDOh, sDOl, LDB, c, 32 * p2), x);
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] *= sEGS[32 * p2 + 8 * lq + e];
       b1[p2] = split8(x);
@@ -436,43 +498,6 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 }
 
 // ============================================================================ chunk-local gradients
-
-// Split-matrix operands.  A 64-row fp32 matrix the gradient kernel reads as MFMA operands
-// is kept in LDS as bf16 hi and lo planes (hi + lo is the value to ~2^-16 relative), split
-// once when it is written, so no fragment read converts.  op_vec: lane (q, r) gets entries
-// k0 + 8q .. +7 of storage row r0 + r (one 16-byte read per plane); op_tr: entries
-// k0 + 8q .. +7 down storage column c0 + r (two transposed 8-byte reads per plane).
-template <bool LO = true>
-__device__ __forceinline__ Op op_vec(const bf16_t* h, const bf16_t* lo, int ld, int r0, int k0) {
-  const int l = lane_id();
-  const int off = (r0 + (l & 15)) * ld + k0 + 8 * (l >> 4);
-  Op o;
-  o.h = *(const u32x4*)(h + off);
-  if constexpr (LO) o.l = *(const u32x4*)(lo + off);
-  else o.l = o.h;
-  return o;
-}
-template <bool LO = true>
-__device__ __forceinline__ Op op_tr(const bf16_t* h, const bf16_t* lo, int ld, int c0, int k0) {
-  Op o;
-  o.h = frag_tr(h, ld, k0, c0);
-  if constexpr (LO) o.l = frag_tr(lo, ld, k0, c0);
-  else o.l = o.h;
-  return o;
-}
-// A C-layout tile (lane (q, r): rows row0 + 4q .. +3 of column col0 + r) into column-major
-// planes (storage [col][row]): one 8-byte write per plane.
-__device__ __forceinline__ void put_ct(bf16_t* h, bf16_t* lo, int ld, int row0, int col0, f32x4 c) {
-  const int l = lane_id();
-  const int off = (col0 + (l & 15)) * ld + row0 + 4 * (l >> 4);
-  *(u32x2*)(h + off) = pack_hi4(c);
-  *(u32x2*)(lo + off) = pack_lo4(c);
-}
-// Four consecutive entries (one row, 4 columns from col) into row-major planes.
-__device__ __forceinline__ void put_row4(bf16_t* h, bf16_t* lo, int off, f32x4 c) {
-  *(u32x2*)(h + off) = pack_hi4(c);
-  *(u32x2*)(lo + off) = pack_lo4(c);
-}
 
 // Eight wavefronts (two per SIMD: the LDS holds one workgroup per CU).  Wavefront w owns
 // dk column blocks w + 8m and dv column blocks w + 8m of the (chunk x head) gradients,
