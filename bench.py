@@ -153,7 +153,7 @@ def cpu_decode_baseline(B=8, budget_s=10.0):
 # scaled by a plain copy kernel's counters), for the shapes they were taken on; summaries
 # and commands in profiles/prefill_c1.md and profiles/decode_step_c2_b64.md.
 MEASURED_TRAFFIC = {
-    ("core", 4, 4096, 16, 32, 128): 1_146_940_416,  # prep 132.6 MiB + 281.9, scan 415.8 + 263.5
+    ("core", 4, 4096, 16, 32, 128): 1_154_719_808,  # prep 152.2 MiB + 284.7, scan 408.3 + 256.0
     ("decode", 64, 16, 32, 128): 277_401_702,       # state read + written once
 }
 

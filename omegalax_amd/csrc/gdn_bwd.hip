@@ -38,7 +38,6 @@ namespace {
 
 constexpr int C = kC;
 constexpr int NT = kNT;
-constexpr int LDF = C + 4;  // row stride (floats) of 64-wide fp32 LDS matrices
 
 struct Op {
   u32x4 h, l;
@@ -892,9 +891,10 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       f32x4 acc = zero4();
       if (bj <= bi) {
 #pragma unroll
-        for (int p2 = 0; p2 <= bj / 2; ++p2)  // B: rows of X
-          acc = mm3<true, true>(acc, op_tr(sMh, sMl, LDB, 16 * bi, 32 * p2),
-                                op_tr(sXh, sXl, LDB, 16 * bj, 32 * p2));
+        for (int p2 = 0; p2 < 2; ++p2)  // B: rows of X
+          if (p2 <= bj / 2)
+            acc = mm3<true, true>(acc, op_tr(sMh, sMl, LDB, 16 * bi, 32 * p2),
+                                  op_tr(sXh, sXl, LDB, 16 * bj, 32 * p2));
       }
       dl[jj] = acc;
     }

@@ -328,8 +328,10 @@ __device__ __forceinline__ void load_task_inputs(const ChunkParams& p, const Pre
 // Each workgroup runs one task, whose first phase waits on its global loads; three
 // resident workgroups per CU (the LDS limit) hide that latency.  A persistent variant
 // that prefetched the next task into registers needed about 80 more registers, so
-// only two fitted, and was slower.
-constexpr int kPrepBlocksPerCU = 3;
+// only two fitted, and was slower.  fp32 inputs stage hi and lo rows, whose LDS allows
+// two workgroups.
+template <int MODE>
+constexpr int prep_blocks_per_cu() { return MODE == MODE_F32 ? 2 : 3; }
 
 // A-layout 16x16 fp32 tile (lane (q, r) holds M[16 bi + r][16 bj + 4q .. +3]) into a
 // row-major 64x64 matrix
@@ -342,7 +344,7 @@ __device__ __forceinline__ void put_f32_tile(float* m, int bi, int bj, f32x4 a) 
 // (X^T with X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in
 // gdn_chunk.h).
 template <int DK, int MODE, bool BWD = false>
-__global__ __launch_bounds__(NT, kPrepBlocksPerCU) void prep_kernel(ChunkParams p) {
+__global__ __launch_bounds__(NT, prep_blocks_per_cu<MODE>()) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, F32 = MODE == MODE_F32;
