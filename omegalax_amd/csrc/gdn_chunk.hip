@@ -43,14 +43,17 @@ namespace omx {
 namespace {
 
 constexpr int C = kC;
-constexpr int NWC = 4;         // column wavefronts per workgroup
-constexpr int NT = kNT;
-constexpr int BV = 16 * NWC;   // state columns per workgroup
 constexpr int LDT = kLDT;
-static_assert(NT == 64 * NWC, "threads");
+constexpr int kBlockCols = 64;  // dv columns per block of the other kernels (nb = dv / 64)
 
-template <int DK, int MODE>
+// NWC_: 16-column state tiles (compute wavefronts) per workgroup.  Four on every path;
+// the direct-load path also runs with two or one, so that sequences x heads x dv / 16 tiles
+// fill the chip when 64-column workgroups would leave CUs idle.
+template <int DK, int MODE, int NWC_ = 4>
 struct Cfg {
+  static constexpr int NWC = NWC_;
+  static constexpr int BV = 16 * NWC;  // state columns per workgroup
+  static constexpr int NT = 64 * NWC;  // compute threads
   static constexpr bool IS = MODE == MODE_F32;  // q/k/v split hi+lo
   static constexpr bool OS = MODE == MODE_F32;  // output-path operands split
   static constexpr int NS = IS ? 2 : 1;
@@ -67,10 +70,10 @@ struct Cfg {
   // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
   // into padded rows.
   static constexpr bool DIRECT = MODE != MODE_F32 && DK == 128;
-  // with direct loads a fifth wavefront issues them (it shares a SIMD with one of the
-  // four compute wavefronts, so each may hold at most half the register file)
+  // with direct loads one more wavefront issues them; next to four compute wavefronts it
+  // shares a SIMD with one of them, so each may hold at most half the register file
   static constexpr int NTH = DIRECT ? NT + 64 : NT;
-  static constexpr int WPE = DIRECT ? 2 : 1;
+  static constexpr int WPE = DIRECT && NWC == 4 ? 2 : 1;
   static constexpr int NBUF = DIRECT ? 2 : 1;
   static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
   static constexpr int SZV = DIRECT ? C * BV : NS * C * LDT;  // elements of a V buffer
@@ -78,6 +81,7 @@ struct Cfg {
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
   static_assert(!DIRECT || REC % 1024 == 0, "direct loads move the record in 1 KiB pieces");
   static_assert(DK % 32 == 0 && DK <= 128, "dk");
+  static_assert(DIRECT || NWC == 4, "register staging runs four column wavefronts");
   static_assert(NI_KQ * NT == 2 * C * SEGS && (C * SEGS) % NT == 0, "item split");
   static_assert(NI_V * NT == C * (BV / 8), "item split");
 };
@@ -100,6 +104,7 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
                                          long long t0, int nvalid, const unsigned char* rec,
                                          int hk, int h, int col0) {
   using Q_ = Cfg<DK, MODE>;
+  constexpr int NT = Q_::NT, BV = Q_::BV;
   constexpr bool F32 = MODE == MODE_F32;
   using In = typename std::conditional<F32, float, bf16_t>::type;
   const int tid = threadIdx.x;
@@ -138,16 +143,19 @@ __device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE
 // fragment read hit 16 different segments (all 64 banks), and swz_k(r) >> 1 is
 // distinct over rows 0..7 and over rows 8..15, the rows one pass of the transposed
 // 8-byte read (4 consecutive rows per 16 lanes) covers, so its 8 rows x 32 bytes
-// also spread over all banks.  A V row (64 columns) is 8 segments; swz_v(r) = r & 6
-// makes the 8 rows x 32 bytes of a transposed read pass conflict-free the same way.
+// also spread over all banks.  A V row of a 64-column block is 8 segments; swz_v(r) = r & 6
+// makes the 8 rows x 32 bytes of a transposed read pass conflict-free the same way.  Rows
+// of narrower blocks (SV = 4 or 2 segments) keep the bits of r & 6 that index a segment.
 __device__ __forceinline__ int swz_k(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
-__device__ __forceinline__ int swz_v(int r) { return r & 6; }
+template <int SV>
+__device__ __forceinline__ int swz_v(int r) { return r & 6 & (SV - 1); }
 
-// element offset of (row, col) in a swizzled buffer with 8-element segments
+// element offset of (row, col) in a swizzled buffer with 8-element segments: K / Q rows
+// (128 elements) or V rows (ROWLEN = the block's columns)
 template <int ROWLEN>
 __device__ __forceinline__ int swz_off(int row, int col) {
   const int g = col >> 3;
-  const int sw = ROWLEN == 128 ? swz_k(row & 15) : swz_v(row);
+  const int sw = ROWLEN == 128 ? swz_k(row & 15) : swz_v<ROWLEN / 8>(row);
   return row * ROWLEN + ((g ^ sw) << 3) + (col & 7);
 }
 
@@ -162,6 +170,7 @@ __device__ __forceinline__ u32x2 swz_rows4_k(const bf16_t* base, int row0, int c
   return ds_read_tr(base + swz_off<128>(row0 + 4 * q + (s >> 2), col0 + 4 * (s & 3)));
 }
 // four consecutive rows row0 + 4q .. +3 of column col0 + r of a V buffer (as rows4_tr)
+template <int BV>
 __device__ __forceinline__ u32x2 swz_rows4_v(const bf16_t* base, int row0, int col0) {
   const int l = lane_id(), q = l >> 4, s = l & 15;
   return ds_read_tr(base + swz_off<BV>(row0 + 4 * q + (s >> 2), col0 + 4 * (s & 3)));
@@ -191,8 +200,8 @@ __device__ __forceinline__ u32x4 join(u32x2 a, u32x2 b) { return u32x4{a[0], a[1
 
 // Issue one chunk's loads straight into an LDS buffer (global_load_lds_dwordx4: lane i
 // of an instruction writes 16 bytes at the buffer offset + 16 i), all from the loader
-// wavefront: 16 instructions each of K and Q rows, 8 of V rows and one per KiB of the
-// record.  Rows past the sequence end repeat the last valid row: every product they
+// wavefront: 16 instructions each of K and Q rows, BV / 8 of V rows and one per KiB of
+// the record.  Rows past the sequence end repeat the last valid row: every product they
 // enter is multiplied by their zero beta, so they need no clearing.  Addresses are a
 // uniform base plus a 32-bit lane byte offset (scalar-base loads).
 typedef __attribute__((address_space(3))) void lds_void;
@@ -201,12 +210,14 @@ typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // The buffers are passed as LDS-space pointers (cast where the __shared__ arrays are
 // named), so no generic-to-LDS conversion happens here.
-template <int DK, int MODE>
+template <int DK, int MODE, int BV>
 __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, int nvalid,
                                           const unsigned char* rec, int hk, int h, int col0,
                                           lds_bf16* sK, lds_bf16* sQ, lds_bf16* sV, lds_u8* sRec) {
   typedef __attribute__((address_space(1))) void glob_void;
   constexpr int NRP = rec_bytes(MODE) / 1024;
+  // V rows: SV 16-byte segments per row, 64 / SV rows per instruction, SV instructions
+  constexpr int SV = BV / 8, RPI = 64 / SV;
   const int l = lane_id();
   const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
   const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
@@ -214,7 +225,7 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
   const unsigned kld = (unsigned)p.ks_ld, qld = (unsigned)p.qs_ld, vld = (unsigned)p.vs_ld;
   if (nvalid == C) {
     // K/Q instruction mi covers rows 4 mi + l/16, whose swizzle repeats every 4
-    // instructions, and V instruction mi rows 8 mi + l/8, whose swizzle does not depend
+    // instructions, and V instruction mi rows RPI mi + l/SV, whose swizzle does not depend
     // on mi: a few lane offsets plus uniform row steps
 #pragma unroll
     for (int m0 = 0; m0 < 4; ++m0) {
@@ -229,11 +240,11 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                          (lds_void*)(sQ + 512 * mi), 16, 0, 0);
       }
     }
-    const unsigned vrow = (unsigned)(l >> 3);
-    const unsigned vo = 2u * (vrow * vld + 8u * (unsigned)((l & 7) ^ swz_v((int)vrow)));
+    const unsigned vrow = (unsigned)(l / SV);
+    const unsigned vo = 2u * (vrow * vld + 8u * (unsigned)((l % SV) ^ swz_v<SV>((int)vrow)));
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi)
-      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb + (long long)(8 * mi) * p.vs_ld, vo),
+    for (int mi = 0; mi < SV; ++mi)
+      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb + (long long)(RPI * mi) * p.vs_ld, vo),
                                        (lds_void*)(sV + 512 * mi), 16, 0, 0);
   } else {
     // a sequence's last, partial chunk: rows past its end repeat the last valid row
@@ -248,10 +259,10 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                        (lds_void*)(sQ + 512 * mi), 16, 0, 0);
     }
 #pragma unroll
-    for (int mi = 0; mi < 8; ++mi) {
-      const int row = 8 * mi + (l >> 3);
+    for (int mi = 0; mi < SV; ++mi) {
+      const int row = RPI * mi + l / SV;
       const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
-      const unsigned g = (unsigned)((l & 7) ^ swz_v(row));
+      const unsigned g = (unsigned)((l % SV) ^ swz_v<SV>(row));
       __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, 2u * (rr * vld + 8u * g)),
                                        (lds_void*)(sV + 512 * mi), 16, 0, 0);
     }
@@ -264,12 +275,13 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
 
 // BWD (the backward pass's recompute): stores the state entering every chunk and V_new,
 // and o only when p.o is set.
-template <int DK, int MODE, bool BWD = false>
+template <int DK, int MODE, bool BWD = false, int NWC_ = 4>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
 // SIMD) instead of holding back for a second workgroup.
-__global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE>::WPE, Cfg<DK, MODE>::WPE))) void scan_kernel(ChunkParams p) {
-  using Q_ = Cfg<DK, MODE>;
+__global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE, NWC_>::WPE, Cfg<DK, MODE, NWC_>::WPE))) void scan_kernel(ChunkParams p) {
+  using Q_ = Cfg<DK, MODE, NWC_>;
+  constexpr int NWC = Q_::NWC, BV = Q_::BV, NT = Q_::NT;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
   constexpr bool F32 = MODE == MODE_F32;
@@ -343,7 +355,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     const int nv0 = (int)((s1 - s0) < C ? (s1 - s0) : C);
     if constexpr (DIRECT) {
       if (loader) {
-        stage_all<DK, MODE>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
+        stage_all<DK, MODE, BV>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
                             (lds_bf16*)sV0, (lds_u8*)sRec0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the first barrier
       }
@@ -461,7 +473,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
     float vv[4][4];  // V at rows 16i + 4lq + v, column 16w + lr
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x2 vw = DIRECT ? swz_rows4_v(sV, 16 * i, 16 * wave) : rows4_tr(sV, LDT, 16 * i, 16 * wave);
+      const u32x2 vw = DIRECT ? swz_rows4_v<BV>(sV, 16 * i, 16 * wave) : rows4_tr(sV, LDT, 16 * i, 16 * wave);
       vv[i][0] = __uint_as_float(vw[0] << 16);
       vv[i][1] = __uint_as_float(vw[0] & 0xffff0000u);
       vv[i][2] = __uint_as_float(vw[1] << 16);
@@ -717,7 +729,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
         if (j + 1 < nchunks) {
           const long long tn = s0 + (long long)(j + 1) * C;
           const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
-          stage_all<DK, MODE>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
+          stage_all<DK, MODE, BV>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the next barrier
       };
@@ -771,21 +783,61 @@ __global__ __launch_bounds__((Cfg<DK, MODE>::NTH)) __attribute__((amdgpu_waves_p
   }
 }
 
-template <int DK, int MODE, bool BWD = false>
+// The scan's workgroups cover Cfg::BV columns each; p.nb (the other kernels' 64-column
+// blocks) is replaced by the scan's own count in a copy of the parameters.
+template <int DK, int MODE, bool BWD = false, int NWC = 4>
 hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
-  const unsigned grid = (unsigned)(p.N * p.Hv * p.nb);
-  hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD>), dim3(grid), dim3(Cfg<DK, MODE>::NTH), 0, stream, p);
+  using Q_ = Cfg<DK, MODE, NWC>;
+  ChunkParams q = p;
+  q.nb = p.DV / Q_::BV;
+  const unsigned grid = (unsigned)(q.N * q.Hv * q.nb);
+  hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD, NWC>), dim3(grid), dim3(Q_::NTH), 0, stream, q);
   return hipGetLastError();
+}
+
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
+      v = 256;
+    cus[dev] = v;
+  }
+  return cus[dev];
+}
+
+// Column tiles per workgroup for the direct-load scan: 4 (64 columns) when that gives a
+// workgroup per CU, else 2 or 1, the widest that still does.  The workgroups walk their
+// sequences' chunks in order, so a grid smaller than the chip leaves CUs idle for the
+// whole call; narrower workgroups also leave each CU's LDS to fewer wavefronts.
+int scan_tiles_per_wg(const ChunkParams& p) {
+  const long long tiles = (long long)p.N * p.Hv * (p.DV / 16);
+  const long long cus = device_cus();
+  if (tiles >= 4 * cus) return 4;
+  if (tiles >= 2 * cus) return 2;
+  return 1;
+}
+
+template <int DK, int MODE>
+hipError_t launch_scan_direct(const ChunkParams& p, hipStream_t stream) {
+  switch (scan_tiles_per_wg(p)) {
+    case 1: return launch_scan_cfg<DK, MODE, false, 1>(p, stream);
+    case 2: return launch_scan_cfg<DK, MODE, false, 2>(p, stream);
+    default: return launch_scan_cfg<DK, MODE, false, 4>(p, stream);
+  }
 }
 
 }  // namespace
 
-int chunk_block_cols() { return BV; }
+int chunk_block_cols() { return kBlockCols; }
 
 int chunk_record_bytes(int mode) { return rec_bytes(mode); }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
-  if (dv % BV != 0 || dv > 256) return false;
+  if (dv % kBlockCols != 0 || dv > 256) return false;
   if (f32_inputs) return dk == 32 || dk == 64;
   return dk == 64 || dk == 128;
 }
@@ -812,11 +864,11 @@ hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream) {
     return hipErrorInvalidValue;
   }
   if (mode == MODE_LAYER) {
-    if (p.dk == 128) return launch_scan_cfg<128, MODE_LAYER>(p, stream);
+    if (p.dk == 128) return launch_scan_direct<128, MODE_LAYER>(p, stream);
     if (p.dk == 64) return launch_scan_cfg<64, MODE_LAYER>(p, stream);
     return hipErrorInvalidValue;
   }
-  if (p.dk == 128) return launch_scan_cfg<128, MODE_BF16>(p, stream);
+  if (p.dk == 128) return launch_scan_direct<128, MODE_BF16>(p, stream);
   if (p.dk == 64) return launch_scan_cfg<64, MODE_BF16>(p, stream);
   return hipErrorInvalidValue;
 }
