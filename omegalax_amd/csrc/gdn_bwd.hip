@@ -182,6 +182,11 @@ __device__ __forceinline__ u32x2 load4(const bf16_t* src, bool valid) {
   return valid ? *(const u32x2*)src : u32x2{0u, 0u};
 }
 __device__ __forceinline__ void store4(float* dst, float4 x) { *(float4*)dst = x; }
+// a float at the precision T (bf16 rounded to nearest even)
+template <class T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return f2bf(x); }
+
 __device__ __forceinline__ float4 to_f4(float4 x) { return x; }
 __device__ __forceinline__ float4 to_f4(u32x2 x) {
   return float4{__uint_as_float(x[0] << 16), __uint_as_float(x[0] & 0xffff0000u),
@@ -940,14 +945,16 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
           a_t = mm3<true, F32>(a_t, op_vec(sDPh, sDPl, LDB, 16 * i, 32 * p2),
                                kq_col<false>(sQ, LDK, 16 * cb, 32 * p2));
       }
-      float* dqo = p.dqh + (t0 * Hv + h) * (long long)DK;
-      float* dko = p.dkh + (t0 * Hv + h) * (long long)DK;
+      // per value head rows at the input precision: the q/k finalisation sums them and
+      // rounds to that precision anyway
+      KT* dqo = (KT*)p.dqh + (t0 * Hv + h) * (long long)DK;
+      KT* dko = (KT*)p.dkh + (t0 * Hv + h) * (long long)DK;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * i + 4 * lq + v, col = 16 * cb + lr;
         if (row < nvalid) {
-          dqo[(long long)row * Hv * DK + col] = scale * a_q[v];
-          dko[(long long)row * Hv * DK + col] = a_k[v] + scale * a_t[v];
+          dqo[(long long)row * Hv * DK + col] = from_f32<KT>(scale * a_q[v]);
+          dko[(long long)row * Hv * DK + col] = from_f32<KT>(a_k[v] + scale * a_t[v]);
         }
       }
     }
@@ -1005,10 +1012,10 @@ __global__ __launch_bounds__(NT) void qk_final_kernel(BwdParams p, long long row
   const long long row = rid % rows;
   const long long token = row / p.Hk;
   const int hk = (int)(row % p.Hk);
-  const float* src = (which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk + c4;
+  const In* src = (const In*)(which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk + c4;
   float d[4] = {0.f, 0.f, 0.f, 0.f}, x[4];
   for (int g = 0; g < gqa; ++g) {
-    const float4 w = *(const float4*)(src + (long long)g * dk);
+    const float4 w = to_f4(*(const typename Vec4<In>::type*)(src + (long long)g * dk));
     d[0] += w.x; d[1] += w.y; d[2] += w.z; d[3] += w.w;
   }
   const In* x_in = (const In*)(which ? p.k : p.q) + row * dk + c4;

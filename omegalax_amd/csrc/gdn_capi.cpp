@@ -448,8 +448,8 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
   b.dstates = (float*)(base + ws.dstates);
   b.dvnew = (float*)(base + ws.dvnew);
   b.dh0 = d_initial_state;
-  b.dqh = (float*)(base + ws.dqh);
-  b.dkh = (float*)(base + ws.dkh);
+  b.dqh = base + ws.dqh;  // sized for fp32; bf16 inputs use the first half
+  b.dkh = base + ws.dkh;
   b.dv = dv; b.dg = dg; b.dbeta = dbeta;
   b.q = q; b.k = k; b.dq = dq; b.dk_out = dk;
   b.cu_seqlens = cu_seqlens; b.chunk_off = p.chunk_off;
@@ -606,8 +606,8 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   bp.dstates = (float*)(base + ws.c.dstates);
   bp.dvnew = (float*)(base + ws.c.dvnew);
   bp.dh0 = d_initial_state;
-  bp.dqh = (float*)(base + ws.c.dqh);
-  bp.dkh = (float*)(base + ws.c.dkh);
+  bp.dqh = base + ws.c.dqh;
+  bp.dkh = base + ws.c.dkh;
   bp.dv = lp.grad_v; bp.dg = (float*)(base + ws.dg); bp.dbeta = (float*)(base + ws.dbeta);
   bp.q = lp.q; bp.k = lp.k; bp.dq = lp.grad_q; bp.dk_out = lp.grad_k;
   bp.cu_seqlens = cu_seqlens; bp.chunk_off = p.chunk_off;

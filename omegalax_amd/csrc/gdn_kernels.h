@@ -100,8 +100,9 @@ struct BwdParams {
   float* dstates;              // gradient of the state leaving each chunk [slot][Hv][DV][dk]
   float* dvnew;                // gradient of V_new [tokens][Hv][DV]
   float* dh0;                  // [N][Hv][dk][DV] or null
-  float* dqh;                  // per value head gradient of the normalised q [tokens][Hv][dk]
-  float* dkh;                  // likewise k
+  void* dqh;                   // per value head gradient of the normalised q [tokens][Hv][dk],
+                               // at the input precision (bf16 or fp32)
+  void* dkh;                   // likewise k
   void* dv;                    // [tokens][Hv][DV], input precision
   float* dg;                   // [tokens][Hv]
   float* dbeta;                // [tokens][Hv]
