@@ -11,11 +11,12 @@
 //     O     = scale e^G (Q S) + P V_new                        (:130-137)
 //     S    <- e^{G_last} S + K^T diag(e^{G_last - G}) V_new    (:139-142)
 //
-// Work mapping.  One workgroup of 4 wavefronts per (sequence, value head,
-// 64-column block of dv) walks that sequence's chunks in order.  Wavefront w
-// owns state columns [16w, 16w+16) of the block: its fp32 slice S[dk][16] stays
-// in MFMA accumulator registers for the whole sequence, and every product that
-// touches it runs on that wavefront alone.  All products are 16x16x32 MFMAs: the
+// Work mapping.  One workgroup per (sequence, value head, block of dv columns) walks
+// that sequence's chunks in order; a block is 64 columns (4 compute wavefronts), or on
+// the direct-load path 32 or 16 when 64-column blocks would leave CUs idle.  Wavefront w
+// owns state columns [16w, 16w+16) of the block: its fp32 slice S[dk][16] stays in MFMA
+// accumulator registers for the whole sequence, and every product that touches it runs
+// on that wavefront alone.  All products are 16x16x32 MFMAs: the
 // state's rows are kept in an order (state_row) in which two accumulator tiles
 // side by side are the B operand of K S and Q S, and T, P arrive from the record
 // as 16x32 operands over pairs of 16-token blocks whose contraction order matches
