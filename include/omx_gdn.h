@@ -200,6 +200,7 @@ size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_
  *   d_mixed_qkv    [B, T, conv_dim] bf16;  dz [B, T, Hv, dv] bf16;  da, db [B, T, Hv] bf16
  *   d_conv_w       [conv_dim, K] f32;  dA_log, d_dt_bias [Hv] f32;  d_norm_w [dv] f32
  *   d_initial_state [N, Hv, dk, dv] f32 or NULL
+ * mixed_qkv, d_mixed_qkv, z, d_out, dz and conv_w must be 16-byte aligned.
  * Compiled shapes: K = 4, dk 64/128, dv 64/128, Hv <= 256.
  */
 int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,

@@ -556,6 +556,8 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
           fn);
   REQUIRE(!mixed_qkv || (aligned(mixed_qkv, 16) && aligned(d_mixed_qkv, 16)),
           "%s: mixed_qkv and d_mixed_qkv must be 16-byte aligned", fn);
+  REQUIRE(!z || (aligned(z, 16) && aligned(d_out, 16) && aligned(dz, 16)),
+          "%s: z, d_out and dz must be 16-byte aligned", fn);
   REQUIRE(aligned(conv_w, 16), "%s: conv_w must be 16-byte aligned", fn);
   char* base = (char*)workspace;
   hipStream_t st = (hipStream_t)stream;

@@ -139,56 +139,59 @@ __global__ __launch_bounds__(NT) void gates_kernel(LayerBwdParams p) {
 
 // ---------------------------------------------------------------------------- gated RMSNorm
 
-// Persistent: each wavefront walks (token, value head) rows of dv <= 128 (lane: columns l and
-// l + 64).  n = o r, r = (mean(o^2) + eps)^-1/2, out = w n silu(z):
+// Persistent: each wavefront walks (token, value head) rows of dv <= 128 (lane l: columns
+// 2l and 2l + 1, so o and dO move 8 bytes and z, dout, dz 4 bytes per lane).
+// n = o r, r = (mean(o^2) + eps)^-1/2, out = w n silu(z):
 //   dn = dout w silu(z), dz = dout w n silu'(z), dw = sum dout n silu(z),
 //   do = r (dn - n mean(dn n)).
+// sigmoid(z) comes from the hardware exp2 and reciprocal (about 2 ulp in fp32).
 __global__ __launch_bounds__(NT) void norm_bwd_kernel(LayerBwdParams p) {
   __shared__ float sdw[NT / 64][128];
   const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int dv = p.dv;
+  const int dv = p.dv, c = 2 * l;
+  const bool in = c < dv;  // dv is even
   const long long rows = p.tokens * p.Hv;
   const long long nw = (long long)gridDim.x * (NT / 64);
   float w[2], dw[2] = {0.f, 0.f};
 #pragma unroll
-  for (int e = 0; e < 2; ++e) w[e] = l + 64 * e < dv ? p.norm_w[l + 64 * e] : 0.f;
+  for (int e = 0; e < 2; ++e) w[e] = in ? p.norm_w[c + e] : 0.f;
   for (long long r = (long long)blockIdx.x * (NT / 64) + wave; r < rows; r += nw) {
-    float o[2], z[2], go[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = l + 64 * e;
-      const bool in = c < dv;
-      o[e] = in ? p.o[r * dv + c] : 0.f;
-      z[e] = in ? bf2f(p.z[r * dv + c]) : 0.f;
-      go[e] = in ? bf2f(p.dout[r * dv + c]) : 0.f;
+    float o[2] = {0.f, 0.f}, z[2] = {0.f, 0.f}, go[2] = {0.f, 0.f};
+    if (in) {
+      const float2 ov = *(const float2*)(p.o + r * dv + c);
+      const uint32_t zv = *(const uint32_t*)(p.z + r * dv + c);
+      const uint32_t gv = *(const uint32_t*)(p.dout + r * dv + c);
+      o[0] = ov.x; o[1] = ov.y;
+      z[0] = __uint_as_float(zv << 16); z[1] = __uint_as_float(zv & 0xffff0000u);
+      go[0] = __uint_as_float(gv << 16); go[1] = __uint_as_float(gv & 0xffff0000u);
     }
     float ss = o[0] * o[0] + o[1] * o[1];
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) ss += __shfl_xor(ss, s);
     const float rr = rsqrtf(ss / (float)dv + p.eps);
-    float n[2], dn[2], dnn = 0.f;
+    float n[2], dn[2], dzv[2], dnn = 0.f;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       n[e] = o[e] * rr;
-      const float sz = siluf_(z[e]);
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z[e] * -1.4426950408889634f));
+      const float sz = z[e] * sg;                       // silu(z)
+      const float sgrad = sg * (1.0f + z[e] * (1.0f - sg));  // silu'(z)
       dn[e] = go[e] * w[e] * sz;
       dnn += dn[e] * n[e];
       dw[e] += go[e] * n[e] * sz;
-      const int c = l + 64 * e;
-      if (c < dv) p.dz[r * dv + c] = f2bf(go[e] * w[e] * n[e] * silu_grad(z[e]));
+      dzv[e] = go[e] * w[e] * n[e] * sgrad;
     }
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) dnn += __shfl_xor(dnn, s);
     const float m = dnn / (float)dv;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = l + 64 * e;
-      if (c < dv) p.dO[r * dv + c] = rr * (dn[e] - n[e] * m);
+    if (in) {
+      *(uint32_t*)(p.dz + r * dv + c) = pack_bf16(dzv[0], dzv[1]);
+      *(float2*)(p.dO + r * dv + c) = float2{rr * (dn[0] - n[0] * m), rr * (dn[1] - n[1] * m)};
     }
   }
 #pragma unroll
   for (int e = 0; e < 2; ++e)
-    if (l + 64 * e < dv) sdw[wave][l + 64 * e] = dw[e];
+    if (in) sdw[wave][c + e] = dw[e];
   __syncthreads();
   if (threadIdx.x < dv) {
     float s = 0.f;
