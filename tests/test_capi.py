@@ -184,3 +184,28 @@ def test_chunk_bwd_rejects_bad_arguments(over, code, msg):
     rc, err = _bwd(args.pop("ws"), args.pop("ws_bytes"), **args)
     assert rc == code
     assert msg in err
+
+
+def _prefill_bwd(**over):
+    L = _lib.lib()
+    need = L.omx_gdn_prefill_bwd_workspace_size(2, 100, 2, 4, 128, 128, 2)
+    a = dict(x=16, z=16, a=16, b=16, conv_w=16, A_log=16, dt_bias=16, norm_w=16, eps=1e-6, cu=None,
+             N=2, s0=None, d_out=16, dht=None, dx=16, dz=16, da=16, db=16, dw=16, dA=16, ddt=16,
+             dnw=16, dh0=None, B=2, T=100, Hk=2, Hv=4, dk=128, dv=128, K=4, C=64, ws=256,
+             ws_bytes=need, stream=None)
+    a.update(over)
+    rc = L.omx_gdn_prefill_bwd(*a.values())
+    return rc, L.omx_gdn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(ws_bytes=1024), _lib.EINVAL, "workspace"),
+    (dict(K=3), _lib.EINVAL, "conv kernel size must be 4"),
+    (dict(z=8), _lib.EINVAL, "16-byte aligned"),
+    (dict(d_out=24), _lib.EINVAL, "16-byte aligned"),
+    (dict(dz=None), _lib.EINVAL, "NULL"),
+])
+def test_prefill_bwd_rejects_bad_arguments(over, code, msg):
+    rc, err = _prefill_bwd(**over)
+    assert rc == code, err
+    assert msg in err
