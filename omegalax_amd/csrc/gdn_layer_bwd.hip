@@ -74,7 +74,8 @@ __device__ __forceinline__ float conv_u(const float* wt, float x0, float x1, flo
 
 // d silu(u) / du
 __device__ __forceinline__ float silu_grad(float u) {
-  const float s = 1.0f / (1.0f + __expf(-u));
+  // sigmoid from the hardware exp2 and reciprocal (about 2 ulp in fp32)
+  const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * -1.4426950408889634f));
   return s * (1.0f + u * (1.0f - s));
 }
 
