@@ -193,6 +193,15 @@ __device__ __forceinline__ float4 to_f4(u32x2 x) {
                 __uint_as_float(x[1] << 16), __uint_as_float(x[1] & 0xffff0000u)};
 }
 __device__ __forceinline__ void store4(bf16_t* dst, u32x2 x) { *(u32x2*)dst = x; }
+// 8 consecutive elements (16 bytes of bf16, or two 16-byte fp32 loads) as floats
+__device__ __forceinline__ void load8v(const bf16_t* p, float* x) {
+  const u32x4 w = *(const u32x4*)p;
+  unpack8<false>(&w, x);
+}
+__device__ __forceinline__ void load8v(const float* p, float* x) {
+  const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+  x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
 
 // Row sums of a C-layout tile (rows 16 bi + 4q + v, summed over its 16 columns) added
 // into arr[row] (lanes r == 0 write; one lane per row); column sums likewise.
@@ -996,47 +1005,50 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 
 // ============================================================================ q/k finalisation
 
-// dk / 4 consecutive threads per (token, key head) row of dq or dk, 4 elements each: the
+// dk / 8 consecutive threads per (token, key head) row of dq or dk, 8 elements each: the
 // sum over the key head's value heads, then (qk_l2norm) the L2-norm backward
 // dx = r (dy - y (y . dy)), y = x r, r = rsqrt(sum x^2 + 1e-6) (deltanet.py:30-32; the bf16
 // rounding of y is differentiated as the identity, as autodiff does for a dtype cast).
 template <bool F32>
 __global__ __launch_bounds__(NT) void qk_final_kernel(BwdParams p, long long rows) {
   using In = typename std::conditional<F32, float, bf16_t>::type;
-  const int dk = p.dk, tpr = dk / 4, gqa = p.Hv / p.Hk;
+  const int dk = p.dk, tpr = dk / 8, gqa = p.Hv / p.Hk;
   const long long gid = (long long)blockIdx.x * NT + threadIdx.x;
   const long long rid = gid / tpr;
-  const int c4 = 4 * (int)(gid % tpr);
+  const int c8 = 8 * (int)(gid % tpr);
   if (rid >= 2 * rows) return;  // whole rows drop out together (tpr divides 64)
   const int which = (int)(rid / rows);
   const long long row = rid % rows;
   const long long token = row / p.Hk;
   const int hk = (int)(row % p.Hk);
-  const In* src = (const In*)(which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk + c4;
-  float d[4] = {0.f, 0.f, 0.f, 0.f}, x[4];
+  const In* src = (const In*)(which ? p.dkh : p.dqh) + (token * p.Hv + (long long)hk * gqa) * dk + c8;
+  float d[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x[8];
   for (int g = 0; g < gqa; ++g) {
-    const float4 w = to_f4(*(const typename Vec4<In>::type*)(src + (long long)g * dk));
-    d[0] += w.x; d[1] += w.y; d[2] += w.z; d[3] += w.w;
-  }
-  const In* x_in = (const In*)(which ? p.k : p.q) + row * dk + c4;
+    float w[8];
+    load8v(src + (long long)g * dk, w);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = ldx(x_in + e);
+    for (int e = 0; e < 8; ++e) d[e] += w[e];
+  }
+  load8v((const In*)(which ? p.k : p.q) + row * dk + c8, x);
   if (p.qk_l2norm) {
-    float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
     for (int o = 1; o < tpr; o <<= 1) ss += __shfl_xor(ss, o);
     const float r = rsqrtf(ss + 1e-6f);
     float yd = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) yd += x[e] * r * d[e];
+    for (int e = 0; e < 8; ++e) yd += x[e] * r * d[e];
     for (int o = 1; o < tpr; o <<= 1) yd += __shfl_xor(yd, o);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) d[e] = r * (d[e] - x[e] * r * yd);
+    for (int e = 0; e < 8; ++e) d[e] = r * (d[e] - x[e] * r * yd);
   }
-  In* out = (In*)(which ? p.dk_out : p.dq) + row * dk + c4;
+  In* out = (In*)(which ? p.dk_out : p.dq) + row * dk + c8;
   if constexpr (F32) {
     *(float4*)out = float4{d[0], d[1], d[2], d[3]};
+    *(float4*)(out + 4) = float4{d[4], d[5], d[6], d[7]};
   } else {
-    *(u32x2*)out = u32x2{pack_bf16(d[0], d[1]), pack_bf16(d[2], d[3])};
+    *(u32x4*)out = pack8(d);
   }
 }
 
@@ -1057,7 +1069,7 @@ hipError_t launch_bwd_dk(const BwdParams& p, hipStream_t stream) {
   }
   const long long rows = (long long)p.T * (p.cu_seqlens ? 1 : p.N) * p.Hk;
   if (rows > 0) {
-    const long long threads = 2 * rows * (p.dk / 4);
+    const long long threads = 2 * rows * (p.dk / 8);
     const unsigned g2 = (unsigned)((threads + NT - 1) / NT);
     hipLaunchKernelGGL((qk_final_kernel<F32>), dim3(g2), dim3(NT), 0, stream, p, rows);
     e = hipGetLastError();
