@@ -402,10 +402,13 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
     const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
-    __syncthreads();  // the previous chunk's readers are done
+    // Barriers here order LDS accesses only (lds_barrier): the global stores go to later
+    // kernels and the prefetched rows are per-thread registers, so neither the prefetch
+    // nor the stores are waited for at a barrier.
+    lds_barrier();  // the previous chunk's readers are done
     store_chunk();
     if (j > 0) load_chunk(j - 1);  // lands while this chunk computes
-    __syncthreads();
+    lds_barrier();
     const float* sEG = sGate + kGateEG * C;
     const float* sEGS = sGate + kGateEGS * C;
     const float* sEL = sGate + kGateEL * C;  // e^{G_last - G}; e^{G_last} in the last slot
@@ -710,7 +713,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   // scheduler hoist the reads of several steps and run out of registers
 #pragma unroll 1
   for (int u = 0; u < DV / 32; ++u) {
-    __syncthreads();  // the previous step's readers are done
+    // (every barrier in this kernel orders LDS accesses only, as in the reverse scan)
+    lds_barrier();  // the previous step's readers are done
     store_rows();
     Op bs[NKB], bd[NKB];
 #pragma unroll
@@ -732,7 +736,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         pf_x[m] = load4(xb + kXlpgX + (it >> 4) * C + 4 * (it & 15), true);
       }
     }
-    __syncthreads();
+    lds_barrier();
     const Op ow = op_vec(sDOh, sDOl, LDR, 16 * bi, 0);  // dO and dV_new rows of block bi
     const Op vw = op_vec(sDVh, sDVl, LDR, 16 * bi, 0);
 #pragma unroll
@@ -754,7 +758,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       }
     }
   }
-  __syncthreads();  // every read of the staged slices is done: the region now holds X
+  lds_barrier();  // every read of the staged slices is done: the region now holds X
 #pragma unroll
   for (int m = 0; m < C * 16 / CNT; ++m) {
     const int it = tid + m * CNT;
@@ -799,7 +803,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   // sum of dS_end * S over the state (the e^{G_last} S term of the state update)
   sds = wave_sum(sds);
   if (l == 0) sRed[wave] = sds;
-  __syncthreads();
+  lds_barrier();
 
   // ---------------------------------------------------------------- dX = dU vb^T + dW kbe^T
   {
@@ -819,7 +823,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       put_ct(sDXh, sDXl, LDB, 16 * bi, 16 * bj, dx);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---------------------------------------------------------------- dvb = X^T dU, dkbe = X^T dW
 #pragma unroll
@@ -895,7 +899,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       put_ct(sMh, sMl, LDB, 16 * bi, 16 * bj, acc);
     }
   }
-  __syncthreads();  // M1 complete (a row block's two halves come from two wavefronts)
+  lds_barrier();  // M1 complete (a row block's two halves come from two wavefronts)
   // ---------------------------------------------------------------- dL = -strict_lower(M1 X^T)
   {
     f32x4 dl[2];
@@ -912,7 +916,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       }
       dl[jj] = acc;
     }
-    __syncthreads();  // every read of M1 is complete before its rows are overwritten
+    lds_barrier();  // every read of M1 is complete before its rows are overwritten
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
       const int bj = 2 * half + jj;
@@ -932,7 +936,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       add_cols(colG, bj, -ld);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---------------------------------------------------------------- (Qm + Qm^T) k, dPg^T qs, dPg k
 #pragma unroll
@@ -968,7 +972,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---------------------------------------------------------------- dG, dbeta, dg
   if (wave == 0) {
