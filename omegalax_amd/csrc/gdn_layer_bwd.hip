@@ -110,13 +110,22 @@ __global__ __launch_bounds__(NT) void conv_silu_split_kernel(LayerBwdParams p) {
     if (tb - d >= s0) load8(p.x + (tb - d) * p.conv_dim + c0, xs[d]);
     else zero8(xs[d]);
   }
-  for (long long t = tb; t < te; ++t) {
+  // every row of the block is loaded before the first store: one memory round trip per
+  // thread, and no load consumed after a store (the memory counter retires in order)
+  u32x4 raw[kConvFwdTB];
+#pragma unroll
+  for (int m = 0; m < kConvFwdTB; ++m)
+    raw[m] = tb + m < te ? *(const u32x4*)(p.x + (tb + m) * p.conv_dim + c0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int m = 0; m < kConvFwdTB; ++m) {
+    const long long t = tb + m;
+    if (t >= te) break;
     if (t >= s1) {  // a new sequence starts at t: no history
       token_seq(p.cu_seqlens, p.N, p.T, t, s0, s1);
 #pragma unroll
       for (int d = 1; d < 4; ++d) zero8(xs[d]);
     }
-    load8(p.x + t * p.conv_dim + c0, xs[0]);
+    unpack8<false>(&raw[m], xs[0]);
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
