@@ -183,3 +183,31 @@ def test_chunk_c4_full_size():
     o_ref, _ = run_ref(np_(q[:, :P, :1]), np_(k[:, :P, :1]), np_(v[:, :P, :4]),
                        np_(g[:, :P, :4]), np_(beta[:, :P, :4]), None, "bf16")
     assert rel(np_(o[:, :P, :4]), o_ref) < BF16_TOL
+
+
+def test_chunk_block_width_does_not_change_results():
+    """The scan's workgroups cover 16, 32 or 64 state columns depending on how many tiles
+    the call has (sequences x value heads x dv / 16 against the CU count); each compute
+    wavefront does the same arithmetic on its 16 columns either way.  The same sequences
+    run alone (16-column blocks), replicated 16 times (32-column blocks) and 32 times
+    (64-column blocks on a 256-CU part) give bit-identical outputs and final states."""
+    say("chunk block width invariance")
+    from omegalax_amd import chunk_gated_delta_rule
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    Hk, Hv, d, T = 1, 4, 128, 300
+    q = torch.randn((1, T, Hk, d), generator=gen, device="cuda").bfloat16()
+    k = torch.randn((1, T, Hk, d), generator=gen, device="cuda").bfloat16()
+    v = torch.randn((1, T, Hv, d), generator=gen, device="cuda").bfloat16()
+    g = torch.log(0.9 + 0.09 * torch.rand((1, T, Hv), generator=gen, device="cuda"))
+    beta = torch.sigmoid(torch.randn((1, T, Hv), generator=gen, device="cuda"))
+    S0 = 0.1 * torch.randn((1, Hv, d, d), generator=gen, device="cuda")
+    outs = []
+    for reps in (1, 16, 32):
+        rep = lambda t: t.expand(reps, *t.shape[1:]).contiguous()
+        o, S = chunk_gated_delta_rule(rep(q), rep(k), rep(v), rep(g), rep(beta), 64,
+                                      initial_state=rep(S0), output_final_state=True)
+        torch.cuda.synchronize()
+        outs.append((o[0].cpu(), S[0].cpu(), o[-1].cpu()))
+    for o, S, o_last in outs[1:]:
+        assert torch.equal(o, outs[0][0]) and torch.equal(S, outs[0][1])
+        assert torch.equal(o_last, outs[0][0])
