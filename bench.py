@@ -4,10 +4,15 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
-  prefill  config C1: GDN layer prefill from projection outputs (mixed_qkv, z, a, b)
-           to the gated-norm output, B=4 T=4096 Hk=16 Hv=32 d=128 (headline).
-           A "step" is one omx_gdn_prefill call over the whole batch.
-  decode   config C2: one cached decode step (conv cache + fp32 state in place), B=64.
+  prefill  (default, the headline) config C1: GDN layer prefill from the projection
+           outputs (mixed_qkv, z, a, b) to the gated-norm output, B=4 T=4096 Hk=16 Hv=32
+           d=128.  A "step" is one omx_gdn_prefill call over the whole batch.  The line
+           also carries C3, C4, the C2 decode step at B=64 and B=256, the backward passes
+           and the whole layer with its projections, each under its own key.
+  decode   config C2: one cached decode step (conv cache + fp32 state in place) at
+           --decode-batch, rotating through enough state sets that no step finds its state
+           in the 256 MB last-level cache.
+  c3       config C3: packed layer prefill, 8 sequences in T=32768 with initial states.
   core     one chunk_gated_delta_rule call at --batch/--seq-len/--k-heads/--v-heads
            (C1 by default; C4 is --batch 1 --seq-len 65536 --v-heads 64).
   bwd      one chunk_gated_delta_rule_bwd call (the VJP: forward recompute, reverse state-
@@ -17,13 +22,14 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
            a forward, and a training step (forward + gradients of every parameter and the
            input); the line's value is the training step's tokens/s.
   copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
-The headline line reports prefill tokens/s with the MFMA roofline of the chunked
-rule, timed at the core-function boundary (chunk_gated_delta_rule on the same
-shapes: the chunk-parallel preparation kernel and the state scan), and carries the
-decode step's HBM roofline as "decode", the rule's backward pass (VJP) at C1 as
-"backward", the layer's backward as "layer_backward" and the whole layer with its
-projections (forward and training step) as "layer_module".  Only one GPU is
-used: --gpus above 1 exits with a message.
+
+Every "roofline" object divides the algorithmic work of one timed call by that call's
+own HIP-event time: the headline's is the C1 layer step whose tokens/s is `value`; the
+core call's (the chunked rule alone: deltanet.py:53-153) is under "core".  "traffic" is
+the HBM bytes one call moves, read from rocprofv3 FETCH_SIZE/WRITE_SIZE counters in the
+run named by "traffic_source" (a profile constant: counters cannot be read inside this
+process); null where no such run exists.  Only one GPU is used: --gpus above 1 exits
+with a message.
 
 Kernel durations come from HIP events recorded on the stream the kernels run on
 (torch's current stream, which the library launches on).
@@ -98,30 +104,48 @@ def cpu_cores():
 
 # ----------------------------------------------------------------------------- decode (C2)
 
-def bench_decode(B, steps, warmup, cpu_baseline):
+def bench_decode(B, steps, warmup, cpu_baseline, min_rotation_bytes=512 << 20):
+    """One cached decode step per call, rotating through distinct (inputs, conv cache,
+    state) sets: at least 4 and at least ``min_rotation_bytes`` of state in total, so a
+    step never finds its state in the 256 MB Infinity Cache, as in a multi-layer decode
+    where each layer's state is read once per token."""
     import torch
     from omegalax_amd import gdn_decode_step, workloads as W
     Hk, Hv, d = 16, 32, 128
     _say(f"decode: B={B} generating inputs")
     arrs = W.decode_inputs(B)
-    t = W.to_device(arrs)
+    base = W.to_device(arrs)
+    state_bytes = base["state"].numel() * 4
+    n_sets = max(4, -(-min_rotation_bytes // state_bytes))
+    gen = torch.Generator(device="cuda").manual_seed(1002)
+    sets = [base]
+    for _ in range(n_sets - 1):
+        t = dict(base)
+        t["state"] = 0.02 * torch.randn(base["state"].shape, generator=gen, device="cuda")
+        for key in ("mixed_qkv", "z", "a", "b", "conv_state"):
+            t[key] = torch.randn(base[key].shape, generator=gen, device="cuda").bfloat16()
+        sets.append(t)
     dims = dict(num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+    it = [0]
 
     def step():
+        t = sets[it[0] % n_sets]
+        it[0] += 1
         gdn_decode_step(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
                         t["dt_bias"], t["norm_w"], t["conv_state"], t["state"], **dims)
 
-    _say(f"decode: B={B} timing {steps} steps")
+    _say(f"decode: B={B} timing {steps} steps over {n_sets} state sets "
+         f"({n_sets * state_bytes / 2**20:.0f} MiB)")
     wall, ms = time_launches(step, steps, warmup)
     nbytes = decode_bytes_per_seq(Hk, Hv, d, d) * B
     gbs = nbytes / (ms * 1e-3) / 1e9
+    traffic = MEASURED_TRAFFIC.get(("decode", B, Hk, Hv, d))
     res = {
         "batch": B, "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
-        "tokens_per_s": B * steps / wall,
+        "tokens_per_s": B * steps / wall, "state_sets": n_sets,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": gbs / PEAK_HBM_GBS,
-                     "traffic": MEASURED_TRAFFIC.get(("decode", B, Hk, Hv, d)),
-                     "algorithmic_bytes": nbytes},
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": traffic and traffic[0],
+                     "traffic_source": traffic and traffic[1], "algorithmic_bytes": nbytes},
     }
     if cpu_baseline:
         res["cpu_baseline"] = cpu_decode_baseline()
@@ -150,35 +174,38 @@ def cpu_decode_baseline(B=8, budget_s=10.0):
 # ----------------------------------------------------------------------------- core call
 
 # HBM bytes per call from two rocprofv3 --pmc runs (FETCH_SIZE x 2.0 and WRITE_SIZE x 1.0,
-# scaled by a plain copy kernel's counters), for the shapes they were taken on; summaries
-# and commands in profiles/prefill_c1.md and profiles/decode_step_c2_b64.md.
+# scaled by a plain copy kernel's counters), for the shapes they were taken on, with the
+# profiles/ summary that gives the commands and per-kernel figures.
 MEASURED_TRAFFIC = {
-    ("core", 4, 4096, 16, 32, 128): 1_154_719_808,  # prep 152.2 MiB + 284.7, scan 408.3 + 256.0
-    ("decode", 64, 16, 32, 128): 277_401_702,       # state read + written once
+    ("core", 4, 4096, 16, 32, 128): (1_154_719_808, "profiles/prefill_c1.md (core call)"),
+    ("decode", 64, 16, 32, 128): (277_401_702, "profiles/decode_step_c2_b64.md"),
+    # layer step: prep 303.3 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
+    ("prefill", 4, 4096, 16, 32, 128): (1_712_750_182, "profiles/prefill_c1.md (layer kernels)"),
 }
 
 
-def bench_core(B, T, Hk, Hv, d, steps, warmup, arrs=None):
+def bench_core(B, T, Hk, Hv, d, steps, warmup, arrs=None, long_memory=False):
     """One chunk_gated_delta_rule call (bf16 q/k/v, fp32 gates) over [B, T]: the
-    chunk-parallel preparation kernel and the state scan, HIP-event timed."""
+    chunk-parallel preparation kernel and the state scan, HIP-event timed.  Inputs are
+    drawn on the device (seeded); ``long_memory`` draws C4's gates, e^g ~ U(0.9, 0.9999)."""
     import torch
     from omegalax_amd import chunk_gated_delta_rule, workloads as W
-    rng = np.random.default_rng(7)
-
-    def act(*shape):
-        x = W.round_bf16(rng.standard_normal(shape, dtype=np.float32))
-        return torch.from_numpy(x).cuda().bfloat16()
-
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    act = lambda *shape: torch.randn(shape, generator=gen, device="cuda").bfloat16()
     q, k, v = act(B, T, Hk, d), act(B, T, Hk, d), act(B, T, Hv, d)
-    if arrs is None:
-        arrs = W.layer_inputs(B, T, Hk, Hv, d, d) if B * T <= 16384 else None
     if arrs is not None:
         g32, beta32 = W.gates_f32(arrs["a"], arrs["b"], arrs["A_log"], arrs["dt_bias"])
+        g = torch.from_numpy(g32).cuda()
+        beta = torch.from_numpy(beta32).cuda()
+    elif long_memory:
+        g = torch.log(0.9 + 0.0999 * torch.rand((B, T, Hv), generator=gen, device="cuda"))
+        beta = torch.sigmoid(torch.randn((B, T, Hv), generator=gen, device="cuda")).bfloat16().float()
     else:
-        g32 = -0.1 * rng.random((B, T, Hv), dtype=np.float32)
-        beta32 = rng.random((B, T, Hv), dtype=np.float32)
-    g = torch.from_numpy(g32).cuda()
-    beta = torch.from_numpy(beta32).cuda()
+        a = torch.randn((B, T, Hv), generator=gen, device="cuda")
+        A_log = torch.log(1 + 15 * torch.rand(Hv, generator=gen, device="cuda"))
+        dt = -2 * torch.rand(Hv, generator=gen, device="cuda")
+        g = -torch.exp(A_log) * torch.nn.functional.softplus(a + dt)
+        beta = torch.sigmoid(torch.randn((B, T, Hv), generator=gen, device="cuda")).bfloat16().float()
 
     def core():
         chunk_gated_delta_rule(q, k, v, g, beta, C)
@@ -187,13 +214,16 @@ def bench_core(B, T, Hk, Hv, d, steps, warmup, arrs=None):
     wall, ms = time_launches(core, steps, warmup)
     flops = prefill_flops_per_token_head(d, d) * B * T * Hv
     tf = flops / (ms * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get(("core", B, T, Hk, Hv, d))
     return {
+        "config": f"chunk_gated_delta_rule B={B} T={T} Hk={Hk} Hv={Hv} d={d}",
         "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+        "tokens_per_s": B * T * steps / wall,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
-                     "traffic": MEASURED_TRAFFIC.get(("core", B, T, Hk, Hv, d)),
+                     "traffic": traffic and traffic[0], "traffic_source": traffic and traffic[1],
                      "algorithmic_flops": flops,
-                     "kernels": "prep_kernel + scan_kernel (the two launches of one call)"},
+                     "kernels": "the launches of one chunk_gated_delta_rule call"},
     }
 
 
@@ -299,6 +329,10 @@ def bench_layer_module(steps, warmup, B=4, T=4096, D=2048):
 # ----------------------------------------------------------------------------- prefill (C1)
 
 def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
+    """C1: one gdn_prefill call (projection outputs -> gated-norm output) per step; the
+    roofline divides the step's algorithmic FLOPs (the chunked rule's matmuls, 94.49 GFLOP)
+    by the step's own HIP-event time.  The core call on the same shapes is timed after it
+    and reported under its own key."""
     import torch
     from omegalax_amd import gdn_prefill, workloads as W
     Hk, Hv, d = 16, 32, 128
@@ -314,36 +348,96 @@ def bench_prefill(steps, warmup, cpu_baseline, B=4, T=4096):
     _say(f"prefill: timing {steps} layer steps")
     wall, ms_step = time_launches(step, steps, warmup)
     tokens = B * T
-
-    # the dominant kernels, prep + scan, at the core-function boundary on the same shapes
-    core = bench_core(B, T, Hk, Hv, d, steps, warmup, arrs)
+    flops = prefill_flops_per_token_head(d, d) * tokens * Hv
+    tf = flops / (ms_step * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get(("prefill", B, T, Hk, Hv, d))
     res = {
         "tokens_per_s": tokens * steps / wall, "ms_per_step": wall / steps * 1e3,
-        "step_event_ms": ms_step, "core_kernel_ms": core["kernel_ms"],
-        "roofline": core["roofline"],
+        "step_event_ms": ms_step,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                     "traffic": traffic and traffic[0], "traffic_source": traffic and traffic[1],
+                     "algorithmic_flops": flops,
+                     "kernels": "the launches of one gdn_prefill call (the whole layer step)"},
+        "core": bench_core(B, T, Hk, Hv, d, steps, warmup, arrs),
     }
+    del t
     if cpu_baseline:
         res["cpu_baseline"] = cpu_prefill_baseline()
     return res
 
 
-def cpu_prefill_baseline(budget_s=15.0):
-    """Oracle layer prefill (numpy restatement, fp32 core like the reference) on a bounded
-    C1 sample: B=1, T=512, the C1 head layout; numpy's BLAS uses the visible cores."""
+def bench_c3(steps, warmup, total=32768, n=8):
+    """C3: packed layer prefill, ``n`` sequences (seeded Dirichlet lengths, minimum 256) in
+    one row of ``total`` tokens, each from its own initial state, final states returned.
+    Inputs are drawn on the device; cu_seqlens is a device tensor."""
+    import torch
+    from omegalax_amd import gdn_prefill, workloads as W
+    Hk, Hv, d = 16, 32, 128
+    lens = W.varlen_lengths(total, n)
+    cu = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)).cuda()
+    p = W.layer_params(np.random.default_rng(1010), Hk, Hv, d, d)
+    p = {k_: torch.from_numpy(v_).cuda() for k_, v_ in p.items()}
+    gen = torch.Generator(device="cuda").manual_seed(1003)
+    conv_dim = 2 * Hk * d + Hv * d
+    x = torch.randn((1, total, conv_dim), generator=gen, device="cuda").bfloat16()
+    z = torch.randn((1, total, Hv, d), generator=gen, device="cuda").bfloat16()
+    a = torch.randn((1, total, Hv), generator=gen, device="cuda").bfloat16()
+    b = torch.randn((1, total, Hv), generator=gen, device="cuda").bfloat16()
+    s0 = 0.02 * torch.randn((n, Hv, d, d), generator=gen, device="cuda")
+    dims = dict(num_k_heads=Hk, head_k_dim=d, num_v_heads=Hv, head_v_dim=d)
+
+    def step():
+        gdn_prefill(x, z, a, b, p["conv_w"], p["A_log"], p["dt_bias"], p["norm_w"],
+                    cu_seqlens=cu, initial_state=s0, output_final_state=True, **dims)
+
+    _say(f"c3: T={total} in {n} packed sequences (longest {int(lens.max())}), timing {steps} steps")
+    wall, ms = time_launches(step, steps, warmup)
+    flops = prefill_flops_per_token_head(d, d) * total * Hv
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"config": f"C3 packed layer prefill T={total}, {n} sequences "
+                      f"(lengths {lens.tolist()}), initial states, Hk=16 Hv=32 d=128",
+            "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
+            "tokens_per_s": total * steps / wall,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
+                         "algorithmic_flops": flops,
+                         "kernels": "the launches of one gdn_prefill call"}}
+
+
+def cpu_prefill_baseline(T=4096, budget_s=20.0):
+    """Oracle layer prefill (numpy restatement, fp32 core like the reference; numpy's BLAS
+    uses the visible cores) on a bounded C1 sample: one of C1's four sequences, B=1 T=4096
+    in the C1 head layout.  C1's sequences are independent, so C1 takes four times the
+    sample's time on this path: the tokens/s rate is the same."""
     from oracle import gdn_oracle as O
     from omegalax_amd import workloads as W
-    B, T = 1, 512
+    B = 1
     d = W.layer_inputs(B, T)
     n = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or n == 0:
+    while True:  # whole runs only, while the next one still fits the budget
         O.gdn_prefill_layer(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"], d["A_log"],
                             d["dt_bias"], d["norm_w"], Hk=16, dk=128, Hv=32, dv=128,
                             dtype=np.float32)
         n += 1
-    el = time.perf_counter() - t0
+        el = time.perf_counter() - t0
+        if el * (n + 1) / n > budget_s:
+            break
     return {"value": B * T * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
-            "sample": f"{n} runs of the numpy fp32 layer prefill restatement, B={B} T={T}, C1 head layout"}
+            "sample": f"{n} run(s) of the numpy fp32 layer prefill restatement on one C1 "
+                      f"sequence (B=1 T={T}, Hk=16 Hv=32 d=128); C1 (4 such sequences) "
+                      f"extrapolates to {4 * el / n:.1f} s at the same tokens/s"}
+
+
+def _line(metric, value, unit, steps, warmup, ms, dtype, config, **extra):
+    line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype,
+            "data": "synthetic (seeded N(0,1) activations, random-init params)",
+            "config": config}
+    line.update(extra)
+    return json.dumps(line)
 
 
 def main():
@@ -351,7 +445,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode", "core", "bwd", "layer_bwd",
+    ap.add_argument("--workload", choices=["prefill", "decode", "c3", "core", "bwd", "layer_bwd",
                                            "layer_module", "copy"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
@@ -359,6 +453,8 @@ def main():
     ap.add_argument("--seq-len", type=int, default=4096, help="core workload: tokens each")
     ap.add_argument("--k-heads", type=int, default=16, help="core workload")
     ap.add_argument("--v-heads", type=int, default=32, help="core workload")
+    ap.add_argument("--long-memory", action="store_true",
+                    help="core workload: C4's gates, e^g ~ U(0.9, 0.9999)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -371,108 +467,86 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     cpu = not args.no_cpu_baseline
+    K, W_ = args.steps, args.warmup
     if args.workload == "copy":
         # calibration of the FETCH_SIZE / WRITE_SIZE counters: a plain 256 MiB device copy
         src = torch.empty(1 << 26, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
-        wall, ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup)
+        wall, ms = time_launches(lambda: dst.copy_(src), K, W_)
         gbs = 2 * src.numel() * 4 / (ms * 1e-3) / 1e9
-        print(json.dumps({"metric": "device copy GB/s (counter calibration)", "value": gbs,
-                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-                          "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
-                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-                          "dtype": "f32", "data": "synthetic",
-                          "config": {"workload": "256 MiB read + 256 MiB written"}}), flush=True)
+        print(_line("device copy GB/s (counter calibration)", gbs, "GB/s", K, W_,
+                    wall / K * 1e3, "f32", {"workload": "256 MiB read + 256 MiB written"}),
+              flush=True)
         return 0
     if args.workload == "layer_module":
-        res = bench_layer_module(args.steps, args.warmup)
-        line = {
-            "metric": "GatedDeltaNet training-step tokens/s (projections included, config C1)",
-            "value": res["train_tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
-            "steps": max(args.steps // 2, 5), "warmup": args.warmup,
-            "ms_per_step": res["train_step_ms"], "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded N(0,1) hidden states and output cotangent, random-init params)",
-            "config": {"workload": res["config"]}, "layer_module": res,
-        }
-        print(json.dumps(line), flush=True)
+        res = bench_layer_module(K, W_)
+        n_t = max(K // 2, 5)
+        print(_line("GatedDeltaNet training-step tokens/s (projections included, config C1)",
+                    res["train_tokens_per_s"], "tokens/s", n_t, W_, res["train_step_ms"],
+                    "bf16", {"workload": res["config"]}, layer_module=res), flush=True)
         return 0
     if args.workload == "layer_bwd":
-        res = bench_layer_bwd(args.steps, args.warmup)
-        line = {
-            "metric": "gdn_prefill_bwd tokens/s (GDN layer backward, config C1)",
-            "value": res["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded N(0,1) activations and cotangent, random-init params)",
-            "config": {"workload": "C1 GDN layer backward B=4 T=4096 Hk=16 Hv=32 d=128"},
-            "kernel_ms": res["kernel_ms"],
-        }
-        print(json.dumps(line), flush=True)
+        res = bench_layer_bwd(K, W_)
+        print(_line("gdn_prefill_bwd tokens/s (GDN layer backward, config C1)",
+                    res["tokens_per_s"], "tokens/s", K, W_, res["ms_per_step"], "bf16",
+                    {"workload": "C1 GDN layer backward B=4 T=4096 Hk=16 Hv=32 d=128"},
+                    kernel_ms=res["kernel_ms"]), flush=True)
         return 0
     if args.workload == "bwd":
         B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads
-        res = bench_bwd(B, T, Hk, Hv, 128, args.steps, args.warmup)
-        line = {
-            "metric": "chunk_gated_delta_rule_bwd TFLOP/s (bf16 MFMA roofline)",
-            "value": res["roofline"]["achieved"], "unit": "TFLOP/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded N(0,1) activations and cotangents, random-init gates)",
-            "config": {"workload": f"chunk_gated_delta_rule_bwd B={B} T={T} Hk={Hk} Hv={Hv} d=128",
-                       "chunk": C},
-            "roofline": res["roofline"], "kernel_ms": res["kernel_ms"],
-        }
-        print(json.dumps(line), flush=True)
+        res = bench_bwd(B, T, Hk, Hv, 128, K, W_)
+        print(_line("chunk_gated_delta_rule_bwd TFLOP/s (bf16 MFMA roofline)",
+                    res["roofline"]["achieved"], "TFLOP/s", K, W_, res["ms_per_step"], "bf16",
+                    {"workload": f"chunk_gated_delta_rule_bwd B={B} T={T} Hk={Hk} Hv={Hv} d=128",
+                     "chunk": C}, roofline=res["roofline"], kernel_ms=res["kernel_ms"]),
+              flush=True)
         return 0
     if args.workload == "core":
         B, T, Hk, Hv = args.batch, args.seq_len, args.k_heads, args.v_heads
-        core = bench_core(B, T, Hk, Hv, 128, args.steps, args.warmup)
-        line = {
-            "metric": "chunk_gated_delta_rule TFLOP/s (bf16 MFMA roofline)",
-            "value": core["roofline"]["achieved"], "unit": "TFLOP/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": core["ms_per_step"],
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-            "data": "synthetic (seeded N(0,1) activations, random-init params)",
-            "config": {"workload": f"chunk_gated_delta_rule B={B} T={T} Hk={Hk} Hv={Hv} d=128",
-                       "chunk": C},
-            "roofline": core["roofline"], "kernel_ms": core["kernel_ms"],
-        }
-        print(json.dumps(line), flush=True)
+        core = bench_core(B, T, Hk, Hv, 128, K, W_, long_memory=args.long_memory)
+        print(_line("chunk_gated_delta_rule TFLOP/s (bf16 MFMA roofline)",
+                    core["roofline"]["achieved"], "TFLOP/s", K, W_, core["ms_per_step"], "bf16",
+                    {"workload": core["config"], "chunk": C}, roofline=core["roofline"],
+                    kernel_ms=core["kernel_ms"]), flush=True)
+        return 0
+    if args.workload == "c3":
+        res = bench_c3(K, W_)
+        print(_line("C3 packed GDN layer prefill tokens/s", res["tokens_per_s"], "tokens/s", K,
+                    W_, res["ms_per_step"], "bf16", {"workload": res["config"]},
+                    roofline=res["roofline"], kernel_ms=res["kernel_ms"]), flush=True)
         return 0
     if args.workload == "decode":
-        dec = bench_decode(args.decode_batch, args.steps, args.warmup, cpu)
-        line = {
-            "metric": "decode-step HBM GB/s (GDN decode, config C2)",
-            "value": dec["roofline"]["achieved"], "unit": "GB/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": dec["ms_per_step"],
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-            "data": "synthetic (seeded N(0,1) activations, random-init params)",
-            "config": {"workload": f"C2 decode step B={args.decode_batch} Hk=16 Hv=32 d=128"},
-            "roofline": dec["roofline"], "decode": dec,
-        }
+        dec = bench_decode(args.decode_batch, K, W_, cpu)
+        extra = {"roofline": dec["roofline"], "decode": dec}
         if cpu:
-            line["cpu_baseline"] = dec.pop("cpu_baseline")
-        print(json.dumps(line), flush=True)
+            extra["cpu_baseline"] = dec.pop("cpu_baseline")
+        print(_line("decode-step HBM GB/s (GDN decode, config C2)", dec["roofline"]["achieved"],
+                    "GB/s", K, W_, dec["ms_per_step"], "f32",
+                    {"workload": f"C2 decode step B={args.decode_batch} Hk=16 Hv=32 d=128"},
+                    **extra), flush=True)
         return 0
-    pre = bench_prefill(args.steps, args.warmup, cpu)
-    dec = bench_decode(args.decode_batch, max(args.steps, 20), args.warmup, False)
-    bwd = bench_bwd(4, 4096, 16, 32, 128, max(args.steps // 2, 5), args.warmup)
-    lbwd = bench_layer_bwd(max(args.steps // 2, 5), args.warmup)
-    mod = bench_layer_module(args.steps, args.warmup)
-    line = {
-        "metric": "GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
-        "value": pre["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": pre["ms_per_step"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) activations, random-init params)",
-        "config": {"workload": "C1 GDN layer prefill (projection outputs -> gated-norm output)",
-                   "batch": 4, "seq_len": 4096, "k_heads": 16, "v_heads": 32, "head_dim": 128,
-                   "chunk": 64},
+    # the headline: C1 layer prefill, with every other config under its own key
+    pre = bench_prefill(K, W_, cpu)
+    c3 = bench_c3(max(K // 2, 5), W_)
+    c4 = bench_core(1, 65536, 16, 64, 128, max(K // 4, 3), min(W_, 2), long_memory=True)
+    dec64 = bench_decode(64, max(K, 20), W_, False)
+    dec256 = bench_decode(256, max(K, 20), W_, False)
+    bwd = bench_bwd(4, 4096, 16, 32, 128, max(K // 2, 5), W_)
+    lbwd = bench_layer_bwd(max(K // 2, 5), W_)
+    mod = bench_layer_module(K, W_)
+    dec = lambda r: {"config": f"C2 B={r['batch']} (state rotated over {r['state_sets']} sets)",
+                     "roofline": r["roofline"], "kernel_ms": r["kernel_ms"],
+                     "tokens_per_s": r["tokens_per_s"]}
+    extra = {
         "roofline": pre["roofline"],
-        "decode": {"config": f"C2 B={args.decode_batch}", "roofline": dec["roofline"],
-                   "kernel_ms": dec["kernel_ms"], "tokens_per_s": dec["tokens_per_s"]},
-        "prefill_detail": {k_: pre[k_] for k_ in ("step_event_ms", "core_kernel_ms")},
+        "core": {k_: pre["core"][k_] for k_ in ("config", "kernel_ms", "roofline")},
+        "prefill_detail": {"step_event_ms": pre["step_event_ms"]},
+        "c3": c3,
+        "c4": {"config": "C4 core call B=1 T=65536 Hk=16 Hv=64 d=128, e^g ~ U(0.9, 0.9999)",
+               "kernel_ms": c4["kernel_ms"], "tokens_per_s": c4["tokens_per_s"],
+               "roofline": c4["roofline"]},
+        "decode": dec(dec64),
+        "decode_b256": dec(dec256),
         "backward": {"config": "chunk_gated_delta_rule_bwd at C1 (B=4 T=4096 Hk=16 Hv=32 d=128)",
                      "kernel_ms": bwd["kernel_ms"], "roofline": bwd["roofline"]},
         "layer_backward": {"config": "gdn_prefill_bwd at C1", "kernel_ms": lbwd["kernel_ms"],
@@ -480,8 +554,12 @@ def main():
         "layer_module": mod,
     }
     if cpu:
-        line["cpu_baseline"] = pre["cpu_baseline"]
-    print(json.dumps(line), flush=True)
+        extra["cpu_baseline"] = pre["cpu_baseline"]
+    print(_line("GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
+                pre["tokens_per_s"], "tokens/s", K, W_, pre["ms_per_step"], "bf16",
+                {"workload": "C1 GDN layer prefill (projection outputs -> gated-norm output)",
+                 "batch": 4, "seq_len": 4096, "k_heads": 16, "v_heads": 32, "head_dim": 128,
+                 "chunk": 64}, **extra), flush=True)
     return 0
 
 

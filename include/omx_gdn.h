@@ -10,9 +10,12 @@
  * query).  Buffers are dense, row-major, in the layouts given per argument.
  *
  * Return value: OMX_GDN_OK (0) or a negative code; omx_gdn_last_error() then
- * returns a message for the calling thread.  Arguments are validated on the
- * host before any HIP call, so a bad call returns OMX_GDN_EINVAL without
- * touching the GPU.
+ * returns a message for the calling thread.  Scalar arguments, pointers and
+ * alignments are validated on the host before any HIP call, so a bad call returns
+ * OMX_GDN_EINVAL without touching the GPU.  The contents of device arrays are not
+ * read on the host (that would need a device-to-host copy and a synchronisation):
+ * their preconditions are stated per argument, together with what the kernels do
+ * when one is violated.
  *
  * dtype codes: OMX_GDN_F32 (float32) or OMX_GDN_BF16 (bfloat16 as uint16 bits).
  * Shapes: B batch, T tokens, Hk key heads, Hv value heads (Hv % Hk == 0; value
@@ -61,6 +64,12 @@ int omx_gdn_abi_version(void);
  *                sequence n spans tokens [cu[n], cu[n+1]); each sequence starts from
  *                its own initial state and chunks restart at its first token.
  *                Without it N = B.
+ *                Precondition: 0 = cu[0] <= cu[1] <= ... <= cu[N] = T.  The kernels
+ *                read the offsets as c[0] = 0, c[N] = T and c[n] = max(c[n-1],
+ *                clamp(cu[n], 0, T)) in between (equal to cu when it is valid), so
+ *                whatever the array holds the sequences are ordered, disjoint and
+ *                cover every token: no output row is left unwritten, no two
+ *                workgroups write one row, and no reduction reads an unwritten row.
  *   o            [B, T, Hv, dv] f32 (the reference returns fp32, deltanet.py:153)
  *   final_state  [N, Hv, dk, dv] f32 or NULL (the reference discards it, :146)
  *   chunk_size   must be 64.

@@ -6,8 +6,15 @@ import numpy as np
 
 def round_bf16(x):
     """Round to the nearest bfloat16 (ties to even); returns float32 holding bf16 values."""
-    a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = a.view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
-    out = u.astype(np.uint32).view(np.float32)
-    return np.where(np.isnan(a), a, out).astype(np.float32)
+    a = np.array(x, dtype=np.float32, copy=True, order="C")
+    u = a.view(np.uint32)
+    nan = np.isnan(a)
+    # uint32 arithmetic: a finite value's sum cannot wrap (it rounds up to inf at most);
+    # NaNs, whose sum may wrap, are restored below
+    r = (u >> 16) & 1
+    r += 0x7FFF
+    u += r
+    u &= 0xFFFF0000
+    if nan.any():
+        a[nan] = np.nan
+    return a

@@ -53,9 +53,10 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // the preparation kernel (one per chunk slot and value head; a sequence adds at
 // most one partial chunk, so ceil(tokens/64) + N slots cover any packing), the
 // normalised k and q, (layer) the conv output of v, the bf16 o and the partial
-// sums of o^2 for the gated norm, and the chunk offsets of packed sequences.
+// sums of o^2 for the gated norm, and the plan of packed sequences (chunk offsets and
+// the ordered copy of cu_seqlens the kernels read).
 struct ChunkWs {
-  size_t rec, kn, qn, vc, opart, off, total;
+  size_t rec, kn, qn, vc, opart, off, cu, total;
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
@@ -79,6 +80,8 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
   }
   w.off = o;
+  o += align_up((size_t)(N + 1) * 4, 256);
+  w.cu = o;
   o += align_up((size_t)(N + 1) * 4, 256);
   w.total = o;
   return w;
@@ -206,6 +209,9 @@ void setup_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int 
   p.n_rec = p.cu_seqlens ? (int)((p.T + 63) / 64 + p.N) : p.N * p.nch;
   p.rec = (unsigned char*)(base + ws.rec);
   p.chunk_off = p.cu_seqlens ? (int32_t*)(base + ws.off) : nullptr;
+  // the kernels after the plan read its ordered copy of the offsets
+  p.cu_in = p.cu_seqlens;
+  if (p.cu_seqlens) p.cu_seqlens = (const int32_t*)(base + ws.cu);
   const bool norm = p.qk_l2norm || mode == omx::kModeLayer;
   p.kn = norm ? base + ws.kn : nullptr;
   p.qn = norm ? base + ws.qn : nullptr;
@@ -452,7 +458,7 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
   b.dkh = base + ws.dkh;
   b.dv = dv; b.dg = dg; b.dbeta = dbeta;
   b.q = q; b.k = k; b.dq = dq; b.dk_out = dk;
-  b.cu_seqlens = cu_seqlens; b.chunk_off = p.chunk_off;
+  b.cu_seqlens = p.cu_seqlens; b.chunk_off = p.chunk_off;
   b.N = p.N; b.T = p.T; b.Hk = p.Hk; b.Hv = p.Hv; b.dk = p.dk; b.DV = p.DV; b.nb = p.nb;
   b.nch = p.nch; b.n_rec = p.n_rec; b.in_f32 = f32 ? 1 : 0; b.qk_l2norm = p.qk_l2norm;
   b.scale = scale;
@@ -575,12 +581,9 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   lp.part_conv = (float*)(base + ws.pc);
   lp.dx = (uint16_t*)d_mixed_qkv; lp.dz = (uint16_t*)dz; lp.da = (uint16_t*)da;
   lp.db = (uint16_t*)db; lp.d_conv_w = d_conv_w; lp.dA_log = dA_log; lp.d_dt_bias = d_dt_bias;
-  lp.d_norm_w = d_norm_w; lp.cu_seqlens = cu_seqlens; lp.tokens = tokens;
+  lp.d_norm_w = d_norm_w; lp.tokens = tokens;
   lp.N = (int)N; lp.T = (int)T; lp.Hk = (int)Hk; lp.Hv = (int)Hv; lp.dk = (int)dk; lp.dv = (int)dv;
   lp.conv_dim = (int)(2 * Hk * dk + Hv * dv);
-  // forward recompute: conv + SiLU, gates, then the rule's prep and scan (keeping o)
-  hipError_t e = omx::launch_layer_fwd_pieces(lp, st);
-  if (e != hipSuccess) return launch_status(e, fn);
   omx::ChunkParams p{};
   p.q = lp.q; p.k = lp.k; p.v = lp.v;
   p.q_ld = Hk * dk; p.k_ld = Hk * dk; p.v_ld = Hv * dv;
@@ -595,7 +598,12 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   p.xlpg = (float*)(base + ws.c.xlpg);
   p.states = (float*)(base + ws.c.states);
   p.vnew = (float*)(base + ws.c.vnew);
+  // the packed-sequence plan first: every kernel below reads its ordered offsets
+  lp.cu_seqlens = p.cu_seqlens;
+  hipError_t e = hipSuccess;
   if (p.cu_seqlens) e = omx::launch_chunk_plan(p, st);
+  // forward recompute: conv + SiLU, gates, then the rule's prep and scan (keeping o)
+  if (e == hipSuccess) e = omx::launch_layer_fwd_pieces(lp, st);
   if (e == hipSuccess) e = omx::launch_prep_bwd(p, omx::kModeBF16, st);
   if (e == hipSuccess) e = omx::launch_scan_bwd(p, omx::kModeBF16, st);
   // the gated norm's adjoint gives the rule's cotangent
@@ -612,7 +620,7 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   bp.dkh = base + ws.c.dkh;
   bp.dv = lp.grad_v; bp.dg = (float*)(base + ws.dg); bp.dbeta = (float*)(base + ws.dbeta);
   bp.q = lp.q; bp.k = lp.k; bp.dq = lp.grad_q; bp.dk_out = lp.grad_k;
-  bp.cu_seqlens = cu_seqlens; bp.chunk_off = p.chunk_off;
+  bp.cu_seqlens = p.cu_seqlens; bp.chunk_off = p.chunk_off;
   bp.N = p.N; bp.T = p.T; bp.Hk = p.Hk; bp.Hv = p.Hv; bp.dk = p.dk; bp.DV = p.DV; bp.nb = p.nb;
   bp.nch = p.nch; bp.n_rec = p.n_rec; bp.in_f32 = 0; bp.qk_l2norm = 1; bp.scale = p.scale;
   e = omx::launch_bwd(bp, st);

@@ -61,7 +61,9 @@ struct ChunkParams {
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
-  const int32_t* cu_seqlens;   // [N+1] or null (then sequence n = batch row n of length T)
+  const int32_t* cu_seqlens;   // [N+1] or null (then sequence n = batch row n of length T):
+                               // the plan's ordered copy (workspace) once set up
+  const int32_t* cu_in;        // the caller's cu_seqlens, read only by the plan kernel
   int N, T, Hk, Hv, dk, DV, nb, conv_k, conv_dim;
   float scale, eps;
   int qk_l2norm;
@@ -127,7 +129,8 @@ int chunk_block_cols();
 bool layer_dims_supported(int dk, int dv);
 // bytes of one (chunk, value head) record for a mode
 int chunk_record_bytes(int mode);
-// cu_seqlens -> chunk_off (one workgroup); then the preparation kernel and the scan
+// cu_in -> the ordered offsets cu_seqlens and chunk_off (one workgroup); then the
+// preparation kernel and the scan
 hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);
 hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream);
 hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream);

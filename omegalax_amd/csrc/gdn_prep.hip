@@ -722,22 +722,45 @@ hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// chunk_off[n] = sum over m < n of ceil(len_m / 64), chunk_off[N] = the total, with
-// each length taken from the clamped range seq_range gives.  One workgroup.
+// The packed-sequence plan, one workgroup:
+//  * cu_out, the offsets every later kernel reads: c[0] = 0, c[N] = T and, between,
+//    c[n] = max(c[n-1], clamp(cu[n], 0, T)) (a running maximum), so the sequences are
+//    ordered, disjoint and tile [0, T) whatever the caller's array holds.  For valid
+//    offsets (0 = cu[0] <= ... <= cu[N] = T) c equals cu;
+//  * off[n] = sum over m < n of ceil(len_m / 64), off[N] = the total chunk count.
 __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* cu, int N, int T,
-                                                          int32_t* off) {
+                                                          int32_t* cu_out, int32_t* off) {
+  __shared__ int wmax[16];
   __shared__ int wsum[16];
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
-  int carry = 0;
+  auto clamped = [&](int n) {
+    if (n == 0) return 0;
+    if (n >= N) return T;
+    const int x = cu[n];
+    return x < 0 ? 0 : (x > T ? T : x);
+  };
+  int carry_max = 0, carry = 0;
   for (int base = 0; base < N; base += 1024) {
     const int n = base + tid;
+    int m = n < N ? clamped(n) : 0;  // inclusive running maximum within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(m, o, 64);
+      if (l >= o) m = m > y ? m : y;
+    }
+    if (l == 63) wmax[w] = m;
+    __syncthreads();
+    int mb = carry_max;
+    for (int v = 0; v < w; ++v) mb = mb > wmax[v] ? mb : wmax[v];
+    const int c0 = m > mb ? m : mb;  // c[n]
     int cnt = 0;
     if (n < N) {
-      long long s0, s1;
-      seq_range(cu, n, T, s0, s1);
-      cnt = (int)((s1 - s0 + C - 1) / C);
+      const int x1 = clamped(n + 1);
+      const int c1 = x1 > c0 ? x1 : c0;  // c[n + 1]
+      cu_out[n] = c0;
+      cnt = (c1 - c0 + C - 1) / C;
     }
-    int x = cnt;  // inclusive scan within the wave
+    int x = cnt;  // inclusive scan of the chunk counts within the wave
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(x, o, 64);
@@ -748,19 +771,26 @@ __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* cu, int
     int before = carry;
     for (int v = 0; v < w; ++v) before += wsum[v];
     if (n < N) off[n] = before + x - cnt;
-    int total = 0;
-    for (int v = 0; v < 16; ++v) total += wsum[v];
+    int total = 0, bmax = carry_max;
+    for (int v = 0; v < 16; ++v) {
+      total += wsum[v];
+      bmax = bmax > wmax[v] ? bmax : wmax[v];
+    }
     carry += total;
+    carry_max = bmax;
     __syncthreads();
   }
-  if (tid == 0) off[N] = carry;
+  if (tid == 0) {
+    off[N] = carry;
+    cu_out[N] = T;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p.cu_seqlens, p.N, p.T,
-                     p.chunk_off);
+  hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p.cu_in, p.N, p.T,
+                     const_cast<int32_t*>(p.cu_seqlens), p.chunk_off);
   return hipGetLastError();
 }
 

@@ -61,19 +61,29 @@ def _f32(t):
     return None if t is None else t.to(torch.float32).contiguous()
 
 
-def _check_cu_seqlens(cu, B, T):
-    """Validate packed-sequence offsets (int32 [N+1], 0 = cu[0] <= ... <= cu[N] = T, B == 1).
+def _cu_seqlens(cu, B, T, dev):
+    """Packed-sequence offsets for the kernels: int32 [N+1] with B == 1.
 
-    One small device-to-host copy; the kernels also clamp offsets to [0, T].
+    Valid offsets rise monotonically from cu[0] = 0 to cu[N] = T.  A device tensor is
+    passed through without reading it on the host (no device-to-host copy, so the call
+    can be captured into a HIP graph); the kernels read the offsets as their running
+    maximum clamped to [0, T], with the first forced to 0 and the last to T, so every
+    token belongs to exactly one sequence whatever the array holds.  A CPU tensor is
+    checked on the host (ValueError when invalid) and copied to the device.
+    Returns (offsets on ``dev``, N).
     """
     if cu.dtype != torch.int32 or cu.dim() != 1 or cu.numel() < 2:
         raise ValueError("cu_seqlens must be a 1-D int32 tensor with at least 2 entries")
     if B != 1:
         raise ValueError(f"cu_seqlens requires batch size 1, got {B}")
-    h = cu.detach().to("cpu")
+    if cu.is_cuda:
+        if cu.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {cu.device}")
+        return cu.contiguous(), cu.numel() - 1
+    h = cu
     if int(h[0]) != 0 or int(h[-1]) != T or bool((h[1:] < h[:-1]).any()):
         raise ValueError(f"cu_seqlens must rise monotonically from 0 to T={T}: {h.tolist()[:16]}")
-    return cu.numel() - 1
+    return cu.to(dev), cu.numel() - 1
 
 
 def _workspace(nbytes, device):
@@ -87,23 +97,25 @@ def _prep_inputs(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seql
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError("q, k, v must share a dtype")
     g, beta = _f32(g_BTH), _f32(beta_BTH)
-    dev = _dev(q, k, v, g, beta, initial_state, cu_seqlens)
+    dev = _dev(q, k, v, g, beta, initial_state)
     B, T, Hk, A = q.shape
     H, U = v.shape[2], v.shape[3]
     if k.shape != q.shape or v.shape[:2] != (B, T) or g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
                          f"g{tuple(g.shape)} beta{tuple(beta.shape)}")
-    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
+    N = B
+    if cu_seqlens is not None:
+        cu_seqlens, N = _cu_seqlens(cu_seqlens, B, T, dev)
     if initial_state is not None:
         initial_state = _f32(initial_state)
         if tuple(initial_state.shape) != (N, H, A, U):
             raise ValueError(f"initial_state must be {(N, H, A, U)}, got {tuple(initial_state.shape)}")
-    return q, k, v, g, beta, initial_state, dev, (B, T, Hk, A, H, U, N)
+    return q, k, v, g, beta, initial_state, cu_seqlens, dev, (B, T, Hk, A, H, U, N)
 
 
 def _chunk_fwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, chunk_size, initial_state,
                output_final_state, cu_seqlens, scale, use_qk_l2norm):
-    q, k, v, g, beta, initial_state, dev, dims = _prep_inputs(
+    q, k, v, g, beta, initial_state, cu_seqlens, dev, dims = _prep_inputs(
         q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seqlens)
     B, T, Hk, A, H, U, N = dims
     o = torch.empty((B, T, H, U), dtype=torch.float32, device=dev)
@@ -130,7 +142,7 @@ def chunk_gated_delta_rule_bwd(q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, do_BTHU,
     and summed over each key head's value heads), dg/dbeta [B,T,H] fp32,
     d_initial_state [N,H,A,U] fp32.
     """
-    q, k, v, g, beta, initial_state, dev, dims = _prep_inputs(
+    q, k, v, g, beta, initial_state, cu_seqlens, dev, dims = _prep_inputs(
         q_BTHA, k_BTHA, v_BTHU, g_BTH, beta_BTH, initial_state, cu_seqlens)
     B, T, Hk, A, H, U, N = dims
     do = _f32(do_BTHU)
@@ -247,7 +259,7 @@ def _gdn_prefill_fwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_
     z = z.contiguous()
     a, b = a.contiguous(), b.contiguous()
     conv_w, A_log, dt_bias, norm_w = (_f32(t) for t in (conv_w, A_log, dt_bias, norm_w))
-    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, cu_seqlens, initial_state, conv_state)
+    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state, conv_state)
     for name, t in (("mixed_qkv", x), ("z", z), ("a", a), ("b", b)):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{name} must be bf16")
@@ -257,7 +269,9 @@ def _gdn_prefill_fwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_
         raise ValueError("mixed_qkv / conv_w channel count does not match the head layout")
     if z.numel() != B * T * Hv * dv or a.shape != (B, T, Hv) or b.shape != (B, T, Hv):
         raise ValueError("z/a/b shape does not match the head layout")
-    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
+    N = B
+    if cu_seqlens is not None:
+        cu_seqlens, N = _cu_seqlens(cu_seqlens, B, T, dev)
     if initial_state is not None:
         initial_state = _f32(initial_state)
         if tuple(initial_state.shape) != (N, Hv, dk, dv):
@@ -297,8 +311,7 @@ def gdn_prefill_bwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, d_out, *
     a, b = a.contiguous(), b.contiguous()
     d_out = d_out.to(torch.bfloat16).contiguous()
     conv_w, A_log, dt_bias, norm_w = (_f32(t) for t in (conv_w, A_log, dt_bias, norm_w))
-    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, cu_seqlens, initial_state, d_out,
-               d_final_state)
+    dev = _dev(x, z, a, b, conv_w, A_log, dt_bias, norm_w, initial_state, d_out, d_final_state)
     for name, t in (("mixed_qkv", x), ("z", z), ("a", a), ("b", b)):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{name} must be bf16")
@@ -308,11 +321,19 @@ def gdn_prefill_bwd(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, d_out, *
         raise ValueError("mixed_qkv / conv_w channel count does not match the head layout")
     if z.numel() != B * T * Hv * dv or d_out.numel() != B * T * Hv * dv:
         raise ValueError("z / d_out size does not match the head layout")
-    N = B if cu_seqlens is None else _check_cu_seqlens(cu_seqlens, B, T)
+    if a.shape != (B, T, Hv) or b.shape != (B, T, Hv):
+        raise ValueError(f"a and b must be {(B, T, Hv)}, got {tuple(a.shape)}, {tuple(b.shape)}")
+    N = B
+    if cu_seqlens is not None:
+        cu_seqlens, N = _cu_seqlens(cu_seqlens, B, T, dev)
     if initial_state is not None:
         initial_state = _f32(initial_state)
+        if tuple(initial_state.shape) != (N, Hv, dk, dv):
+            raise ValueError(f"initial_state must be {(N, Hv, dk, dv)}, got {tuple(initial_state.shape)}")
     if d_final_state is not None:
         d_final_state = _f32(d_final_state)
+        if tuple(d_final_state.shape) != (N, Hv, dk, dv):
+            raise ValueError(f"d_final_state must be {(N, Hv, dk, dv)}, got {tuple(d_final_state.shape)}")
     dx = torch.empty_like(x)
     dz = torch.empty_like(z)
     da = torch.empty_like(a)

@@ -7,8 +7,15 @@ the fixtures here come from those third-party functions
 (transformers/models/qwen3_5/modeling_qwen3_5.py):
   torch_chunk_gated_delta_rule, torch_recurrent_gated_delta_rule,
   causal_conv1d_fn, causal_conv1d_update, Qwen3_5RMSNormGated, l2norm.
-All in float32 on the CPU.  Run once here (transformers 5.15.0); the .npz files
-are committed and the tests read only those.
+All in float32 on the CPU.  The layer fixtures (``layer_*.npz``) run the whole
+``Qwen3_5GatedDeltaNet`` module (projections, conv, gates, GQA, chunked rule, gated
+norm, out_proj) with a padding mask, and its cached decode (``DynamicCache``:
+prefill, then single-token steps through causal_conv1d_update and
+torch_recurrent_gated_delta_rule).  In float32 HF's module computes what
+deltanet.py:226-306 computes (its gated norm's casts are then identities), so these
+pin the layer wiring: which channels are q, k and v, a -> g and b -> beta, and which
+z a norm row pairs with.  Run once here (transformers 5.15.0); the .npz files are
+committed and the tests read only those.
 
     python tests/golden/make_golden.py
 """
@@ -98,6 +105,61 @@ def norm_case(name, seed, N, D):
                         l2=l2.numpy())
 
 
+LAYER_PREFIX = "model.language_model.layers.0.linear_attn."
+
+
+def layer_case(name, seed, D, Hk, Hv, dk, dv, B, T, pad, T0, steps, save_state):
+    """One Qwen3_5GatedDeltaNet layer in fp32: a masked prefill of [B, T] (row 1 has
+    ``pad`` masked tokens at the front, row 0 ``pad`` at the back), and an unmasked
+    prefill of T0 tokens into a DynamicCache followed by ``steps`` cached decode steps."""
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3_5.configuration_qwen3_5 import Qwen3_5TextConfig
+    cfg = Qwen3_5TextConfig(hidden_size=D, linear_num_key_heads=Hk, linear_num_value_heads=Hv,
+                            linear_key_head_dim=dk, linear_value_head_dim=dv,
+                            linear_conv_kernel_dim=4, num_hidden_layers=1,
+                            layer_types=["linear_attention"], rms_norm_eps=1e-6, vocab_size=16,
+                            intermediate_size=16, num_attention_heads=2, num_key_value_heads=1,
+                            head_dim=16)
+    rng = np.random.default_rng(seed)
+    m = hf.Qwen3_5GatedDeltaNet(cfg, 0).float().eval()
+    conv_dim = 2 * Hk * dk + Hv * dv
+    n = lambda s, *shape: torch.from_numpy((s * rng.standard_normal(shape)).astype(np.float32))
+    params = {
+        "in_proj_qkv.weight": n(0.25, conv_dim, D), "in_proj_z.weight": n(0.25, Hv * dv, D),
+        "in_proj_b.weight": n(0.25, Hv, D), "in_proj_a.weight": n(0.25, Hv, D),
+        "conv1d.weight": n(0.3, conv_dim, 1, 4),
+        "dt_bias": torch.from_numpy(rng.uniform(-2.0, 0.0, Hv).astype(np.float32)),
+        "A_log": torch.from_numpy(np.log(rng.uniform(1.0, 16.0, Hv)).astype(np.float32)),
+        "norm.weight": 1.0 + n(0.1, dv), "out_proj.weight": n(0.25 / np.sqrt(Hv), D, Hv * dv),
+    }
+    with torch.no_grad():
+        sd = m.state_dict()
+        for k_, v_ in params.items():
+            assert sd[k_].shape == v_.shape, (k_, sd[k_].shape, v_.shape)
+            sd[k_].copy_(v_)
+    hidden = n(1.0, B, T, D)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    if pad:
+        mask[0, T - pad:] = 0
+        if B > 1:
+            mask[1, :pad] = 0
+    hid0 = n(1.0, B, T0, D)
+    hid_dec = n(1.0, steps, B, 1, D)
+    with torch.no_grad():
+        out = m(hidden, attention_mask=mask)
+        cache = DynamicCache(config=cfg)
+        out0 = m(hid0, cache_params=cache)
+        outs = [m(hid_dec[s], cache_params=cache) for s in range(steps)]
+    fx = {LAYER_PREFIX + k_: v_.numpy() for k_, v_ in params.items()}
+    fx.update(dims=np.array([D, Hk, Hv, dk, dv], np.int64), hidden=hidden.numpy(),
+              mask=mask.numpy().astype(np.int32), out=out.numpy(), hidden_prefill=hid0.numpy(),
+              out_prefill=out0.numpy(), hidden_decode=hid_dec[:, :, 0].numpy(),
+              out_decode=torch.stack(outs)[:, :, 0].numpy())
+    if save_state:
+        fx["state_after_decode"] = cache.layers[0].recurrent_states[0].numpy()
+    np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **fx)
+
+
 def main():
     torch.set_num_threads(4)
     chunk_case("chunk_gqa_pad_c16", 11, B=1, T=100, Hk=1, H=2, dk=16, dv=32, C=16, with_s0=False)
@@ -107,6 +169,13 @@ def main():
     recurrent_case("recurrent_gqa_s0", 21, B=2, T=5, Hk=2, H=4, dk=16, dv=32)
     conv_case("conv_k4", 31, B=2, T=20, C=24, K=4)
     norm_case("gated_norm", 41, N=16, D=32)
+    layer_case("layer_d128", 51, D=16, Hk=2, Hv=4, dk=128, dv=128, B=2, T=100, pad=9, T0=67,
+               steps=3, save_state=False)
+    layer_case("layer_d64", 52, D=16, Hk=2, Hv=4, dk=64, dv=64, B=2, T=100, pad=0, T0=130,
+               steps=3, save_state=True)
+    # the reference's smoke layout (config.py:94-101): dk=16, dv=32
+    layer_case("layer_smoke_d16", 53, D=16, Hk=2, Hv=4, dk=16, dv=32, B=2, T=33, pad=5, T0=16,
+               steps=4, save_state=True)
 
 
 if __name__ == "__main__":

@@ -82,6 +82,37 @@ def test_decode_c2_full_size_b64():
     assert np.array_equal(np_(t["conv_state"]), conv_ref)
 
 
+def test_decode_c2_b256_streamed_state():
+    """Config C2 at B=256: S [256,32,128,128] fp32 is 512 MiB, above the size (192 MiB)
+    where the kernel streams the state with non-temporal loads and stores.  Sequences
+    are independent, so the fp64 oracle checks a sample of them (first, last and two
+    inside), each against the whole-batch GPU call."""
+    from omegalax_amd import gdn_decode_step
+    say("decode C2 B=256 (non-temporal state path)")
+    B = 256
+    d = W.decode_inputs(B)
+    t = W.to_device(d)
+    assert t["state"].numel() * 4 > 192 << 20
+    out = gdn_decode_step(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                          t["dt_bias"], t["norm_w"], t["conv_state"], t["state"],
+                          num_k_heads=16, head_k_dim=128, num_v_heads=32, head_v_dim=128)
+    torch.cuda.synchronize()
+    rows = np.array([0, 77, 200, 255])
+    ref, conv_ref, S_ref = O.gdn_decode_step(d["mixed_qkv"][rows], d["z"][rows], d["a"][rows],
+                                             d["b"][rows], d["conv_w"], d["A_log"],
+                                             d["dt_bias"], d["norm_w"], d["conv_state"][rows],
+                                             d["state"][rows].astype(np.float64),
+                                             Hk=16, dk=128, Hv=32, dv=128)
+    idx = torch.from_numpy(rows).cuda()
+    assert rel(np_(out.index_select(0, idx)), ref) < BF16_TOL
+    assert rel(np_(t["state"].index_select(0, idx)), S_ref) < STATE_TOL
+    assert np.array_equal(np_(t["conv_state"].index_select(0, idx)), conv_ref)
+    # every sequence was updated: no state row is left as it was
+    S0 = torch.from_numpy(d["state"]).cuda()
+    changed = (t["state"] != S0).flatten(1).any(dim=1)
+    assert bool(changed.all())
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("B,Hk,Hv,dk,dv", [(2, 2, 4, 64, 64), (3, 16, 32, 128, 128),
                                            (1, 1, 3, 32, 16)])

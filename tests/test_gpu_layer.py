@@ -55,8 +55,8 @@ def ref_prefill(d, dims, cu=None, S0=None, conv0=None):
 
 
 @pytest.mark.parametrize("B,T,Hk,Hv,dk,dv", [
-    (2, 100, 2, 4, 128, 128),   # dv split over two workgroups: epilogue kernel
-    (1, 64, 1, 1, 64, 64),      # one workgroup holds dv: fused norm
+    (2, 100, 2, 4, 128, 128),   # two batch rows, a partial last chunk
+    (1, 64, 1, 1, 64, 64),      # exactly one chunk
     (2, 3, 1, 2, 64, 64),       # shorter than the conv window
     (1, 200, 2, 2, 64, 128),
     (1, 130, 1, 2, 128, 64),
@@ -89,6 +89,37 @@ def test_layer_varlen_with_carried_states():
     t = W.to_device(d)
     out, S, conv = gpu_prefill(t, dims, cu, S0, conv0)
     ref, S_ref, conv_ref = ref_prefill(d, dims, cu, S0, conv0)
+    assert rel(np_(out), ref) < BF16_TOL
+    assert rel(np_(S), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv), conv_ref)
+
+
+def test_layer_offsets_host_checked_or_read_as_ordered_repair():
+    """cu_seqlens on the host is checked there (ValueError when invalid); on the device it
+    is never read by the host, and the kernels read invalid offsets as c[0] = 0, c[N] = T,
+    c[n] = running max of clamp(cu[n], 0, T): the result is then that of the repaired
+    offsets, bit for bit, with every output row written."""
+    from omegalax_amd import gdn_prefill
+    say("layer offsets: host check and device repair")
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    T = 150
+    d = W.layer_inputs(1, T, **dims, seed=8)
+    t = W.to_device(d)
+    kw = dict(num_k_heads=2, head_k_dim=128, num_v_heads=4, head_v_dim=128,
+              output_final_state=True)
+    bad = np.array([3, 70, 40, 120], np.int32)
+    fixed = np.array([0, 70, 70, T], np.int32)
+    with pytest.raises(ValueError, match="monotonically"):
+        gdn_prefill(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                    t["dt_bias"], t["norm_w"], cu_seqlens=torch.from_numpy(bad), **kw)
+    host = gdn_prefill(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
+                       t["dt_bias"], t["norm_w"], cu_seqlens=torch.from_numpy(fixed), **kw)
+    out, S, conv = gpu_prefill(t, dims, bad)
+    out2, S2, conv2 = gpu_prefill(t, dims, fixed)
+    for a, b, c in zip((out, S, conv), (out2, S2, conv2), host):
+        assert bool(torch.isfinite(a.float()).all())
+        assert torch.equal(a, b) and torch.equal(a, c)
+    ref, S_ref, conv_ref = ref_prefill(d, dims, fixed)
     assert rel(np_(out), ref) < BF16_TOL
     assert rel(np_(S), S_ref) < STATE_TOL
     assert np.array_equal(np_(conv), conv_ref)

@@ -177,3 +177,35 @@ def test_layer_module_trains_end_to_end():
     say("  " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
     for n, e in errs.items():
         assert e < BF16_TOL, (n, e)
+
+
+def test_layer_bwd_c1_heads_packed_persistent_rows():
+    """The C1 head layout (Hk=16, Hv=32, d=128) with tokens * Hv = 19,200 rows, above the
+    16,384 (token, value head) rows one pass of the norm adjoint's persistent grid covers, so
+    its wavefronts take a second row; three packed sequences, one of a single token."""
+    say("layer bwd C1 heads, T=600 packed in 3 sequences (norm adjoint's second pass)")
+    lens = [200, 1, 399]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    dims = dict(Hk=16, dk=128, Hv=32, dv=128)
+    d = make(11, 1, int(cu[-1]), 16, 32, 128, 128, N=len(lens))
+    got = run_gpu(d, dims, cu)
+    say("  oracle (fp64, about 20 s)")
+    check(got, run_ref(d, dims, cu))
+
+
+def test_layer_bwd_reads_invalid_offsets_as_their_ordered_repair():
+    """Offsets that break 0 = cu[0] <= ... <= cu[N] = T are read as c[0] = 0, c[N] = T,
+    c[n] = running max of clamp(cu[n], 0, T): every token belongs to one sequence, so no
+    gradient row is left unwritten and no parameter gradient sums one."""
+    say("layer bwd with invalid offsets")
+    T = 150
+    bad = np.array([3, 70, 40, 120], np.int32)       # cu[0] > 0, a decrease, cu[N] < T
+    fixed = np.array([0, 70, 70, T], np.int32)
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    d = make(13, 1, T, 2, 4, 128, 128, N=3)
+    got = run_gpu(d, dims, bad)
+    want = run_gpu(d, dims, fixed)
+    for n, a, b in zip(NAMES, got, want):
+        assert np.all(np.isfinite(a)), n
+        assert np.array_equal(a, b), n
+    check(got, run_ref(d, dims, fixed))

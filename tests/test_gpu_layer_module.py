@@ -3,9 +3,12 @@
 * the layer forward (projections as bf16 GEMMs, the fused kernel path between them)
   against the oracle's layer restatement on the same projection outputs
   (deltanet.py:226-306), with an attention mask;
-* packed documents (segment ids) against one run per document;
+* packed documents (segment ids) against the oracle's layer run on each document
+  alone (state and conv window restart at every document), and against one GPU run
+  per document;
 * a right-padded prefill into the decode cache, then cached decode steps, against
-  a full prefill of each row.
+  the oracle's prefill of each row's real tokens followed by the oracle's decode
+  steps (gdn_decode_step), and against a full GPU prefill of each row.
 Tolerance: bf16 outputs 2e-2 (max-abs-normalised).
 """
 import sys
@@ -74,6 +77,30 @@ def test_layer_forward_matches_oracle_with_mask():
     assert rel(np_(out), ref) < BF16_TOL
 
 
+def oracle_rows(p, cfg, h_TD):
+    """The oracle's layer (bf16 rounding points) on one sequence's bf16 projection
+    outputs: returns (out [T, D] fp64, final state, conv state)."""
+    import torch.nn.functional as F
+    h = h_TD[None]
+    T = h.shape[1]
+    mixed, z, a, b = (F.linear(h, w) for w in (p.in_proj_qkv, p.in_proj_z, p.in_proj_a, p.in_proj_b))
+    n, S, conv = O.gdn_prefill_layer(np_(mixed), np_(z).reshape(1, T, cfg.num_v_heads, cfg.head_v_dim),
+                                     np_(a), np_(b), np_(p.conv_w), np_(p.A_log), np_(p.dt_bias),
+                                     np_(p.norm_w), Hk=cfg.num_k_heads, dk=cfg.head_k_dim,
+                                     Hv=cfg.num_v_heads, dv=cfg.head_v_dim)
+    return np.asarray(n, np.float64)[0] @ np_(p.out_proj).astype(np.float64).T, S, conv
+
+
+def oracle_decode(p, cfg, h_BD, conv, S):
+    import torch.nn.functional as F
+    mixed, z, a, b = (F.linear(h_BD, w) for w in (p.in_proj_qkv, p.in_proj_z, p.in_proj_a, p.in_proj_b))
+    n, conv, S = O.gdn_decode_step(np_(mixed), np_(z).reshape(h_BD.shape[0], cfg.num_v_heads, -1),
+                                   np_(a), np_(b), np_(p.conv_w), np_(p.A_log), np_(p.dt_bias),
+                                   np_(p.norm_w), conv, S, Hk=cfg.num_k_heads, dk=cfg.head_k_dim,
+                                   Hv=cfg.num_v_heads, dv=cfg.head_v_dim)
+    return np.asarray(n, np.float64) @ np_(p.out_proj).astype(np.float64).T, conv, S
+
+
 def test_packed_documents_equal_separate_runs():
     from omegalax_amd.layer import gated_deltanet_forward
     say("layer module packed documents")
@@ -91,6 +118,8 @@ def test_packed_documents_equal_separate_runs():
         alone = gated_deltanet_forward(p, cfg, hidden[b:b + 1, s:e].contiguous())
         torch.cuda.synchronize()
         assert rel(np_(out[b, s:e]), np_(alone[0])) < BF16_TOL, (b, s, e)
+        ref, _, _ = oracle_rows(p, cfg, hidden[b, s:e])
+        assert rel(np_(out[b, s:e]), ref) < BF16_TOL, (b, s, e)
 
 
 def test_right_padded_prefill_cache_then_decode_equals_full_prefill():
@@ -123,3 +152,11 @@ def test_right_padded_prefill_cache_then_decode_equals_full_prefill():
             assert float(out_p[b, n:].abs().max()) == 0.0  # padded positions
         for s in range(steps):
             assert rel(np_(outs[s][b]), np_(ref[0, n + s])) < BF16_TOL, (b, s)
+        # the oracle: prefill of the row's real tokens, then its decode steps
+        o_ref, S, conv = oracle_rows(p, cfg, full[b, :n])
+        assert rel(np_(out_p[b, :n]), o_ref) < BF16_TOL, b
+        for s in range(steps):
+            o_ref, conv, S = oracle_decode(p, cfg, full[b:b + 1, n + s], conv, S)
+            assert rel(np_(outs[s][b]), o_ref[0]) < BF16_TOL, (b, s)
+        assert rel(np_(cache.recurrent_state[b]), S[0]) < 1e-3, b
+        assert np.array_equal(np_(cache.conv_state[b]), conv[0]), b
