@@ -4,7 +4,7 @@
 // call, so an invalid request returns OMX_GDN_EINVAL (with a message from
 // omx_gdn_last_error) on any machine, GPU or not.  No C++ exception crosses
 // the ABI and nothing here synchronises the stream.
-#include "../../include/omx_gdn.h"
+#include "omx_gdn.h"
 
 #include <hip/hip_runtime.h>
 
