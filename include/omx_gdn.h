@@ -129,6 +129,32 @@ size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t 
                                       int64_t dv, int64_t N);
 
 /*
+ * omx_gdn_prefill without a workspace argument: the same kernels, with their scratch
+ * (the workspace omx_gdn_prefill_workspace_size gives) in a fixed device array of the
+ * library, omx_gdn_prefill_noalloc_max_scratch() bytes (64 MiB) per GPU, held from the
+ * library's first use on that GPU until the process ends.  No reference counterpart:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  It calls no hipMalloc/hipFree
+ * and no allocating library routine.
+ *   Arguments, layouts and results are those of omx_gdn_prefill.  Shapes whose workspace
+ * exceeds the fixed size are rejected with OMX_GDN_EINVAL (at the Qwen3.5 head layout,
+ * Hk=16 Hv=32 d=128, about 1,900 tokens per call).  Every call on one GPU uses that
+ * GPU's one array: calls that overlap on one GPU (other streams, other threads) race
+ * and give undefined results; serialise them.  Nothing in the scratch needs to start
+ * at zero: every region is written before it is read within a call.
+ */
+int omx_gdn_prefill_noalloc(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                            const float* conv_w, const float* A_log, const float* dt_bias,
+                            const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                            const float* initial_state, float* final_state,
+                            const void* conv_state_in, void* conv_state_out, void* out,
+                            int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                            int64_t K, int64_t chunk_size, void* stream);
+
+/* Bytes of the fixed scratch behind omx_gdn_prefill_noalloc. */
+size_t omx_gdn_prefill_noalloc_max_scratch(void);
+
+/*
  * One cached decode step for one token per sequence: conv-cache update + SiLU,
  * gates, q/k L2-norm, recurrent rule, gated RMSNorm.  No reference counterpart:
  * omegalax drops the cache for Qwen3.5 (model.py:324-326) and its decode API

@@ -35,6 +35,9 @@ SIGNATURES = {
     "omx_gdn_prefill": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _i64, _p, _p, _p, _p, _p,
                              _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "omx_gdn_prefill_workspace_size": (_sz, [_i64] * 7),
+    "omx_gdn_prefill_noalloc": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _i64, _p, _p, _p, _p,
+                                     _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
+    "omx_gdn_prefill_noalloc_max_scratch": (_sz, []),
     "omx_gdn_decode_step": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _p, _p,
                                  _i64, _i64, _i64, _i64, _i64, _i64, _p]),
     "omx_gdn_recurrent_step": (_i, [_p, _p, _p, _i, _p, _p, _p, _p,

@@ -12,6 +12,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "gdn_kernels.h"
@@ -310,14 +311,19 @@ size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t 
   return chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer).total;
 }
 
-int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
-                    const float* conv_w, const float* A_log, const float* dt_bias,
-                    const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
-                    const float* initial_state, float* final_state, const void* conv_state_in,
-                    void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
-                    int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
-                    void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "omx_gdn_prefill";
+}  // extern "C"
+
+namespace {
+
+// The layer prefill behind omx_gdn_prefill and omx_gdn_prefill_noalloc (`fn` names the
+// entry point in error messages).
+int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const void* a,
+                  const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
+                  const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                  const float* initial_state, float* final_state, const void* conv_state_in,
+                  void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                  int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                  void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
@@ -370,6 +376,77 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
     e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, eps,
                                   (hipStream_t)stream);
   return launch_status(e, fn);
+}
+
+// The fixed scratch of omx_gdn_prefill_noalloc: a file-scope device array, so that entry
+// point allocates nothing.  Each device holds its own copy (allocated when the library's
+// code object is loaded there, kept until the process ends).  Host code never uses the
+// array's name as an address: the per-device address comes from hipGetSymbolAddress.
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (looked up once per device, with it current).
+int scratch_for_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(OMX_GDN_ELAUNCH, "%s: hipGetDevice failed: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(OMX_GDN_EUNSUPPORTED, "%s: device index %d above %d", fn, dev, kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(OMX_GDN_ELAUNCH, "%s: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                  fn, dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return OMX_GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                    const float* conv_w, const float* A_log, const float* dt_bias,
+                    const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                    const float* initial_state, float* final_state, const void* conv_state_in,
+                    void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                    int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  return prefill_entry("omx_gdn_prefill", mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w,
+                       eps, cu_seqlens, N, initial_state, final_state, conv_state_in,
+                       conv_state_out, out, B, T, Hk, Hv, dk, dv, K, chunk_size, workspace,
+                       workspace_bytes, stream);
+}
+
+size_t omx_gdn_prefill_noalloc_max_scratch(void) { return kNoAllocScratchBytes; }
+
+int omx_gdn_prefill_noalloc(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                            const float* conv_w, const float* A_log, const float* dt_bias,
+                            const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                            const float* initial_state, float* final_state,
+                            const void* conv_state_in, void* conv_state_out, void* out, int64_t B,
+                            int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t K,
+                            int64_t chunk_size, void* stream) {
+  const char* fn = "omx_gdn_prefill_noalloc";
+  const size_t need = omx_gdn_prefill_workspace_size(B, T, Hk, Hv, dk, dv, N);
+  REQUIRE(need <= kNoAllocScratchBytes,
+          "%s: these shapes need %zu bytes of scratch, above the fixed %zu (call omx_gdn_prefill "
+          "with a workspace instead)",
+          fn, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(fn, &ws);
+  if (rc) return rc;
+  return prefill_entry(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps, cu_seqlens,
+                       N, initial_state, final_state, conv_state_in, conv_state_out, out, B, T,
+                       Hk, Hv, dk, dv, K, chunk_size, ws, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"
