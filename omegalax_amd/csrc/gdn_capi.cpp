@@ -134,6 +134,70 @@ int check_heads(const char* fn, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv) 
   return OMX_GDN_OK;
 }
 
+// Head dims a call runs at: the caller's when the kernels are compiled for them, else
+// the smallest compiled dims that cover them (the call then runs on zero-padded copies,
+// gdn_pad.hip); ok = false when none do.
+struct HeadDims {
+  int64_t dk, dv;
+  bool pad, ok;
+};
+enum DimsKind { kCoreFwd, kLayerFwd, kCoreBwd, kLayerBwd };
+
+HeadDims head_dims(DimsKind kind, int64_t dk, int64_t dv, bool f32) {
+  auto compiled = [&](int64_t a, int64_t b) {
+    switch (kind) {
+      case kCoreFwd: return omx::chunk_dims_supported((int)a, (int)b, f32);
+      case kLayerFwd: return omx::layer_dims_supported((int)a, (int)b);
+      case kCoreBwd: return omx::bwd_dims_supported((int)a, (int)b, f32);
+      default: return omx::bwd_dims_supported((int)a, (int)b, false);
+    }
+  };
+  if (dk < 1 || dv < 1 || dk > 128 || dv > 256) return {dk, dv, false, compiled(dk, dv) && dk >= 1};
+  if (compiled(dk, dv)) return {dk, dv, false, true};
+  for (int64_t k2 = 32; k2 <= 128; k2 *= 2) {
+    if (k2 < dk) continue;
+    for (int64_t v2 = (dv + 63) / 64 * 64; v2 <= 256; v2 += 64)
+      if (compiled(k2, v2)) return {k2, v2, true, true};
+  }
+  return {dk, dv, false, false};
+}
+
+// Sub-allocation of a workspace in 256-byte aligned pieces.
+struct Arena {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes, 256);
+    return at;
+  }
+};
+
+omx::PadView pv(const void* p, int64_t G, int64_t E, int64_t rs, int64_t gs) {
+  return omx::PadView{p, (int)G, (int)E, (long long)rs, (long long)gs};
+}
+
+// [R][G][E] -> [R][G2][E2] copy with zero fill (or the reverse, cropping)
+hipError_t pad3(const void* src, int64_t G, int64_t E, void* dst, int64_t G2, int64_t E2,
+                int64_t R, int esize, hipStream_t st) {
+  return omx::launch_pad_copy(pv(src, G, E, G * E, E), pv(dst, G2, E2, G2 * E2, E2), R, esize, st);
+}
+
+// the channel blocks [q Hk*dk | k Hk*dk | v Hv*dv] of R rows of `per` values per channel
+// (mixed_qkv: per = 1; conv weights: per = K; conv caches: per = K - 1), re-laid at
+// (dk2, dv2) with zero channels (or cropped back)
+hipError_t pad_channels(const void* src, int64_t dk, int64_t dv, void* dst, int64_t dk2,
+                        int64_t dv2, int64_t Hk, int64_t Hv, int64_t R, int64_t per, int esize,
+                        hipStream_t st) {
+  const int64_t cs = 2 * Hk * dk + Hv * dv, cd = 2 * Hk * dk2 + Hv * dv2;
+  hipError_t e = omx::launch_pad_copy(pv(src, 2 * Hk, dk * per, cs * per, dk * per),
+                                      pv(dst, 2 * Hk, dk2 * per, cd * per, dk2 * per), R, esize, st);
+  if (e != hipSuccess) return e;
+  const char* s2 = (const char*)src + 2 * Hk * dk * per * esize;
+  char* d2 = (char*)dst + 2 * Hk * dk2 * per * esize;
+  return omx::launch_pad_copy(pv(s2, Hv, dv * per, cs * per, dv * per),
+                              pv(d2, Hv, dv2 * per, cd * per, dv2 * per), R, esize, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -246,22 +310,13 @@ hipError_t launch_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspac
   return e;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
-                                        int64_t dv, int64_t N, int in_dtype) {
-  return chunk_ws(B, T, Hk, Hv, dk, dv, N,
-                  in_dtype == OMX_GDN_F32 ? omx::kModeF32 : omx::kModeBF16).total;
-}
-
-int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
-                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
-                      int64_t N, float* o, float* final_state, int64_t B, int64_t T, int64_t Hk,
-                      int64_t Hv, int64_t dk, int64_t dv, int64_t chunk_size, float scale,
-                      int qk_l2norm, void* workspace, size_t workspace_bytes, void* stream) {
-  const char* fn = "omx_gdn_chunk_fwd";
+// The chunked rule at compiled head dims (omx_gdn_chunk_fwd pads other dims around it).
+int chunk_fwd_core(const char* fn, const void* q, const void* k, const void* v, int in_dtype,
+                   const float* g, const float* beta, const float* initial_state,
+                   const int32_t* cu_seqlens, int64_t N, float* o, float* final_state, int64_t B,
+                   int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t chunk_size,
+                   float scale, int qk_l2norm, void* workspace, size_t workspace_bytes,
+                   void* stream) {
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
@@ -279,7 +334,8 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   }
   const bool f32 = in_dtype == OMX_GDN_F32;
   if (!omx::chunk_dims_supported((int)dk, (int)dv, f32))
-    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled for %s inputs",
+    return fail(OMX_GDN_EUNSUPPORTED,
+                "%s: head dims dk=%lld dv=%lld not supported for %s inputs (dk <= 128, dv <= 256)",
                 fn, (long long)dk, (long long)dv, f32 ? "fp32" : "bf16");
   const int mode = f32 ? omx::kModeF32 : omx::kModeBF16;
   const ChunkWs ws = chunk_ws(B, T, Hk, Hv, dk, dv, N, mode);
@@ -306,24 +362,123 @@ int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype,
   return launch_status(launch_chunked(p, ws, workspace, mode, (hipStream_t)stream), fn);
 }
 
-size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
-                                      int64_t dv, int64_t N) {
-  return chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer).total;
+// Checks every entry point of the chunked path makes before looking at head dims.
+int chunk_shape_check(const char* fn, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                      int64_t chunk_size, int64_t B, int64_t T, const int32_t* cu_seqlens,
+                      int64_t N) {
+  int rc = check_heads(fn, Hk, Hv, dk, dv);
+  if (rc) return rc;
+  REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
+  REQUIRE(B >= 0 && T >= 0, "%s: negative shape (B=%lld, T=%lld)", fn, (long long)B, (long long)T);
+  REQUIRE(B * T <= (int64_t)1 << 31, "%s: too many tokens (%lld)", fn, (long long)(B * T));
+  if (cu_seqlens) {
+    REQUIRE(B == 1, "%s: cu_seqlens requires batch 1 (got %lld)", fn, (long long)B);
+    REQUIRE(N >= 1 && N <= (1 << 20), "%s: sequence count %lld out of range", fn, (long long)N);
+  } else {
+    REQUIRE(N == B, "%s: without cu_seqlens N must equal B (%lld vs %lld)", fn, (long long)N,
+            (long long)B);
+  }
+  return OMX_GDN_OK;
+}
+
+// Workspace of a padded core forward: q, k, v, o, initial and final state at the padded
+// dims, then the workspace of the call at those dims.
+struct FwdPadWs {
+  size_t q, k, v, o, s0, s1, inner, total;
+};
+FwdPadWs fwd_pad_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk2, int64_t dv2,
+                    int64_t N, bool f32) {
+  FwdPadWs w{};
+  if (B < 0 || T < 0 || N < 0) return w;
+  const size_t tok = (size_t)(B * T), esz = f32 ? 4 : 2, st = (size_t)(N * Hv * dk2 * dv2) * 4;
+  Arena a;
+  w.q = a.take(tok * Hk * dk2 * esz);
+  w.k = a.take(tok * Hk * dk2 * esz);
+  w.v = a.take(tok * Hv * dv2 * esz);
+  w.o = a.take(tok * Hv * dv2 * 4);
+  w.s0 = a.take(st);
+  w.s1 = a.take(st);
+  w.inner = a.off;
+  w.total = w.inner + chunk_ws(B, T, Hk, Hv, dk2, dv2, N, f32 ? omx::kModeF32 : omx::kModeBF16).total;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                        int64_t dv, int64_t N, int in_dtype) {
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  const HeadDims hd = head_dims(kCoreFwd, dk, dv, f32);
+  if (hd.pad) return fwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N, f32).total;
+  return chunk_ws(B, T, Hk, Hv, dk, dv, N, f32 ? omx::kModeF32 : omx::kModeBF16).total;
+}
+
+int omx_gdn_chunk_fwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
+                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
+                      int64_t N, float* o, float* final_state, int64_t B, int64_t T, int64_t Hk,
+                      int64_t Hv, int64_t dk, int64_t dv, int64_t chunk_size, float scale,
+                      int qk_l2norm, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "omx_gdn_chunk_fwd";
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  const HeadDims hd = head_dims(kCoreFwd, dk, dv, f32);
+  if (!hd.pad)
+    return chunk_fwd_core(fn, q, k, v, in_dtype, g, beta, initial_state, cu_seqlens, N, o,
+                          final_state, B, T, Hk, Hv, dk, dv, chunk_size, scale, qk_l2norm,
+                          workspace, workspace_bytes, stream);
+  // head dims the kernels are not compiled for: run on zero-padded copies
+  int rc = chunk_shape_check(fn, Hk, Hv, dk, dv, chunk_size, B, T, cu_seqlens, N);
+  if (rc) return rc;
+  REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
+          in_dtype);
+  const FwdPadWs w = fwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N, f32);
+  REQUIRE(workspace_bytes >= w.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, w.total);
+  if (N == 0 || (B * T == 0 && !final_state)) return ok();
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  if (B * T > 0) REQUIRE(q && k && v && g && beta && o, "%s: a required pointer is NULL", fn);
+  char* base = (char*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  const int esz = f32 ? 4 : 2;
+  const int64_t tok = B * T, dk2 = hd.dk, dv2 = hd.dv;
+  hipError_t e = hipSuccess;
+  if (tok > 0) {
+    e = pad3(q, Hk, dk, base + w.q, Hk, dk2, tok, esz, st);
+    if (e == hipSuccess) e = pad3(k, Hk, dk, base + w.k, Hk, dk2, tok, esz, st);
+    if (e == hipSuccess) e = pad3(v, Hv, dv, base + w.v, Hv, dv2, tok, esz, st);
+  }
+  if (e == hipSuccess && initial_state)
+    e = pad3(initial_state, dk, dv, base + w.s0, dk2, dv2, N * Hv, 4, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  rc = chunk_fwd_core(fn, base + w.q, base + w.k, base + w.v, in_dtype, g, beta,
+                      initial_state ? (const float*)(base + w.s0) : nullptr, cu_seqlens, N,
+                      (float*)(base + w.o), final_state ? (float*)(base + w.s1) : nullptr, B, T,
+                      Hk, Hv, dk2, dv2, chunk_size, scale, qk_l2norm, base + w.inner,
+                      workspace_bytes - w.inner, stream);
+  if (rc) return rc;
+  if (tok > 0) e = pad3(base + w.o, Hv, dv2, o, Hv, dv, tok, 4, st);
+  if (e == hipSuccess && final_state)
+    e = pad3(base + w.s1, dk2, dv2, final_state, dk, dv, N * Hv, 4, st);
+  return launch_status(e, fn);
 }
 
 }  // extern "C"
 
 namespace {
 
-// The layer prefill behind omx_gdn_prefill and omx_gdn_prefill_noalloc (`fn` names the
-// entry point in error messages).
-int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const void* a,
-                  const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
-                  const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
-                  const float* initial_state, float* final_state, const void* conv_state_in,
-                  void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
-                  int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+// The layer prefill at compiled head dims.  dk_real and dv_real are the caller's head dims
+// (they differ from dk, dv when the buffers are zero-padded copies): q is scaled by
+// dk_real^-1/2 and the gated norm's mean divides by dv_real.
+int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const void* a,
+                 const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
+                 const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                 const float* initial_state, float* final_state, const void* conv_state_in,
+                 void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                 int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                 void* workspace, size_t workspace_bytes, void* stream, int64_t dk_real,
+                 int64_t dv_real) {
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
@@ -339,7 +494,8 @@ int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const vo
             (long long)B);
   }
   if (!omx::layer_dims_supported((int)dk, (int)dv))
-    return fail(OMX_GDN_EUNSUPPORTED, "%s: head dims dk=%lld dv=%lld not compiled", fn,
+    return fail(OMX_GDN_EUNSUPPORTED,
+                "%s: head dims dk=%lld dv=%lld not supported (dk <= 128, dv <= 256)", fn,
                 (long long)dk, (long long)dv);
   const ChunkWs ws = chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer);
   const size_t need = ws.total;
@@ -365,7 +521,7 @@ int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const vo
   p.nb = (int)(dv / omx::chunk_block_cols());
   p.conv_k = (int)K;
   p.conv_dim = (int)(2 * Hk * dk + Hv * dv);
-  p.scale = 1.0f / sqrtf((float)dk);
+  p.scale = 1.0f / sqrtf((float)dk_real);
   p.eps = eps;
   p.qk_l2norm = 1;
   p.o_part = (char*)workspace + ws.opart;
@@ -373,8 +529,99 @@ int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const vo
   REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
   if (e == hipSuccess)
-    e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, eps,
-                                  (hipStream_t)stream);
+    e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, (int)dv_real,
+                                  eps, (hipStream_t)stream);
+  return launch_status(e, fn);
+}
+
+// Workspace of a padded layer prefill: mixed_qkv, z, the output, conv weights, norm weight,
+// initial and final state and the conv caches in and out at the padded dims (conv caches
+// and weights sized for K = 4, the largest the prefill takes), then the call's workspace.
+struct LayerPadWs {
+  size_t x, z, out, cw, nw, s0, s1, c0, c1, inner, total;
+};
+LayerPadWs layer_pad_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk2, int64_t dv2,
+                        int64_t N) {
+  LayerPadWs w{};
+  if (B < 0 || T < 0 || N < 0) return w;
+  const size_t tok = (size_t)(B * T), cd = (size_t)(2 * Hk * dk2 + Hv * dv2);
+  const size_t st = (size_t)(N * Hv * dk2 * dv2) * 4;
+  Arena a;
+  w.x = a.take(tok * cd * 2);
+  w.z = a.take(tok * Hv * dv2 * 2);
+  w.out = a.take(tok * Hv * dv2 * 2);
+  w.cw = a.take(cd * 4 * 4);
+  w.nw = a.take(dv2 * 4);
+  w.s0 = a.take(st);
+  w.s1 = a.take(st);
+  w.c0 = a.take((size_t)N * cd * 3 * 2);
+  w.c1 = a.take((size_t)N * cd * 3 * 2);
+  w.inner = a.off;
+  w.total = w.inner + chunk_ws(B, T, Hk, Hv, dk2, dv2, N, omx::kModeLayer).total;
+  return w;
+}
+
+size_t prefill_ws_bytes(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                        int64_t N) {
+  const HeadDims hd = head_dims(kLayerFwd, dk, dv, false);
+  if (hd.pad) return layer_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N).total;
+  return chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer).total;
+}
+
+// The layer prefill behind omx_gdn_prefill and omx_gdn_prefill_noalloc (`fn` names the
+// entry point in error messages): at compiled head dims directly, else on zero-padded
+// copies.
+int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const void* a,
+                  const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
+                  const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                  const float* initial_state, float* final_state, const void* conv_state_in,
+                  void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
+                  int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  const HeadDims hd = head_dims(kLayerFwd, dk, dv, false);
+  if (!hd.pad)
+    return prefill_core(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps, cu_seqlens,
+                        N, initial_state, final_state, conv_state_in, conv_state_out, out, B, T,
+                        Hk, Hv, dk, dv, K, chunk_size, workspace, workspace_bytes, stream, dk, dv);
+  int rc = chunk_shape_check(fn, Hk, Hv, dk, dv, chunk_size, B, T, cu_seqlens, N);
+  if (rc) return rc;
+  REQUIRE(K >= 2 && K <= 4, "%s: conv kernel size %lld not in [2, 4]", fn, (long long)K);
+  const LayerPadWs w = layer_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N);
+  REQUIRE(workspace_bytes >= w.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, w.total);
+  if (N == 0) return ok();
+  const int64_t tok = B * T, dk2 = hd.dk, dv2 = hd.dv;
+  if (tok > 0) REQUIRE(mixed_qkv && z && a && b && out, "%s: an activation pointer is NULL", fn);
+  REQUIRE(conv_w && A_log && dt_bias && norm_w, "%s: a parameter pointer is NULL", fn);
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  char* base = (char*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (tok > 0) {
+    e = pad_channels(mixed_qkv, dk, dv, base + w.x, dk2, dv2, Hk, Hv, tok, 1, 2, st);
+    if (e == hipSuccess) e = pad3(z, Hv, dv, base + w.z, Hv, dv2, tok, 2, st);
+  }
+  if (e == hipSuccess) e = pad_channels(conv_w, dk, dv, base + w.cw, dk2, dv2, Hk, Hv, 1, K, 4, st);
+  if (e == hipSuccess) e = pad3(norm_w, 1, dv, base + w.nw, 1, dv2, 1, 4, st);
+  if (e == hipSuccess && initial_state)
+    e = pad3(initial_state, dk, dv, base + w.s0, dk2, dv2, N * Hv, 4, st);
+  if (e == hipSuccess && conv_state_in)
+    e = pad_channels(conv_state_in, dk, dv, base + w.c0, dk2, dv2, Hk, Hv, N, K - 1, 2, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  rc = prefill_core(fn, base + w.x, base + w.z, a, b, (const float*)(base + w.cw), A_log, dt_bias,
+                    (const float*)(base + w.nw), eps, cu_seqlens, N,
+                    initial_state ? (const float*)(base + w.s0) : nullptr,
+                    final_state ? (float*)(base + w.s1) : nullptr,
+                    conv_state_in ? base + w.c0 : nullptr, conv_state_out ? base + w.c1 : nullptr,
+                    base + w.out, B, T, Hk, Hv, dk2, dv2, K, chunk_size, base + w.inner,
+                    workspace_bytes - w.inner, stream, dk, dv);
+  if (rc) return rc;
+  if (tok > 0) e = pad3(base + w.out, Hv, dv2, out, Hv, dv, tok, 2, st);
+  if (e == hipSuccess && final_state)
+    e = pad3(base + w.s1, dk2, dv2, final_state, dk, dv, N * Hv, 4, st);
+  if (e == hipSuccess && conv_state_out)
+    e = pad_channels(base + w.c1, dk2, dv2, conv_state_out, dk, dv, Hk, Hv, N, K - 1, 2, st);
   return launch_status(e, fn);
 }
 
@@ -412,6 +659,11 @@ int scratch_for_current_device(const char* fn, void** out) {
 }  // namespace
 
 extern "C" {
+
+size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                      int64_t dv, int64_t N) {
+  return prefill_ws_bytes(B, T, Hk, Hv, dk, dv, N);
+}
 
 int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
                     const float* conv_w, const float* A_log, const float* dt_bias,
@@ -454,20 +706,18 @@ int omx_gdn_prefill_noalloc(const void* mixed_qkv, const void* z, const void* a,
 // ---------------------------------------------------------------------------- backward
 extern "C" {
 
-size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
-                                        int64_t dv, int64_t N, int in_dtype) {
-  return bwd_ws(B, T, Hk, Hv, dk, dv, N,
-                in_dtype == OMX_GDN_F32 ? omx::kModeF32 : omx::kModeBF16).total;
-}
+}  // extern "C"
 
-int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
-                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
-                      int64_t N, const float* d_o, const float* d_final_state, void* dq, void* dk,
-                      void* dv, float* dg, float* dbeta, float* d_initial_state, int64_t B,
-                      int64_t T, int64_t Hk, int64_t Hv, int64_t dk_dim, int64_t dv_dim,
-                      int64_t chunk_size, float scale, int qk_l2norm, void* workspace,
-                      size_t workspace_bytes, void* stream) {
-  const char* fn = "omx_gdn_chunk_bwd";
+namespace {
+
+// The rule's backward at compiled head dims (omx_gdn_chunk_bwd pads other dims around it).
+int chunk_bwd_core(const char* fn, const void* q, const void* k, const void* v, int in_dtype,
+                   const float* g, const float* beta, const float* initial_state,
+                   const int32_t* cu_seqlens, int64_t N, const float* d_o,
+                   const float* d_final_state, void* dq, void* dk, void* dv, float* dg,
+                   float* dbeta, float* d_initial_state, int64_t B, int64_t T, int64_t Hk,
+                   int64_t Hv, int64_t dk_dim, int64_t dv_dim, int64_t chunk_size, float scale,
+                   int qk_l2norm, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_heads(fn, Hk, Hv, dk_dim, dv_dim);
   if (rc) return rc;
   REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
@@ -486,8 +736,7 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
   const bool f32 = in_dtype == OMX_GDN_F32;
   if (!omx::bwd_dims_supported((int)dk_dim, (int)dv_dim, f32))
     return fail(OMX_GDN_EUNSUPPORTED,
-                "%s: head dims dk=%lld dv=%lld not compiled for %s inputs (bf16: dk 64/128, "
-                "fp32: dk 32/64; dv 64/128)",
+                "%s: head dims dk=%lld dv=%lld not supported for %s inputs (dk <= 128, dv <= 128)",
                 fn, (long long)dk_dim, (long long)dv_dim, f32 ? "fp32" : "bf16");
   const int mode = f32 ? omx::kModeF32 : omx::kModeBF16;
   const BwdWs ws = bwd_ws(B, T, Hk, Hv, dk_dim, dv_dim, N, mode);
@@ -542,6 +791,107 @@ int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
   return launch_status(omx::launch_bwd(b, st), fn);
 }
 
+// Workspace of a padded core backward: q, k, v, d_o, initial state, final-state cotangent,
+// dq, dk, dv and the initial-state gradient at the padded dims, then the call's workspace.
+struct BwdPadWs {
+  size_t q, k, v, dO, s0, ds, gq, gk, gv, gs0, inner, total;
+};
+BwdPadWs bwd_pad_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk2, int64_t dv2,
+                    int64_t N, bool f32) {
+  BwdPadWs w{};
+  if (B < 0 || T < 0 || N < 0) return w;
+  const size_t tok = (size_t)(B * T), esz = f32 ? 4 : 2, st = (size_t)(N * Hv * dk2 * dv2) * 4;
+  Arena a;
+  w.q = a.take(tok * Hk * dk2 * esz);
+  w.k = a.take(tok * Hk * dk2 * esz);
+  w.v = a.take(tok * Hv * dv2 * esz);
+  w.dO = a.take(tok * Hv * dv2 * 4);
+  w.s0 = a.take(st);
+  w.ds = a.take(st);
+  w.gq = a.take(tok * Hk * dk2 * esz);
+  w.gk = a.take(tok * Hk * dk2 * esz);
+  w.gv = a.take(tok * Hv * dv2 * esz);
+  w.gs0 = a.take(st);
+  w.inner = a.off;
+  w.total = w.inner + bwd_ws(B, T, Hk, Hv, dk2, dv2, N, f32 ? omx::kModeF32 : omx::kModeBF16).total;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                        int64_t dv, int64_t N, int in_dtype) {
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  const HeadDims hd = head_dims(kCoreBwd, dk, dv, f32);
+  if (hd.pad) return bwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N, f32).total;
+  return bwd_ws(B, T, Hk, Hv, dk, dv, N, f32 ? omx::kModeF32 : omx::kModeBF16).total;
+}
+
+int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype, const float* g,
+                      const float* beta, const float* initial_state, const int32_t* cu_seqlens,
+                      int64_t N, const float* d_o, const float* d_final_state, void* dq, void* dk,
+                      void* dv, float* dg, float* dbeta, float* d_initial_state, int64_t B,
+                      int64_t T, int64_t Hk, int64_t Hv, int64_t dk_dim, int64_t dv_dim,
+                      int64_t chunk_size, float scale, int qk_l2norm, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  const char* fn = "omx_gdn_chunk_bwd";
+  const bool f32 = in_dtype == OMX_GDN_F32;
+  const HeadDims hd = head_dims(kCoreBwd, dk_dim, dv_dim, f32);
+  if (!hd.pad)
+    return chunk_bwd_core(fn, q, k, v, in_dtype, g, beta, initial_state, cu_seqlens, N, d_o,
+                          d_final_state, dq, dk, dv, dg, dbeta, d_initial_state, B, T, Hk, Hv,
+                          dk_dim, dv_dim, chunk_size, scale, qk_l2norm, workspace,
+                          workspace_bytes, stream);
+  int rc = chunk_shape_check(fn, Hk, Hv, dk_dim, dv_dim, chunk_size, B, T, cu_seqlens, N);
+  if (rc) return rc;
+  REQUIRE(in_dtype == OMX_GDN_F32 || in_dtype == OMX_GDN_BF16, "%s: unknown in_dtype %d", fn,
+          in_dtype);
+  const BwdPadWs w = bwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N, f32);
+  REQUIRE(workspace_bytes >= w.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, w.total);
+  if (N == 0) return ok();
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  const int64_t tok = B * T, dk2 = hd.dk, dv2 = hd.dv;
+  if (tok > 0)
+    REQUIRE(q && k && v && g && beta && d_o && dq && dk && dv && dg && dbeta,
+            "%s: a required pointer is NULL", fn);
+  char* base = (char*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  const int esz = f32 ? 4 : 2;
+  hipError_t e = hipSuccess;
+  if (tok > 0) {
+    e = pad3(q, Hk, dk_dim, base + w.q, Hk, dk2, tok, esz, st);
+    if (e == hipSuccess) e = pad3(k, Hk, dk_dim, base + w.k, Hk, dk2, tok, esz, st);
+    if (e == hipSuccess) e = pad3(v, Hv, dv_dim, base + w.v, Hv, dv2, tok, esz, st);
+    if (e == hipSuccess) e = pad3(d_o, Hv, dv_dim, base + w.dO, Hv, dv2, tok, 4, st);
+  }
+  if (e == hipSuccess && initial_state)
+    e = pad3(initial_state, dk_dim, dv_dim, base + w.s0, dk2, dv2, N * Hv, 4, st);
+  if (e == hipSuccess && d_final_state)
+    e = pad3(d_final_state, dk_dim, dv_dim, base + w.ds, dk2, dv2, N * Hv, 4, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  rc = chunk_bwd_core(fn, base + w.q, base + w.k, base + w.v, in_dtype, g, beta,
+                      initial_state ? (const float*)(base + w.s0) : nullptr, cu_seqlens, N,
+                      (const float*)(base + w.dO),
+                      d_final_state ? (const float*)(base + w.ds) : nullptr, base + w.gq,
+                      base + w.gk, base + w.gv, dg, dbeta,
+                      d_initial_state ? (float*)(base + w.gs0) : nullptr, B, T, Hk, Hv, dk2, dv2,
+                      chunk_size, scale, qk_l2norm, base + w.inner, workspace_bytes - w.inner,
+                      stream);
+  if (rc) return rc;
+  if (tok > 0) {
+    e = pad3(base + w.gq, Hk, dk2, dq, Hk, dk_dim, tok, esz, st);
+    if (e == hipSuccess) e = pad3(base + w.gk, Hk, dk2, dk, Hk, dk_dim, tok, esz, st);
+    if (e == hipSuccess) e = pad3(base + w.gv, Hv, dv2, dv, Hv, dv_dim, tok, esz, st);
+  }
+  if (e == hipSuccess && d_initial_state)
+    e = pad3(base + w.gs0, dk2, dv2, d_initial_state, dk_dim, dv_dim, N * Hv, 4, st);
+  return launch_status(e, fn);
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------- layer backward
@@ -591,22 +941,20 @@ LayerBwdWs layer_bwd_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk
 
 extern "C" {
 
-size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
-                                          int64_t dv, int64_t N) {
-  return layer_bwd_ws(B, T, Hk, Hv, dk, dv, N).total;
-}
+}  // extern "C"
 
-int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,
-                        const float* conv_w, const float* A_log, const float* dt_bias,
-                        const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
-                        const float* initial_state, const void* d_out,
-                        const float* d_final_state, void* d_mixed_qkv, void* dz, void* da,
-                        void* db, float* d_conv_w, float* dA_log, float* d_dt_bias,
-                        float* d_norm_w, float* d_initial_state, int64_t B, int64_t T,
-                        int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t K,
-                        int64_t chunk_size, void* workspace, size_t workspace_bytes,
-                        void* stream) {
-  const char* fn = "omx_gdn_prefill_bwd";
+namespace {
+
+// The layer backward at compiled head dims; dk_real and dv_real as for prefill_core.
+int prefill_bwd_core(const char* fn, const void* mixed_qkv, const void* z, const void* a,
+                     const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
+                     const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                     const float* initial_state, const void* d_out, const float* d_final_state,
+                     void* d_mixed_qkv, void* dz, void* da, void* db, float* d_conv_w,
+                     float* dA_log, float* d_dt_bias, float* d_norm_w, float* d_initial_state,
+                     int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv,
+                     int64_t K, int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                     void* stream, int64_t dk_real, int64_t dv_real) {
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
@@ -623,8 +971,8 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   }
   if (!omx::bwd_dims_supported((int)dk, (int)dv, false) || Hv > 256)
     return fail(OMX_GDN_EUNSUPPORTED,
-                "%s: dk=%lld dv=%lld Hv=%lld not compiled (dk 64/128, dv 64/128, Hv <= 256)", fn,
-                (long long)dk, (long long)dv, (long long)Hv);
+                "%s: dk=%lld dv=%lld Hv=%lld not supported (dk <= 128, dv <= 128, Hv <= 256)",
+                fn, (long long)dk, (long long)dv, (long long)Hv);
   const LayerBwdWs ws = layer_bwd_ws(B, T, Hk, Hv, dk, dv, N);
   REQUIRE(workspace_bytes >= ws.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
           fn, workspace_bytes, ws.total);
@@ -661,6 +1009,7 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   lp.d_norm_w = d_norm_w; lp.tokens = tokens;
   lp.N = (int)N; lp.T = (int)T; lp.Hk = (int)Hk; lp.Hv = (int)Hv; lp.dk = (int)dk; lp.dv = (int)dv;
   lp.conv_dim = (int)(2 * Hk * dk + Hv * dv);
+  lp.dv_mean = (int)dv_real;
   omx::ChunkParams p{};
   p.q = lp.q; p.k = lp.k; p.v = lp.v;
   p.q_ld = Hk * dk; p.k_ld = Hk * dk; p.v_ld = Hv * dv;
@@ -668,7 +1017,7 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   p.initial_state = initial_state; p.final_state = nullptr; p.cu_seqlens = cu_seqlens;
   p.N = (int)N; p.T = (int)T; p.Hk = (int)Hk; p.Hv = (int)Hv; p.dk = (int)dk; p.DV = (int)dv;
   p.nb = (int)(dv / omx::chunk_block_cols());
-  p.scale = 1.0f / sqrtf((float)dk); p.qk_l2norm = 1;
+  p.scale = 1.0f / sqrtf((float)dk_real); p.qk_l2norm = 1;
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
   REQUIRE(((B * T + 63) / 64 + N) * Hv <= INT32_MAX, "%s: grid too large", fn);
   setup_chunked(p, ws.c.f, workspace, omx::kModeBF16);
@@ -703,6 +1052,115 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
   e = omx::launch_bwd(bp, st);
   // gates and conv + SiLU adjoints
   if (e == hipSuccess) e = omx::launch_layer_tail_bwd(lp, st);
+  return launch_status(e, fn);
+}
+
+// Workspace of a padded layer backward: mixed_qkv, z, conv weights, norm weight, the output
+// cotangent, initial state, final-state cotangent and the gradients of mixed_qkv, z, the
+// conv and norm weights and the initial state at the padded dims, then the call's.
+struct LayerBwdPadWs {
+  size_t x, z, cw, nw, dout, s0, ds, gx, gz, gcw, gnw, gs0, inner, total;
+};
+LayerBwdPadWs layer_bwd_pad_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk2,
+                               int64_t dv2, int64_t N) {
+  LayerBwdPadWs w{};
+  if (B < 0 || T < 0 || N < 0) return w;
+  const size_t tok = (size_t)(B * T), cd = (size_t)(2 * Hk * dk2 + Hv * dv2);
+  const size_t st = (size_t)(N * Hv * dk2 * dv2) * 4;
+  Arena a;
+  w.x = a.take(tok * cd * 2);
+  w.z = a.take(tok * Hv * dv2 * 2);
+  w.cw = a.take(cd * 4 * 4);
+  w.nw = a.take(dv2 * 4);
+  w.dout = a.take(tok * Hv * dv2 * 2);
+  w.s0 = a.take(st);
+  w.ds = a.take(st);
+  w.gx = a.take(tok * cd * 2);
+  w.gz = a.take(tok * Hv * dv2 * 2);
+  w.gcw = a.take(cd * 4 * 4);
+  w.gnw = a.take(dv2 * 4);
+  w.gs0 = a.take(st);
+  w.inner = a.off;
+  w.total = w.inner + layer_bwd_ws(B, T, Hk, Hv, dk2, dv2, N).total;
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
+                                          int64_t dv, int64_t N) {
+  const HeadDims hd = head_dims(kLayerBwd, dk, dv, false);
+  if (hd.pad) return layer_bwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N).total;
+  return layer_bwd_ws(B, T, Hk, Hv, dk, dv, N).total;
+}
+
+int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,
+                        const float* conv_w, const float* A_log, const float* dt_bias,
+                        const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
+                        const float* initial_state, const void* d_out,
+                        const float* d_final_state, void* d_mixed_qkv, void* dz, void* da,
+                        void* db, float* d_conv_w, float* dA_log, float* d_dt_bias,
+                        float* d_norm_w, float* d_initial_state, int64_t B, int64_t T,
+                        int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t K,
+                        int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const char* fn = "omx_gdn_prefill_bwd";
+  const HeadDims hd = head_dims(kLayerBwd, dk, dv, false);
+  if (!hd.pad || Hv > 256)
+    return prefill_bwd_core(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps,
+                            cu_seqlens, N, initial_state, d_out, d_final_state, d_mixed_qkv, dz,
+                            da, db, d_conv_w, dA_log, d_dt_bias, d_norm_w, d_initial_state, B, T,
+                            Hk, Hv, dk, dv, K, chunk_size, workspace, workspace_bytes, stream, dk,
+                            dv);
+  int rc = chunk_shape_check(fn, Hk, Hv, dk, dv, chunk_size, B, T, cu_seqlens, N);
+  if (rc) return rc;
+  REQUIRE(K == 4, "%s: conv kernel size must be 4 (got %lld)", fn, (long long)K);
+  const LayerBwdPadWs w = layer_bwd_pad_ws(B, T, Hk, Hv, hd.dk, hd.dv, N);
+  REQUIRE(workspace_bytes >= w.total, "%s: workspace of %zu bytes is smaller than the %zu needed",
+          fn, workspace_bytes, w.total);
+  if (N == 0) return ok();
+  const int64_t tok = B * T, dk2 = hd.dk, dv2 = hd.dv;
+  REQUIRE(conv_w && A_log && dt_bias && norm_w && d_conv_w && dA_log && d_dt_bias && d_norm_w,
+          "%s: a parameter or parameter-gradient pointer is NULL", fn);
+  if (tok > 0)
+    REQUIRE(mixed_qkv && z && a && b && d_out && d_mixed_qkv && dz && da && db,
+            "%s: an activation or activation-gradient pointer is NULL", fn);
+  REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
+          fn);
+  char* base = (char*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (tok > 0) {
+    e = pad_channels(mixed_qkv, dk, dv, base + w.x, dk2, dv2, Hk, Hv, tok, 1, 2, st);
+    if (e == hipSuccess) e = pad3(z, Hv, dv, base + w.z, Hv, dv2, tok, 2, st);
+    if (e == hipSuccess) e = pad3(d_out, Hv, dv, base + w.dout, Hv, dv2, tok, 2, st);
+  }
+  if (e == hipSuccess) e = pad_channels(conv_w, dk, dv, base + w.cw, dk2, dv2, Hk, Hv, 1, K, 4, st);
+  if (e == hipSuccess) e = pad3(norm_w, 1, dv, base + w.nw, 1, dv2, 1, 4, st);
+  if (e == hipSuccess && initial_state)
+    e = pad3(initial_state, dk, dv, base + w.s0, dk2, dv2, N * Hv, 4, st);
+  if (e == hipSuccess && d_final_state)
+    e = pad3(d_final_state, dk, dv, base + w.ds, dk2, dv2, N * Hv, 4, st);
+  if (e != hipSuccess) return launch_status(e, fn);
+  rc = prefill_bwd_core(fn, base + w.x, base + w.z, a, b, (const float*)(base + w.cw), A_log,
+                        dt_bias, (const float*)(base + w.nw), eps, cu_seqlens, N,
+                        initial_state ? (const float*)(base + w.s0) : nullptr, base + w.dout,
+                        d_final_state ? (const float*)(base + w.ds) : nullptr, base + w.gx,
+                        base + w.gz, da, db, (float*)(base + w.gcw), dA_log, d_dt_bias,
+                        (float*)(base + w.gnw), d_initial_state ? (float*)(base + w.gs0) : nullptr,
+                        B, T, Hk, Hv, dk2, dv2, K, chunk_size, base + w.inner,
+                        workspace_bytes - w.inner, stream, dk, dv);
+  if (rc) return rc;
+  if (tok > 0) {
+    e = pad_channels(base + w.gx, dk2, dv2, d_mixed_qkv, dk, dv, Hk, Hv, tok, 1, 2, st);
+    if (e == hipSuccess) e = pad3(base + w.gz, Hv, dv2, dz, Hv, dv, tok, 2, st);
+  }
+  if (e == hipSuccess) e = pad_channels(base + w.gcw, dk2, dv2, d_conv_w, dk, dv, Hk, Hv, 1, K, 4, st);
+  if (e == hipSuccess) e = pad3(base + w.gnw, 1, dv2, d_norm_w, 1, dv, 1, 4, st);
+  if (e == hipSuccess && d_initial_state)
+    e = pad3(base + w.gs0, dk2, dv2, d_initial_state, dk, dv, N * Hv, 4, st);
   return launch_status(e, fn);
 }
 

@@ -839,7 +839,7 @@ int chunk_record_bytes(int mode) { return rec_bytes(mode); }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
   if (dv % kBlockCols != 0 || dv > 256) return false;
-  if (f32_inputs) return dk == 32 || dk == 64;
+  if (f32_inputs) return dk == 32 || dk == 64 || dk == 128;
   return dk == 64 || dk == 128;
 }
 
@@ -862,6 +862,7 @@ hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream) {
   if (mode == MODE_F32) {
     if (p.dk == 64) return launch_scan_cfg<64, MODE_F32>(p, stream);
     if (p.dk == 32) return launch_scan_cfg<32, MODE_F32>(p, stream);
+    if (p.dk == 128) return launch_scan_cfg<128, MODE_F32>(p, stream);
     return hipErrorInvalidValue;
   }
   if (mode == MODE_LAYER) {

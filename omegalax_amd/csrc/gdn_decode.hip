@@ -45,7 +45,7 @@ __device__ __forceinline__ void store_st(float* p, float4 x) {
   else *(float4*)p = x;
 }
 
-template <int DK, int DV, bool LAYER, typename InT, bool NT>
+template <int DK, int DV, bool LAYER, typename InT, bool NT, bool EARLY>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   constexpr int CG = DV / 4;            // column groups of 4
   constexpr int RG = kThreads / CG;     // row groups
@@ -56,6 +56,26 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int gqa = p.Hv / p.Hk;
+  const int cg = tid % CG, rg = tid / CG;
+
+  // With EARLY the state reads are issued first, so they stream in while the conv, the
+  // norms and their barriers run; otherwise they follow the conv.  The next value head's
+  // state is loaded while the current one is reduced and updated, so a workgroup keeps
+  // two heads' state reads in flight.
+  auto load_state = [&](int hh, float4* st) {
+    const float* S = p.state + ((size_t)b * p.Hv + hk * gqa + hh) * DK * DV;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int row = rg + r * RG;
+      if (row < DK) st[r] = load_st<NT>(S + (size_t)row * DV + 4 * cg);
+      else st[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float4 st[R], stn[R];
+  if (EARLY) {
+    load_state(0, st);
+    if (gqa > 1) load_state(1, stn);
+  }
 
   __shared__ __align__(16) float s_q[DK];
   __shared__ __align__(16) float s_k[DK];
@@ -156,24 +176,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   }
   lds_barrier();
   const float qk = s_scal[2];
+  if (!EARLY) {
+    load_state(0, st);
+    if (gqa > 1) load_state(1, stn);
+  }
 
-  const int cg = tid % CG, rg = tid / CG;
-  // The state of value head hh + 1 is loaded while head hh is reduced and updated,
-  // so a workgroup keeps two heads' state reads in flight.
-  auto load_state = [&](int hh, float4* st) {
-    const float* S = p.state + ((size_t)b * p.Hv + hk * gqa + hh) * DK * DV;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int row = rg + r * RG;
-      if (row < DK) st[r] = load_st<NT>(S + (size_t)row * DV + 4 * cg);
-      else st[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  };
-  float4 st[R], stn[R];
-  load_state(0, st);
   for (int hh = 0; hh < gqa; ++hh) {
     const int h = hk * gqa + hh;
-    if (hh + 1 < gqa) load_state(hh + 1, stn);
+    if (hh > 0 && hh + 1 < gqa) load_state(hh + 1, stn);
     float alpha, beta;
     if (LAYER) {
       const float av = bf2f(((const bf16_t*)p.a)[(size_t)b * p.Hv + h]);
@@ -263,30 +273,35 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   }
 }
 
-template <int DK, int DV, bool NT>
-void launch_nt(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
+template <int DK, int DV, bool NT, bool EARLY>
+void launch_cfg(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
   dim3 grid(p.Hk, p.B);
   if (layer) {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t, NT>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t, NT, EARLY>), grid, dim3(kThreads), 0,
+                       stream, p);
   } else if (in_bf16) {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, false, bf16_t, NT>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, bf16_t, NT, EARLY>), grid, dim3(kThreads), 0,
+                       stream, p);
   } else {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, false, float, NT>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, float, NT, EARLY>), grid, dim3(kThreads), 0,
+                       stream, p);
   }
 }
 
-// A decode loop reads and rewrites the whole state every step.  A state that fits
-// the last-level cache (MI355X: 256 MB Infinity Cache) stays resident from step to
-// step through ordinary accesses; a larger one is streamed with non-temporal
-// accesses so that it does not thrash that cache (measured at C2: B=64 at 128 MB
-// gains from residency, B=256 at 512 MB from streaming).
-constexpr size_t kStreamStateBytes = 192u << 20;
+// The state is read once and written once per step and is not touched again until the
+// layer's next token, after every other layer's state has streamed through: accesses are
+// non-temporal so they do not evict the conv cache and the token rows from the caches.
+// (Measured at C2 with the state rotated over 512 MiB, as in a multi-layer decode: B=64
+// 72.8 us with ordinary accesses, 56.8 us streamed; B=256 198.5 vs 197.9 us.)  Issuing the
+// state reads before the conv pays when the grid is at most two rounds of the chip's
+// resident workgroups (B=64: 56.8 -> 54.5 us) and costs when it is more (B=256: 197.0 ->
+// 209.4 us, the conv's small loads then queue behind a saturated stream).
+constexpr long long kEarlyMaxWorkgroups = 2048;
 
 template <int DK, int DV>
 hipError_t launch_dims(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
-  const size_t state_bytes = (size_t)p.B * p.Hv * DK * DV * sizeof(float);
-  if (state_bytes > kStreamStateBytes) launch_nt<DK, DV, true>(p, layer, in_bf16, stream);
-  else launch_nt<DK, DV, false>(p, layer, in_bf16, stream);
+  if ((long long)p.B * p.Hk <= kEarlyMaxWorkgroups) launch_cfg<DK, DV, true, true>(p, layer, in_bf16, stream);
+  else launch_cfg<DK, DV, true, false>(p, layer, in_bf16, stream);
   return hipGetLastError();
 }
 

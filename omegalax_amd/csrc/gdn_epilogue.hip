@@ -4,7 +4,9 @@
 // output: out = w * o * rsqrt(mean(o^2) + eps) * silu(z).  The chunked scan
 // writes o in bf16; this kernel forms mean(o^2) from those values (the row's
 // bf16 rounding moves the norm by at most 2^-9 relative) and applies the norm.
-// Memory-bound: two bf16 reads and one bf16 write per element.  A row is handled by
+// Memory-bound: two bf16 reads and one bf16 write per element.  The mean divides by
+// dv_mean, the caller's dv when the rows are zero-padded copies (their extra columns
+// are zero and add nothing to the sum of squares).  A row is handled by
 // a group of G lanes (G = dv / 8 rounded up to a power of two, at most 32), one
 // thread per 8 columns (16-byte accesses); the row's sum of squares is a butterfly
 // over the group.
@@ -20,7 +22,8 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
                                                             const uint4* __restrict__ z,
                                                             const float* __restrict__ norm_w,
                                                             uint4* __restrict__ out,
-                                                            long long rows, int dv, float eps) {
+                                                            long long rows, int dv, float inv_dv,
+                                                            float eps) {
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
   const long long row = gid / G;
   const int j = (int)(gid % G);  // octet of the row
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
 #pragma unroll
   for (int m = 1; m < G; m <<= 1) ss += __shfl_xor(ss, m, G);
   if (!active) return;
-  const float rn = rsqrtf(ss / (float)dv + eps);
+  const float rn = rsqrtf(ss * inv_dv + eps);
   const int c = 8 * j;
   const float4 w0 = *(const float4*)(norm_w + c), w1 = *(const float4*)(norm_w + c + 4);
   const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -62,23 +65,25 @@ __global__ __launch_bounds__(256) void norm_epilogue_kernel(const uint4* __restr
 
 template <int G>
 hipError_t launch_g(const void* o_part, const void* z, const float* norm_w, void* out,
-                    long long rows, int dv, float eps, hipStream_t stream) {
+                    long long rows, int dv, int dv_mean, float eps, hipStream_t stream) {
   const long long threads = rows * G;
   const unsigned grid = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL((norm_epilogue_kernel<G>), dim3(grid), dim3(256), 0, stream,
-                     (const uint4*)o_part, (const uint4*)z, norm_w, (uint4*)out, rows, dv, eps);
+                     (const uint4*)o_part, (const uint4*)z, norm_w, (uint4*)out, rows, dv,
+                     1.0f / (float)dv_mean, eps);
   return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_norm_epilogue(const void* o_part, const void* z, const float* norm_w, void* out,
-                                long long rows, int dv, float eps, hipStream_t stream) {
+                                long long rows, int dv, int dv_mean, float eps,
+                                hipStream_t stream) {
   if (rows == 0) return hipSuccess;
   const int per_row = dv / 8;
-  if (per_row <= 8) return launch_g<8>(o_part, z, norm_w, out, rows, dv, eps, stream);
-  if (per_row <= 16) return launch_g<16>(o_part, z, norm_w, out, rows, dv, eps, stream);
-  if (per_row <= 32) return launch_g<32>(o_part, z, norm_w, out, rows, dv, eps, stream);
+  if (per_row <= 8) return launch_g<8>(o_part, z, norm_w, out, rows, dv, dv_mean, eps, stream);
+  if (per_row <= 16) return launch_g<16>(o_part, z, norm_w, out, rows, dv, dv_mean, eps, stream);
+  if (per_row <= 32) return launch_g<32>(o_part, z, norm_w, out, rows, dv, dv_mean, eps, stream);
   return hipErrorInvalidValue;
 }
 

@@ -182,6 +182,7 @@ struct LayerBwdParams {
   const int32_t* cu_seqlens;
   long long tokens;
   int N, T, Hk, Hv, dk, dv, conv_dim;
+  int dv_mean;                 // divisor of the norm's means (dv, or the real dv of padded rows)
 };
 int layer_bwd_norm_blocks();
 long long layer_bwd_conv_blocks(long long tokens);
@@ -191,9 +192,23 @@ hipError_t launch_layer_norm_bwd(const LayerBwdParams& p, hipStream_t stream);
 hipError_t launch_layer_tail_bwd(const LayerBwdParams& p, hipStream_t stream);
 
 // Gated RMSNorm of the layer prefill from bf16 o: out = w * o * rsqrt(mean(o^2) + eps)
-// * silu(z) per (token, value head) row of dv (dv / 8 at most 32).
+// * silu(z) per (token, value head) row of dv (dv / 8 at most 32); the mean divides the
+// row's sum of squares by dv_mean.
 hipError_t launch_norm_epilogue(const void* o_part, const void* z, const float* norm_w, void* out,
-                                long long rows, int dv, float eps, hipStream_t stream);
+                                long long rows, int dv, int dv_mean, float eps,
+                                hipStream_t stream);
+
+// An [R][G][E] view of a buffer for launch_pad_copy: element pointer, group and element
+// counts, row and group strides (elements).
+struct PadView {
+  const void* p;
+  int G, E;
+  long long rs, gs;
+};
+// dst[r][g][e] = (g < src.G && e < src.E) ? src[r][g][e] : 0 for g < dst.G, e < dst.E;
+// esize 2 (bf16) or 4 (fp32) bytes (gdn_pad.hip)
+hipError_t launch_pad_copy(const PadView& src, const PadView& dst, long long R, int esize,
+                           hipStream_t stream);
 
 bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();

@@ -178,7 +178,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_kernel(LayerBwdParams p) {
     float ss = o[0] * o[0] + o[1] * o[1];
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) ss += __shfl_xor(ss, s);
-    const float rr = rsqrtf(ss / (float)dv + p.eps);
+    const float rr = rsqrtf(ss / (float)p.dv_mean + p.eps);
     float n[2], dn[2], dzv[2], dnn = 0.f;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(NT) void norm_bwd_kernel(LayerBwdParams p) {
     }
 #pragma unroll
     for (int s = 1; s < 64; s <<= 1) dnn += __shfl_xor(dnn, s);
-    const float m = dnn / (float)dv;
+    const float m = dnn / (float)p.dv_mean;
     if (in) {
       *(uint32_t*)(p.dz + r * dv + c) = pack_bf16(dzv[0], dzv[1]);
       *(float2*)(p.dO + r * dv + c) = float2{rr * (dn[0] - n[0] * m), rr * (dn[1] - n[1] * m)};

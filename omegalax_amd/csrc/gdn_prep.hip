@@ -811,6 +811,7 @@ hipError_t launch_prep(const ChunkParams& p, int mode, hipStream_t stream) {
   if (mode == MODE_F32) {
     if (p.dk == 64) return launch_prep_cfg<64, MODE_F32>(p, stream);
     if (p.dk == 32) return launch_prep_cfg<32, MODE_F32>(p, stream);
+    if (p.dk == 128) return launch_prep_cfg<128, MODE_F32>(p, stream);
     return hipErrorInvalidValue;
   }
   if (mode == MODE_LAYER) {

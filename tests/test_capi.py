@@ -174,9 +174,10 @@ def _bwd(ws, ws_bytes, **over):
     (dict(do=None), _lib.EINVAL, "NULL"),
     (dict(dg=None), _lib.EINVAL, "NULL"),
     (dict(Hv=5), _lib.EINVAL, "multiple of key heads"),
-    (dict(dkd=96), _lib.EUNSUPPORTED, "not compiled"),
-    (dict(dvd=256), _lib.EUNSUPPORTED, "not compiled"),
-    (dict(dt=_lib.F32), _lib.EUNSUPPORTED, "not compiled"),  # fp32 inputs: dk 32/64 only
+    (dict(dkd=256), _lib.EUNSUPPORTED, "not supported"),
+    (dict(dvd=256), _lib.EUNSUPPORTED, "not supported"),
+    (dict(dt=_lib.F32), _lib.EUNSUPPORTED, "not supported"),  # fp32 inputs: dk <= 64
+    (dict(dkd=96, ws_bytes=_bwd_ws_size()), _lib.EINVAL, "workspace"),  # padded: more workspace
 ])
 def test_chunk_bwd_rejects_bad_arguments(over, code, msg):
     args = dict(ws=256, ws_bytes=_bwd_ws_size())
@@ -209,6 +210,38 @@ def test_prefill_bwd_rejects_bad_arguments(over, code, msg):
     rc, err = _prefill_bwd(**over)
     assert rc == code, err
     assert msg in err
+
+
+@pytest.mark.parametrize("dk,dv,f32", [(16, 32, False), (96, 80, False), (16, 32, True),
+                                       (128, 64, True), (20, 24, True)])
+def test_uncompiled_head_dims_run_padded_with_more_workspace(dk, dv, f32):
+    """Head dims the kernels are not compiled for run on zero-padded copies: the workspace
+    holds the padded buffers on top of the padded call's own workspace."""
+    L = _lib.lib()
+    dt = _lib.F32 if f32 else _lib.BF16
+    dk2 = 32 if (f32 and dk <= 32) else (64 if dk <= 64 else 128)
+    dv2 = (dv + 63) // 64 * 64
+    direct = L.omx_gdn_chunk_fwd_workspace_size(2, 100, 2, 4, dk2, dv2, 2, dt)
+    padded = L.omx_gdn_chunk_fwd_workspace_size(2, 100, 2, 4, dk, dv, 2, dt)
+    if (dk2, dv2) == (dk, dv):
+        assert padded == direct
+    else:
+        esz = 4 if f32 else 2
+        extra = 200 * (2 * 2 * dk2 + 4 * dv2) * esz + 200 * 4 * dv2 * 4 + 2 * 2 * 4 * dk2 * dv2 * 4
+        assert padded >= direct + extra
+    if not f32:
+        assert (L.omx_gdn_prefill_workspace_size(2, 100, 2, 4, dk, dv, 2)
+                > L.omx_gdn_prefill_workspace_size(2, 100, 2, 4, dk2, dv2, 2))
+
+
+def test_head_dims_beyond_every_compiled_size_are_unsupported():
+    L = _lib.lib()
+    ws = L.omx_gdn_chunk_fwd_workspace_size(1, 64, 1, 1, 256, 64, 1, _lib.BF16)
+    rc, err = _chunk(256, ws, B=1, T=64, N=1, Hk=1, Hv=1, dk=256, dv=64)
+    assert rc == _lib.EUNSUPPORTED and "not supported" in err
+    ws = L.omx_gdn_chunk_fwd_workspace_size(1, 64, 1, 1, 64, 320, 1, _lib.BF16)
+    rc, err = _chunk(256, ws, B=1, T=64, N=1, Hk=1, Hv=1, dk=64, dv=320)
+    assert rc == _lib.EUNSUPPORTED and "not supported" in err
 
 
 def test_prefill_noalloc_rejects_shapes_beyond_its_fixed_scratch():

@@ -103,6 +103,11 @@ CASES = [
     (2, 150, 1, 2, 64, 64, "f32"),
     (1, 70, 2, 2, 32, 128, "f32"),
     (1, 120, 1, 6, 128, 64, "bf16"),  # gqa 6
+    # head dims the kernels are not compiled for run on zero-padded copies: the
+    # reference's smoke layout (config.py:94-101), and odd sizes
+    (2, 100, 2, 4, 16, 32, "bf16"),
+    (2, 100, 2, 4, 16, 32, "f32"),
+    (1, 130, 1, 2, 96, 80, "bf16"),
 ]
 
 

@@ -61,6 +61,8 @@ def ref_prefill(d, dims, cu=None, S0=None, conv0=None):
     (1, 200, 2, 2, 64, 128),
     (1, 130, 1, 2, 128, 64),
     (1, 100, 1, 6, 128, 64),    # gqa 6: gate inputs restaged past the prefetched four
+    (2, 33, 2, 4, 16, 32),      # the reference's smoke layout, on zero-padded copies
+    (1, 150, 1, 2, 96, 80),
 ])
 def test_layer_prefill_matches_oracle(B, T, Hk, Hv, dk, dv):
     say(f"layer B={B} T={T} Hk={Hk} Hv={Hv} dk={dk} dv={dv}")
@@ -74,17 +76,18 @@ def test_layer_prefill_matches_oracle(B, T, Hk, Hv, dk, dv):
     assert np.array_equal(np_(conv), conv_ref)
 
 
-def test_layer_varlen_with_carried_states():
-    say("layer varlen")
-    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+@pytest.mark.parametrize("dk,dv", [(128, 128), (16, 32)])
+def test_layer_varlen_with_carried_states(dk, dv):
+    say(f"layer varlen dk={dk} dv={dv}")
+    dims = dict(Hk=2, dk=dk, Hv=4, dv=dv)
     lens = [70, 0, 2, 129, 64]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     T = int(cu[-1])
     d = W.layer_inputs(1, T, **dims, seed=5)
     rng = np.random.default_rng(6)
     N = len(lens)
-    S0 = (0.02 * rng.standard_normal((N, 4, 128, 128))).astype(np.float32)
-    conv_dim = 2 * 2 * 128 + 4 * 128
+    S0 = (0.02 * rng.standard_normal((N, 4, dk, dv))).astype(np.float32)
+    conv_dim = 2 * 2 * dk + 4 * dv
     conv0 = O.round_bf16(rng.standard_normal((N, conv_dim, 3)))
     t = W.to_device(d)
     out, S, conv = gpu_prefill(t, dims, cu, S0, conv0)

@@ -8,9 +8,10 @@ loader.py:173-190, 285-307), the layer runs in bf16 on the GPU
 gated_deltanet_prefill_cache then gated_deltanet_decode), and its output is held to
 * the oracle's layer with the reference's bf16 rounding points, on the GPU's own
   bf16 projection outputs: 2e-2 (max-abs-normalised) -- the parity bar;
-* the fixture's fp32 output itself: 2e-2 at dk=dv=128.  At dk=dv=64 (D=16) the
-  oracle's exact-rounding bf16 emulation is itself 1.8e-2 from the fp32 module, so the
-  bound there is 3e-2: what any bf16 run of the reference would need.
+* the fixture's fp32 output itself: 2e-2 at dk=dv=128.  At dk=dv=64 and at the
+  reference's smoke layout dk=16, dv=32 (both with D=16) the oracle's exact-rounding
+  bf16 emulation is itself 1.8e-2 and 4.7e-2 from the fp32 module, so the bounds there
+  are 3e-2 and 7e-2: what any bf16 run of the reference would need.
 """
 import os
 import sys
@@ -25,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 BF16_TOL = 2e-2
-HF_TOL = {"layer_d128": 2e-2, "layer_d64": 3e-2}
+HF_TOL = {"layer_d128": 2e-2, "layer_d64": 3e-2, "layer_smoke_d16": 7e-2}
 
 
 def rel(a, b):

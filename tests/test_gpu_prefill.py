@@ -88,6 +88,13 @@ CASES = [
     (1, 70, 2, 2, 32, 128, "f32"),
     (1, 150, 1, 6, 128, 64, "bf16"),  # more value heads per key head than the prep prefetches
     (1, 90, 1, 8, 64, 64, "f32"),
+    (2, 100, 2, 2, 128, 128, "f32"),  # fp32 inputs at the Qwen3.5 head dims
+    # head dims the kernels are not compiled for run on zero-padded copies: the
+    # reference's smoke layout (config.py:94-101), and odd sizes
+    (2, 100, 2, 4, 16, 32, "bf16"),
+    (2, 100, 2, 4, 16, 32, "f32"),
+    (1, 130, 1, 2, 96, 80, "bf16"),
+    (1, 70, 2, 2, 48, 200, "f32"),
 ]
 
 
