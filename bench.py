@@ -9,6 +9,7 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
            d=128.  A "step" is one omx_gdn_prefill call over the whole batch.  The line
            also carries C3, C4, the C2 decode step at B=64 and B=256, the backward passes
            and the whole layer with its projections, each under its own key.
+  c1       the C1 leg of the headline alone (the layer step and the core call).
   decode   config C2: one cached decode step (conv cache + fp32 state in place) at
            --decode-batch, rotating through enough state sets that no step finds its state
            in the 256 MB last-level cache.
@@ -177,10 +178,13 @@ def cpu_decode_baseline(B=8, budget_s=10.0):
 # scaled by a plain copy kernel's counters), for the shapes they were taken on, with the
 # profiles/ summary that gives the commands and per-kernel figures.
 MEASURED_TRAFFIC = {
-    ("core", 4, 4096, 16, 32, 128): (1_154_719_808, "profiles/prefill_c1.md (core call)"),
-    ("decode", 64, 16, 32, 128): (277_401_702, "profiles/decode_step_c2_b64.md"),
-    # layer step: prep 303.3 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
-    ("prefill", 4, 4096, 16, 32, 128): (1_712_750_182, "profiles/prefill_c1.md (layer kernels)"),
+    ("core", 4, 4096, 16, 32, 128): (1_154_299_392, "profiles/prefill_c1.md (core call)"),
+    ("core", 1, 65536, 16, 64, 128): (7_707_787_264, "profiles/prefill_c3_c4.md (C4 core call)"),
+    ("decode", 64, 16, 32, 128): (277_278_720, "profiles/decode_step_c2.md (B=64)"),
+    ("decode", 256, 16, 32, 128): (1_107_987_251, "profiles/decode_step_c2.md (B=256)"),
+    # layer step: prep 303.2 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
+    ("prefill", 4, 4096, 16, 32, 128): (1_712_742_400, "profiles/prefill_c1.md (layer kernels)"),
+    ("c3", 32768, 8): (3_483_595_776, "profiles/prefill_c3_c4.md (C3 layer call)"),
 }
 
 
@@ -395,12 +399,14 @@ def bench_c3(steps, warmup, total=32768, n=8):
     wall, ms = time_launches(step, steps, warmup)
     flops = prefill_flops_per_token_head(d, d) * total * Hv
     tf = flops / (ms * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get(("c3", total, n))
     return {"config": f"C3 packed layer prefill T={total}, {n} sequences "
                       f"(lengths {lens.tolist()}), initial states, Hk=16 Hv=32 d=128",
             "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
             "tokens_per_s": total * steps / wall,
             "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
+                         "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                         "traffic": traffic and traffic[0], "traffic_source": traffic and traffic[1],
                          "algorithmic_flops": flops,
                          "kernels": "the launches of one gdn_prefill call"}}
 
@@ -445,8 +451,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=["prefill", "decode", "c3", "core", "bwd", "layer_bwd",
-                                           "layer_module", "copy"],
+    ap.add_argument("--workload", choices=["prefill", "c1", "decode", "c3", "core", "bwd",
+                                           "layer_bwd", "layer_module", "copy"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -508,6 +514,17 @@ def main():
                     core["roofline"]["achieved"], "TFLOP/s", K, W_, core["ms_per_step"], "bf16",
                     {"workload": core["config"], "chunk": C}, roofline=core["roofline"],
                     kernel_ms=core["kernel_ms"]), flush=True)
+        return 0
+    if args.workload == "c1":
+        pre = bench_prefill(K, W_, cpu)
+        extra = {"roofline": pre["roofline"], "step_event_ms": pre["step_event_ms"],
+                 "core": {k_: pre["core"][k_] for k_ in ("config", "kernel_ms", "roofline")}}
+        if cpu:
+            extra["cpu_baseline"] = pre["cpu_baseline"]
+        print(_line("C1 GDN layer prefill tokens/s", pre["tokens_per_s"], "tokens/s", K, W_,
+                    pre["ms_per_step"], "bf16",
+                    {"workload": "C1 GDN layer prefill B=4 T=4096 Hk=16 Hv=32 d=128"}, **extra),
+              flush=True)
         return 0
     if args.workload == "c3":
         res = bench_c3(K, W_)

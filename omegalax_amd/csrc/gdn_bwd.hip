@@ -318,8 +318,8 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nb = p.nb, wid = blockIdx.x;
-  const int blk = wid % nb, h = (wid / nb) % p.Hv, n = wid / (nb * p.Hv);
+  const ScanItem item = scan_item(p.seq_order, p.N, p.Hk, p.Hv, p.nb);
+  const int blk = item.blk, h = item.h, n = item.n;
   const int gqa = p.Hv / p.Hk, hk = h / gqa;
   const int DV = p.DV, col0 = 64 * blk, c = 16 * wave;
   long long s0, s1;

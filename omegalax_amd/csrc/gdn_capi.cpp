@@ -57,7 +57,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // sums of o^2 for the gated norm, and the plan of packed sequences (chunk offsets and
 // the ordered copy of cu_seqlens the kernels read).
 struct ChunkWs {
-  size_t rec, kn, qn, vc, opart, off, cu, total;
+  size_t rec, kn, qn, vc, opart, off, cu, ord, total;
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
@@ -84,6 +84,8 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
   o += align_up((size_t)(N + 1) * 4, 256);
   w.cu = o;
   o += align_up((size_t)(N + 1) * 4, 256);
+  w.ord = o;
+  o += align_up((size_t)N * 4, 256);
   w.total = o;
   return w;
 }
@@ -276,6 +278,7 @@ void setup_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int 
   p.chunk_off = p.cu_seqlens ? (int32_t*)(base + ws.off) : nullptr;
   // the kernels after the plan read its ordered copy of the offsets
   p.cu_in = p.cu_seqlens;
+  p.seq_order = p.cu_seqlens ? (const int32_t*)(base + ws.ord) : nullptr;
   if (p.cu_seqlens) p.cu_seqlens = (const int32_t*)(base + ws.cu);
   const bool norm = p.qk_l2norm || mode == omx::kModeLayer;
   p.kn = norm ? base + ws.kn : nullptr;
@@ -784,7 +787,7 @@ int chunk_bwd_core(const char* fn, const void* q, const void* k, const void* v, 
   b.dkh = base + ws.dkh;
   b.dv = dv; b.dg = dg; b.dbeta = dbeta;
   b.q = q; b.k = k; b.dq = dq; b.dk_out = dk;
-  b.cu_seqlens = p.cu_seqlens; b.chunk_off = p.chunk_off;
+  b.cu_seqlens = p.cu_seqlens; b.chunk_off = p.chunk_off; b.seq_order = p.seq_order;
   b.N = p.N; b.T = p.T; b.Hk = p.Hk; b.Hv = p.Hv; b.dk = p.dk; b.DV = p.DV; b.nb = p.nb;
   b.nch = p.nch; b.n_rec = p.n_rec; b.in_f32 = f32 ? 1 : 0; b.qk_l2norm = p.qk_l2norm;
   b.scale = scale;
@@ -1046,7 +1049,7 @@ int prefill_bwd_core(const char* fn, const void* mixed_qkv, const void* z, const
   bp.dkh = base + ws.c.dkh;
   bp.dv = lp.grad_v; bp.dg = (float*)(base + ws.dg); bp.dbeta = (float*)(base + ws.dbeta);
   bp.q = lp.q; bp.k = lp.k; bp.dq = lp.grad_q; bp.dk_out = lp.grad_k;
-  bp.cu_seqlens = p.cu_seqlens; bp.chunk_off = p.chunk_off;
+  bp.cu_seqlens = p.cu_seqlens; bp.chunk_off = p.chunk_off; bp.seq_order = p.seq_order;
   bp.N = p.N; bp.T = p.T; bp.Hk = p.Hk; bp.Hv = p.Hv; bp.dk = p.dk; bp.DV = p.DV; bp.nb = p.nb;
   bp.nch = p.nch; bp.n_rec = p.n_rec; bp.in_f32 = 0; bp.qk_l2norm = 1; bp.scale = p.scale;
   e = omx::launch_bwd(bp, st);

@@ -172,4 +172,37 @@ __device__ __forceinline__ void seq_range(const int32_t* cu, int n, int T, long 
   }
 }
 
+// Work item of a workgroup of the scans (forward and reverse): sequence n, value head h
+// and column block blk, from blockIdx.x.  The workgroups of one key head of one sequence
+// (gqa value heads x nb blocks, which read the same q/k rows) form a group that runs on
+// one XCD (the hardware deals workgroup i to XCD i % 8), so they share its L2.  When the
+// group count is a multiple of 8, group ranks are dealt round-robin over the XCDs in the
+// order of `order` (sequences longest first; null = index order): every XCD gets a share
+// of every sequence and starts its longest chains first.  Otherwise each XCD takes a
+// contiguous range of groups in index order.
+struct ScanItem {
+  int n, h, blk;
+};
+__device__ __forceinline__ ScanItem scan_item(const int32_t* order, int N, int Hk, int Hv,
+                                              int nb) {
+  const int gqa = Hv / Hk, G = gqa * nb, NG = N * Hk;
+  const unsigned b = blockIdx.x, xcd = b % 8, slot = b / 8;
+  int grp, member;
+  if (NG % 8 == 0) {
+    grp = 8 * (int)(slot / G) + (int)xcd;
+    member = (int)(slot % G);
+  } else {
+    const unsigned nwg = gridDim.x, per = nwg / 8, rem = nwg % 8;
+    const int wid = (int)(xcd * per + (xcd < rem ? xcd : rem) + slot);
+    grp = wid / G;
+    member = wid % G;
+  }
+  const int sr = grp / Hk;
+  ScanItem it;
+  it.n = order ? order[sr] : sr;
+  it.h = (grp % Hk) * gqa + member / nb;
+  it.blk = member % nb;
+  return it;
+}
+
 }  // namespace omx

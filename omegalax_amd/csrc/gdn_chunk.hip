@@ -302,16 +302,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = DIRECT && wave == NWC;  // issues the direct loads, computes nothing
-  // XCD-aware numbering: workgroups are dealt round-robin over the 8 XCDs
-  // (blockIdx % 8); renumber so that consecutive work items -- the gqa x nb
-  // workgroups reading the same key head's q/k -- run on one XCD and share its L2.
-  const unsigned nwg = gridDim.x, xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
-  const unsigned per = nwg / 8, rem = nwg % 8;
-  const int wid = (int)(xcd * per + (xcd < rem ? xcd : rem) + slot);
-  const int nb = p.nb;
-  const int blk = wid % nb;
-  const int h = (wid / nb) % p.Hv;
-  const int n = wid / (nb * p.Hv);
+  // XCD-aware work item (scan_item): a key head's workgroups share one XCD's L2, and
+  // packed sequences start longest first
+  const ScanItem item = scan_item(p.seq_order, p.N, p.Hk, p.Hv, p.nb);
+  const int blk = item.blk, h = item.h, n = item.n;
   const int gqa = p.Hv / p.Hk;
   const int hk = h / gqa;
   const int DV = p.DV;

@@ -73,6 +73,7 @@ struct ChunkParams {
   void* vc;                    // layer: conv + SiLU output of v [tokens, Hv, DV] bf16
   unsigned char* rec;          // per (chunk, value head) records, layout in gdn_chunk.h
   int32_t* chunk_off;          // cu_seqlens: [N+1] first chunk index of each sequence; else null
+  const int32_t* seq_order;    // cu_seqlens: [N] sequences, longest first (the plan); else null
   int nch;                     // chunks per sequence without cu_seqlens
   int n_rec;                   // chunk slots the preparation kernel covers
   // the scan's k, q, v rows: kn/qn/vc or the raw inputs, with row strides (elements)
@@ -114,6 +115,7 @@ struct BwdParams {
   void* dk_out;
   const int32_t* cu_seqlens;
   const int32_t* chunk_off;
+  const int32_t* seq_order;
   int N, T, Hk, Hv, dk, DV, nb, nch, n_rec, in_f32, qk_l2norm;
   float scale;
 };

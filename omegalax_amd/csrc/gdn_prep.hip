@@ -330,8 +330,8 @@ __device__ __forceinline__ void load_task_inputs(const ChunkParams& p, const Pre
 // that prefetched the next task into registers needed about 80 more registers, so
 // only two fitted, and was slower.  fp32 inputs stage hi and lo rows, whose LDS allows
 // two workgroups.
-template <int MODE>
-constexpr int prep_blocks_per_cu() { return MODE == MODE_F32 ? 2 : 3; }
+template <int DK, int MODE>
+constexpr int prep_blocks_per_cu() { return MODE == MODE_F32 ? (DK == 128 ? 1 : 2) : 3; }
 
 // A-layout 16x16 fp32 tile (lane (q, r) holds M[16 bi + r][16 bj + 4q .. +3]) into a
 // row-major 64x64 matrix
@@ -344,7 +344,7 @@ __device__ __forceinline__ void put_f32_tile(float* m, int bi, int bj, f32x4 a) 
 // (X^T with X = (I + L)^-1, Lg = strict_lower(K K^T * Gamma), P, and G; layout in
 // gdn_chunk.h).
 template <int DK, int MODE, bool BWD = false>
-__global__ __launch_bounds__(NT, prep_blocks_per_cu<MODE>()) void prep_kernel(ChunkParams p) {
+__global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_kernel(ChunkParams p) {
   using Q_ = PrepCfg<DK, MODE>;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, F32 = MODE == MODE_F32;
@@ -727,11 +727,17 @@ hipError_t launch_prep_cfg(const ChunkParams& p, hipStream_t stream) {
 //    c[n] = max(c[n-1], clamp(cu[n], 0, T)) (a running maximum), so the sequences are
 //    ordered, disjoint and tile [0, T) whatever the caller's array holds.  For valid
 //    offsets (0 = cu[0] <= ... <= cu[N] = T) c equals cu;
-//  * off[n] = sum over m < n of ceil(len_m / 64), off[N] = the total chunk count.
+//  * off[n] = sum over m < n of ceil(len_m / 64), off[N] = the total chunk count;
+//  * order: the sequences by chunk count, longest first (ties in index order), for at
+//    most kOrderMax sequences (the identity beyond), so that the scans start the longest
+//    chains first.
+constexpr int kOrderMax = 1024;
 __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* cu, int N, int T,
-                                                          int32_t* cu_out, int32_t* off) {
+                                                          int32_t* cu_out, int32_t* off,
+                                                          int32_t* order) {
   __shared__ int wmax[16];
   __shared__ int wsum[16];
+  __shared__ int scnt[kOrderMax];
   const int tid = threadIdx.x, l = tid & 63, w = tid >> 6;
   auto clamped = [&](int n) {
     if (n == 0) return 0;
@@ -759,6 +765,7 @@ __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* cu, int
       const int c1 = x1 > c0 ? x1 : c0;  // c[n + 1]
       cu_out[n] = c0;
       cnt = (c1 - c0 + C - 1) / C;
+      if (n < kOrderMax) scnt[n] = cnt;
     }
     int x = cnt;  // inclusive scan of the chunk counts within the wave
 #pragma unroll
@@ -784,13 +791,27 @@ __global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* cu, int
     off[N] = carry;
     cu_out[N] = T;
   }
+  __syncthreads();  // scnt complete
+  for (int n = tid; n < N; n += 1024) {
+    int rank = n;
+    if (N <= kOrderMax) {
+      const int c = scnt[n];
+      rank = 0;
+      for (int m = 0; m < N; ++m) {
+        const int cm = scnt[m];
+        rank += (cm > c) || (cm == c && m < n);
+      }
+    }
+    order[rank] = n;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream) {
   hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p.cu_in, p.N, p.T,
-                     const_cast<int32_t*>(p.cu_seqlens), p.chunk_off);
+                     const_cast<int32_t*>(p.cu_seqlens), p.chunk_off,
+                     const_cast<int32_t*>(p.seq_order));
   return hipGetLastError();
 }
 
