@@ -3,7 +3,9 @@
     python -m omegalax_amd.build          # compile every source, link the library
 
 Sources are omegalax_amd/csrc/*.hip (device code) and *.cpp (the C ABI); objects go
-to omegalax_amd/_build/ and the library to omegalax_amd/lib/libomx_gdn.so.
+to omegalax_amd/_build/ and the library to omegalax_amd/lib/libomx_gdn.so.  When JAX is
+installed, the XLA FFI handlers (omegalax_amd/xla/gdn_xla_ffi.cc) are built as well, into
+omegalax_amd/lib/libomx_gdn_xla.so.
 """
 from __future__ import annotations
 
@@ -59,6 +61,37 @@ def _compile(src: str) -> str:
     return obj
 
 
+XLA_SRC = os.path.join(PKG, "xla", "gdn_xla_ffi.cc")
+XLA_LIB = os.path.join(LIBDIR, "libomx_gdn_xla.so")
+
+
+def xla_include_dir():
+    """jaxlib's FFI header directory, or None when JAX is not installed."""
+    try:
+        import jax.ffi
+    except ImportError:
+        return None
+    return jax.ffi.include_dir()
+
+
+def build_xla_ffi(verbose: bool = True):
+    """The optional XLA FFI handlers (omegalax_amd/xla/gdn_xla_ffi.cc), linked against
+    libomx_gdn.so; built only when jaxlib's FFI headers are importable."""
+    inc = xla_include_dir()
+    if inc is None:
+        if verbose:
+            print("skipped the XLA FFI handlers: jax is not installed")
+        return None
+    cmd = [hipcc(), *COMMON, "-x", "hip", *DEVICE_FLAGS, "-I", inc, "-shared", XLA_SRC, "-o",
+           XLA_LIB, "-L", LIBDIR, "-lomx_gdn", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"XLA FFI build failed: {' '.join(cmd)}\n{r.stderr}")
+    if verbose:
+        print(f"built {XLA_LIB}")
+    return XLA_LIB
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
@@ -74,6 +107,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")
+    build_xla_ffi(verbose)
     return LIB
 
 

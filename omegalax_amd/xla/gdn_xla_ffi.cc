@@ -1,0 +1,250 @@
+// XLA FFI handlers over libomx_gdn's C ABI (include/omx_gdn.h), for calling the MI355X
+// GatedDeltaNet kernels from JAX with jax.ffi.ffi_call on the ROCm platform.
+//
+// Built by omegalax_amd.build only when jaxlib's FFI headers are importable
+// (jax.ffi.include_dir()); it is not part of libomx_gdn.so and nothing in this
+// repository's torch path loads it.  Each handler validates nothing itself: the C ABI
+// checks shapes, pointers and attributes on the host and its error codes map to FFI
+// errors (EINVAL -> InvalidArgument, EUNSUPPORTED -> Unimplemented, else Internal).
+// Work is enqueued on XLA's stream; no handler synchronises or keeps state, so XLA may
+// run them concurrently and re-run them under remat (model.py:202).
+//
+// The call site they replace is chunk_gated_delta_rule inside _full_deltanet
+// (omegalax/models/qwen3_5/deltanet.py:281), which runs inside shard_map on per-device
+// shapes; the layer-level handlers cover deltanet.py:243-293 and a decode step.
+#include <cmath>
+#include <cstdint>
+
+#include <hip/hip_runtime.h>
+
+#include "omx_gdn.h"
+#include "xla/ffi/api/ffi.h"
+
+namespace ffi = xla::ffi;
+
+namespace {
+
+ffi::Error status(int rc) {
+  if (rc == OMX_GDN_OK) return ffi::Error::Success();
+  if (rc == OMX_GDN_EINVAL) return ffi::Error::InvalidArgument(omx_gdn_last_error());
+  if (rc == OMX_GDN_EUNSUPPORTED)
+    return ffi::Error(ffi::ErrorCode::kUnimplemented, omx_gdn_last_error());
+  return ffi::Error::Internal(omx_gdn_last_error());
+}
+
+int dtype_code(const ffi::AnyBuffer& x) {
+  return x.element_type() == ffi::DataType::BF16 ? OMX_GDN_BF16 : OMX_GDN_F32;
+}
+
+// chunk_gated_delta_rule(q, k, v, g, beta, chunk_size) -> o (deltanet.py:53-153), with an
+// optional initial state in and final state out (pass a [0]-sized buffer for none).
+ffi::Error ChunkFwd(hipStream_t stream, ffi::AnyBuffer q, ffi::AnyBuffer k, ffi::AnyBuffer v,
+                    ffi::Buffer<ffi::F32> g, ffi::Buffer<ffi::F32> beta,
+                    ffi::Buffer<ffi::F32> initial_state, ffi::Result<ffi::Buffer<ffi::F32>> o,
+                    ffi::Result<ffi::Buffer<ffi::F32>> final_state,
+                    ffi::Result<ffi::AnyBuffer> workspace, int64_t chunk_size) {
+  const auto qd = q.dimensions(), vd = v.dimensions();  // [B, T, Hk, dk], [B, T, Hv, dv]
+  if (qd.size() != 4 || vd.size() != 4)
+    return ffi::Error::InvalidArgument("q and v must be rank 4");
+  const int64_t B = qd[0], T = qd[1], Hk = qd[2], dk = qd[3], Hv = vd[2], dv = vd[3];
+  const float* s0 = initial_state.element_count() ? initial_state.typed_data() : nullptr;
+  float* s1 = final_state->element_count() ? final_state->typed_data() : nullptr;
+  return status(omx_gdn_chunk_fwd(q.untyped_data(), k.untyped_data(), v.untyped_data(),
+                                  dtype_code(q), g.typed_data(), beta.typed_data(), s0, nullptr,
+                                  B, o->typed_data(), s1, B, T, Hk, Hv, dk, dv, chunk_size,
+                                  1.0f / std::sqrt((float)dk), 1, workspace->untyped_data(),
+                                  workspace->size_bytes(), stream));
+}
+
+// Its VJP: cotangent do of o -> dq, dk, dv (input dtype), dg, dbeta (fp32).
+ffi::Error ChunkBwd(hipStream_t stream, ffi::AnyBuffer q, ffi::AnyBuffer k, ffi::AnyBuffer v,
+                    ffi::Buffer<ffi::F32> g, ffi::Buffer<ffi::F32> beta, ffi::Buffer<ffi::F32> d_o,
+                    ffi::Result<ffi::AnyBuffer> dq, ffi::Result<ffi::AnyBuffer> dk,
+                    ffi::Result<ffi::AnyBuffer> dv, ffi::Result<ffi::Buffer<ffi::F32>> dg,
+                    ffi::Result<ffi::Buffer<ffi::F32>> dbeta,
+                    ffi::Result<ffi::AnyBuffer> workspace, int64_t chunk_size) {
+  const auto qd = q.dimensions(), vd = v.dimensions();
+  if (qd.size() != 4 || vd.size() != 4)
+    return ffi::Error::InvalidArgument("q and v must be rank 4");
+  const int64_t B = qd[0], T = qd[1], Hk = qd[2], dkd = qd[3], Hv = vd[2], dvd = vd[3];
+  return status(omx_gdn_chunk_bwd(
+      q.untyped_data(), k.untyped_data(), v.untyped_data(), dtype_code(q), g.typed_data(),
+      beta.typed_data(), nullptr, nullptr, B, d_o.typed_data(), nullptr, dq->untyped_data(),
+      dk->untyped_data(), dv->untyped_data(), dg->typed_data(), dbeta->typed_data(), nullptr, B,
+      T, Hk, Hv, dkd, dvd, chunk_size, 1.0f / std::sqrt((float)dkd), 1,
+      workspace->untyped_data(), workspace->size_bytes(), stream));
+}
+
+// GatedDeltaNet.__call__ between the projections and out_proj (deltanet.py:243-293).
+ffi::Error Prefill(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuffer z,
+                   ffi::AnyBuffer a, ffi::AnyBuffer b, ffi::Buffer<ffi::F32> conv_w,
+                   ffi::Buffer<ffi::F32> A_log, ffi::Buffer<ffi::F32> dt_bias,
+                   ffi::Buffer<ffi::F32> norm_w, ffi::Result<ffi::AnyBuffer> out,
+                   ffi::Result<ffi::AnyBuffer> workspace, int64_t num_k_heads, int64_t head_k_dim,
+                   int64_t num_v_heads, int64_t head_v_dim, float eps) {
+  const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();  // [B, T, C], [C, K]
+  if (xd.size() != 3 || wd.size() != 2)
+    return ffi::Error::InvalidArgument("mixed_qkv must be [B, T, C] and conv_w [C, K]");
+  return status(omx_gdn_prefill(
+      mixed_qkv.untyped_data(), z.untyped_data(), a.untyped_data(), b.untyped_data(),
+      conv_w.typed_data(), A_log.typed_data(), dt_bias.typed_data(), norm_w.typed_data(), eps,
+      nullptr, xd[0], nullptr, nullptr, nullptr, nullptr, out->untyped_data(), xd[0], xd[1],
+      num_k_heads, num_v_heads, head_k_dim, head_v_dim, wd[1], 64, workspace->untyped_data(),
+      workspace->size_bytes(), stream));
+}
+
+// Its VJP for the cotangent d_out of the output.
+ffi::Error PrefillBwd(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuffer z,
+                      ffi::AnyBuffer a, ffi::AnyBuffer b, ffi::Buffer<ffi::F32> conv_w,
+                      ffi::Buffer<ffi::F32> A_log, ffi::Buffer<ffi::F32> dt_bias,
+                      ffi::Buffer<ffi::F32> norm_w, ffi::AnyBuffer d_out,
+                      ffi::Result<ffi::AnyBuffer> dx, ffi::Result<ffi::AnyBuffer> dz,
+                      ffi::Result<ffi::AnyBuffer> da, ffi::Result<ffi::AnyBuffer> db,
+                      ffi::Result<ffi::Buffer<ffi::F32>> d_conv_w,
+                      ffi::Result<ffi::Buffer<ffi::F32>> dA_log,
+                      ffi::Result<ffi::Buffer<ffi::F32>> d_dt_bias,
+                      ffi::Result<ffi::Buffer<ffi::F32>> d_norm_w,
+                      ffi::Result<ffi::AnyBuffer> workspace, int64_t num_k_heads,
+                      int64_t head_k_dim, int64_t num_v_heads, int64_t head_v_dim, float eps) {
+  const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();
+  if (xd.size() != 3 || wd.size() != 2)
+    return ffi::Error::InvalidArgument("mixed_qkv must be [B, T, C] and conv_w [C, K]");
+  return status(omx_gdn_prefill_bwd(
+      mixed_qkv.untyped_data(), z.untyped_data(), a.untyped_data(), b.untyped_data(),
+      conv_w.typed_data(), A_log.typed_data(), dt_bias.typed_data(), norm_w.typed_data(), eps,
+      nullptr, xd[0], nullptr, d_out.untyped_data(), nullptr, dx->untyped_data(),
+      dz->untyped_data(), da->untyped_data(), db->untyped_data(), d_conv_w->typed_data(),
+      dA_log->typed_data(), d_dt_bias->typed_data(), d_norm_w->typed_data(), nullptr, xd[0],
+      xd[1], num_k_heads, num_v_heads, head_k_dim, head_v_dim, wd[1], 64,
+      workspace->untyped_data(), workspace->size_bytes(), stream));
+}
+
+// One cached decode step.  The caches are results aliased to the inputs
+// (input_output_aliases={8: 1, 9: 2}); when XLA did not alias them they are copied first
+// and updated in the results.
+ffi::Error DecodeStep(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuffer z,
+                      ffi::AnyBuffer a, ffi::AnyBuffer b, ffi::Buffer<ffi::F32> conv_w,
+                      ffi::Buffer<ffi::F32> A_log, ffi::Buffer<ffi::F32> dt_bias,
+                      ffi::Buffer<ffi::F32> norm_w, ffi::AnyBuffer conv_state,
+                      ffi::Buffer<ffi::F32> state, ffi::Result<ffi::AnyBuffer> out,
+                      ffi::Result<ffi::AnyBuffer> conv_state_out,
+                      ffi::Result<ffi::Buffer<ffi::F32>> state_out, int64_t num_k_heads,
+                      int64_t head_k_dim, int64_t num_v_heads, int64_t head_v_dim, float eps) {
+  const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();  // [B, C], [C, K]
+  if (xd.size() != 2 || wd.size() != 2)
+    return ffi::Error::InvalidArgument("mixed_qkv must be [B, C] and conv_w [C, K]");
+  if (conv_state_out->untyped_data() != conv_state.untyped_data() &&
+      hipMemcpyAsync(conv_state_out->untyped_data(), conv_state.untyped_data(),
+                     conv_state.size_bytes(), hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return ffi::Error::Internal("conv_state copy failed");
+  if (state_out->untyped_data() != state.untyped_data() &&
+      hipMemcpyAsync(state_out->untyped_data(), state.untyped_data(), state.size_bytes(),
+                     hipMemcpyDeviceToDevice, stream) != hipSuccess)
+    return ffi::Error::Internal("state copy failed");
+  return status(omx_gdn_decode_step(
+      mixed_qkv.untyped_data(), z.untyped_data(), a.untyped_data(), b.untyped_data(),
+      conv_w.typed_data(), A_log.typed_data(), dt_bias.typed_data(), norm_w.typed_data(), eps,
+      conv_state_out->untyped_data(), state_out->typed_data(), out->untyped_data(), xd[0],
+      num_k_heads, num_v_heads, head_k_dim, head_v_dim, wd[1], stream));
+}
+
+}  // namespace
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnChunkFwd, ChunkFwd,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Attr<int64_t>("chunk_size"));
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnChunkBwd, ChunkBwd,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Attr<int64_t>("chunk_size"));
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnPrefill, Prefill,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Attr<int64_t>("num_k_heads")
+                                  .Attr<int64_t>("head_k_dim")
+                                  .Attr<int64_t>("num_v_heads")
+                                  .Attr<int64_t>("head_v_dim")
+                                  .Attr<float>("eps"));
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnPrefillBwd, PrefillBwd,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Attr<int64_t>("num_k_heads")
+                                  .Attr<int64_t>("head_k_dim")
+                                  .Attr<int64_t>("num_v_heads")
+                                  .Attr<int64_t>("head_v_dim")
+                                  .Attr<float>("eps"));
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnDecodeStep, DecodeStep,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::Buffer<ffi::F32>>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::Buffer<ffi::F32>>()
+                                  .Attr<int64_t>("num_k_heads")
+                                  .Attr<int64_t>("head_k_dim")
+                                  .Attr<int64_t>("num_v_heads")
+                                  .Attr<int64_t>("head_v_dim")
+                                  .Attr<float>("eps"));

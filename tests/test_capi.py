@@ -255,3 +255,19 @@ def test_prefill_noalloc_rejects_shapes_beyond_its_fixed_scratch():
                                    None, None, 16, 1, 4096, 16, 32, 128, 128, 4, 64, None)
     assert rc == _lib.EINVAL
     assert "scratch" in L.omx_gdn_last_error().decode()
+
+
+def test_xla_ffi_handlers_build_only_with_jax():
+    """The XLA FFI handler source is built only where jaxlib's FFI headers exist; here (no
+    JAX) the build skips it cleanly and the torch path does not need it."""
+    from omegalax_amd import build as B
+    assert os.path.exists(B.XLA_SRC)
+    src = open(B.XLA_SRC).read()
+    for name in ("OmxGdnChunkFwd", "OmxGdnChunkBwd", "OmxGdnPrefill", "OmxGdnPrefillBwd",
+                 "OmxGdnDecodeStep"):
+        assert f"XLA_FFI_DEFINE_HANDLER_SYMBOL({name}," in src
+    try:
+        import jax  # noqa: F401
+    except ImportError:
+        assert B.xla_include_dir() is None
+        assert B.build_xla_ffi(verbose=False) is None
