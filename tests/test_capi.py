@@ -205,6 +205,7 @@ def _prefill_bwd(**over):
     (dict(z=8), _lib.EINVAL, "16-byte aligned"),
     (dict(d_out=24), _lib.EINVAL, "16-byte aligned"),
     (dict(dz=None), _lib.EINVAL, "NULL"),
+    (dict(Hk=1, Hv=257), _lib.EUNSUPPORTED, "Hv <= 256"),
 ])
 def test_prefill_bwd_rejects_bad_arguments(over, code, msg):
     rc, err = _prefill_bwd(**over)

@@ -37,6 +37,8 @@ def np_(t):
 @pytest.mark.parametrize("B,Hk,Hv,dk,dv", [
     (1, 1, 1, 16, 32), (3, 2, 4, 16, 32), (2, 2, 4, 64, 64), (2, 1, 8, 128, 128),
     (2, 2, 2, 32, 128), (4, 16, 32, 128, 128),
+    (2, 2, 16, 128, 128),  # gqa 8, the largest the decode kernel takes, at d = 128
+    (3, 1, 8, 16, 32),     # gqa 8 at the reference smoke layout's head dims
 ])
 def test_decode_steps_match_oracle(B, Hk, Hv, dk, dv):
     from omegalax_amd import gdn_decode_step

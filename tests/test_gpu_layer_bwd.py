@@ -84,6 +84,7 @@ def check(got, ref):
     (1, 100, 1, 6, 128, 64),
     (2, 33, 2, 4, 16, 32),       # the reference's smoke layout, on zero-padded copies
     (1, 90, 1, 2, 96, 48),
+    (1, 40, 32, 256, 64, 64),    # Hv = 256, the most value heads the layer backward takes
 ])
 def test_layer_bwd_matches_oracle(B, T, Hk, Hv, dk, dv):
     say(f"layer bwd B={B} T={T} Hk={Hk} Hv={Hv} dk={dk} dv={dv}")
