@@ -465,7 +465,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the GDN path shards by sequence and head with no exchange; see DESIGN.md)",
+              "(the GDN path shards by sequence and value-head group with no exchange, so one "
+              "GPU's throughput is one shard's)",
               file=sys.stderr)
         return 2
     import torch

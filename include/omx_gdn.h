@@ -21,6 +21,14 @@
  * Shapes: B batch, T tokens, Hk key heads, Hv value heads (Hv % Hk == 0; value
  * head h reads key head h / (Hv/Hk), the repeat-interleave of
  * deltanet.py:272-280), dk/dv head dims, K conv taps, conv_dim = 2*Hk*dk + Hv*dv.
+ *
+ * Head dims: the prefill entry points accept any 1 <= dk <= 128 and 1 <= dv <= 256
+ * (dv <= 128 for the backward entry points).  Shapes the kernels are not compiled for
+ * run on zero-padded copies at the next compiled dims, made in the workspace (the
+ * *_workspace_size queries include them); the results equal the unpadded computation
+ * (q is scaled by 1/sqrt of the caller's dk, the gated norm averages over the caller's
+ * dv).  The decode entry points take dk, dv in {16, 32, 64, 128} and Hv/Hk <= 8.  Other
+ * shapes return OMX_GDN_EUNSUPPORTED.
  */
 #ifndef OMX_GDN_H
 #define OMX_GDN_H
@@ -202,7 +210,9 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
  *   dv             [B, T, Hv, dv] in_dtype
  *   dg, dbeta      [B, T, Hv] f32
  *   d_initial_state [N, Hv, dk, dv] f32 or NULL
- * Compiled shapes: bf16 inputs dk 64/128, fp32 inputs dk 32/64; dv 64/128.
+ * Compiled shapes: bf16 inputs dk 64/128, fp32 inputs dk 32/64; dv 64/128.  Other
+ * dk <= 128 (<= 64 with fp32 inputs) and dv <= 128 run padded (see the head-dims note
+ * at the top).
  */
 int omx_gdn_chunk_bwd(const void* q, const void* k, const void* v, int in_dtype,
                       const float* g, const float* beta, const float* initial_state,
@@ -236,7 +246,8 @@ size_t omx_gdn_chunk_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_
  *   d_conv_w       [conv_dim, K] f32;  dA_log, d_dt_bias [Hv] f32;  d_norm_w [dv] f32
  *   d_initial_state [N, Hv, dk, dv] f32 or NULL
  * mixed_qkv, d_mixed_qkv, z, d_out, dz and conv_w must be 16-byte aligned.
- * Compiled shapes: K = 4, dk 64/128, dv 64/128, Hv <= 256.
+ * Compiled shapes: K = 4, dk 64/128, dv 64/128, Hv <= 256.  Other dk <= 128 and
+ * dv <= 128 run padded (see the head-dims note at the top).
  */
 int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, const void* b,
                         const float* conv_w, const float* A_log, const float* dt_bias,
