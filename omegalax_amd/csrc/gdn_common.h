@@ -50,6 +50,18 @@ __device__ __forceinline__ uint32_t pack_lo_pair(float x0, float x1, uint32_t h)
   return pack_bf16(l0, l1);
 }
 
+// w0 x0 + w1 x1 + w2 x2 + w3 x3 for bf16 weights and inputs held as packed pairs
+// (w01 = (w0, w1), x01 = (x0, x1), ...), as two bf16 dot products (v_dot2_f32_bf16):
+// the products are exact in fp32 and the sums are fp32.  The causal conv's tap sum, with
+// x_d the input d tokens back and w_d its weight.
+__device__ __forceinline__ float dot4_bf16(uint32_t w01, uint32_t w23, uint32_t x01,
+                                           uint32_t x23) {
+  const float s23 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x23),
+                                                    __builtin_bit_cast(bf16x2_t, w23), 0.f, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x01),
+                                         __builtin_bit_cast(bf16x2_t, w01), s23, false);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // log(1 + e^x), the softplus of jax.nn.softplus; exact branch for large x.

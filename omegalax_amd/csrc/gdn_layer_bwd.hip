@@ -67,9 +67,11 @@ __device__ __forceinline__ void zero8(float* x) {
   for (int e = 0; e < 8; ++e) x[e] = 0.f;
 }
 
-// the forward's conv pre-activation, rounded to bf16 as there
+// the forward's conv pre-activation, computed and rounded to bf16 as there (the inputs
+// and the weights wt are bf16 values, so the pairs pack exactly)
 __device__ __forceinline__ float conv_u(const float* wt, float x0, float x1, float x2, float x3) {
-  return round_bf(wt[0] * x0 + wt[1] * x1 + wt[2] * x2 + wt[3] * x3);
+  return round_bf(dot4_bf16(pack_bf16(wt[0], wt[1]), pack_bf16(wt[2], wt[3]), pack_bf16(x0, x1),
+                            pack_bf16(x2, x3)));
 }
 
 // d silu(u) / du

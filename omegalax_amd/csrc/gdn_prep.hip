@@ -100,9 +100,10 @@ __device__ __forceinline__ void put_tile(__amdgpu_buffer_rsrc_t rec, int off, u3
   __builtin_amdgcn_raw_buffer_store_b64(f, rec, 16 * lane_id(), off, 0);
 }
 
-// conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243:
-// wt[e][d] multiplies the input d tokens back (tap K-1-d); taps beyond K are 0
-__device__ __forceinline__ void load_conv_w(const ChunkParams& p, int chu, int chl, float (*wt)[4]) {
+// conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243, as packed
+// pairs: wp[e][0] = (w_0, w_1), wp[e][1] = (w_2, w_3) with w_d the weight of the input d
+// tokens back (tap K-1-d); taps beyond K are 0
+__device__ __forceinline__ void load_conv_w(const ChunkParams& p, int chu, int chl, uint32_t (*wp)[2]) {
   const int K = p.conv_k;
   const int ch0 = chu + chl;
   if (K == 4) {  // uniform: each channel's taps are one 16-byte row
@@ -110,18 +111,19 @@ __device__ __forceinline__ void load_conv_w(const ChunkParams& p, int chu, int c
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float4 w = *(const float4*)at_bytes(wb, 16u * (unsigned)(chl + e));
-      wt[e][0] = round_bf(w.w);
-      wt[e][1] = round_bf(w.z);
-      wt[e][2] = round_bf(w.y);
-      wt[e][3] = round_bf(w.x);
+      wp[e][0] = pack_bf16(w.w, w.z);
+      wp[e][1] = pack_bf16(w.y, w.x);
     }
     return;
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float* w = p.conv_w + (size_t)(ch0 + e) * K;
+    float wt[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) wt[e][d] = d < K ? round_bf(w[K - 1 - d]) : 0.f;
+    for (int d = 0; d < 4; ++d) wt[d] = d < K ? w[K - 1 - d] : 0.f;
+    wp[e][0] = pack_bf16(wt[0], wt[1]);
+    wp[e][1] = pack_bf16(wt[2], wt[3]);
   }
 }
 
@@ -144,12 +146,12 @@ __device__ __forceinline__ u32x4 conv_input(const ChunkParams& p, int n, long lo
 }
 
 // Causal depthwise conv + SiLU (deltanet.py:35-50, 243) of one 8-channel group over
-// chunk rows r0 .. r0+ROWS-1, streaming down the rows with the last three inputs
-// kept in registers.  conv_load issues every input row once (rows r0-3 ..
-// r0+ROWS-1); conv_compute consumes them.  Inputs, weights, the conv sum and the
-// SiLU output are rounded to bf16 like the reference's bf16 ops (the sum
-// accumulates in fp32); rows at or past nvalid give zeros.  emit(m, y) receives
-// row r0 + m.
+// chunk rows r0 .. r0+ROWS-1, streaming down the rows.  conv_load issues every input
+// row once (rows r0-3 .. r0+ROWS-1); conv_compute consumes them.  Inputs and weights
+// are bf16 (the weights cast as the reference casts them), the tap sum is two bf16 dot
+// products per channel with fp32 sums, and the sum and the SiLU output are rounded to
+// bf16 like the reference's bf16 ops; rows at or past nvalid give zeros.
+// emit(m, y) receives row r0 + m as 8 packed bf16 values.
 template <int ROWS>
 __device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long s0, long long t0,
                                           int nvalid, int r0, int chu, int chl, u32x4* raw) {
@@ -161,27 +163,43 @@ __device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long
   }
 }
 
+// The pairs (x_t, x_{t-1}) of the 8 channels from input rows t (cur) and t-1 (prev):
+// word c of pe holds channel 2c's pair, word c of po channel 2c+1's (v_perm_b32).
+__device__ __forceinline__ void time_pairs(const u32x4& cur, const u32x4& prev, u32x4& pe, u32x4& po) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    pe[c] = __builtin_amdgcn_perm(prev[c], cur[c], 0x05040100u);
+    po[c] = __builtin_amdgcn_perm(prev[c], cur[c], 0x07060302u);
+  }
+}
+
 template <int ROWS, class Emit>
-__device__ __forceinline__ void conv_compute(const u32x4* raw, const float (*wt)[4], int nvalid,
+__device__ __forceinline__ void conv_compute(const u32x4* raw, const uint32_t (*wp)[2], int nvalid,
                                              int r0, Emit emit) {
-  float x3[8], x2[8], x1[8];  // inputs 3, 2 and 1 rows back
-  unpack8<false>(&raw[0], x3);
-  unpack8<false>(&raw[1], x2);
-  unpack8<false>(&raw[2], x1);
+  // time pairs of rows m-2 and m-1 (a row's pair holds it and the row before)
+  u32x4 pe2, po2, pe1, po1;
+  time_pairs(raw[1], raw[0], pe2, po2);
+  time_pairs(raw[2], raw[1], pe1, po1);
 #pragma unroll
   for (int m = 0; m < ROWS; ++m) {
-    float x0[8], y[8];
-    unpack8<false>(&raw[m + 3], x0);
-    const float keep = (float)(r0 + m < nvalid);
+    u32x4 pe0, po0;
+    time_pairs(raw[m + 3], raw[m + 2], pe0, po0);
+    u32x4 y;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float acc = wt[e][0] * x0[e] + wt[e][1] * x1[e] + wt[e][2] * x2[e] + wt[e][3] * x3[e];
-      y[e] = round_bf(silu_fast(round_bf(acc))) * keep;
-      x3[e] = x2[e];
-      x2[e] = x1[e];
-      x1[e] = x0[e];
+    for (int c = 0; c < 4; ++c) {
+      const float a0 = dot4_bf16(wp[2 * c][0], wp[2 * c][1], pe0[c], pe2[c]);
+      const float a1 = dot4_bf16(wp[2 * c + 1][0], wp[2 * c + 1][1], po0[c], po2[c]);
+      const uint32_t u = pack_bf16(a0, a1);  // the pre-activations, rounded to bf16
+      y[c] = pack_bf16(silu_fast(__uint_as_float(u << 16)), silu_fast(__uint_as_float(u & 0xffff0000u)));
+    }
+    if (nvalid < kC) {  // uniform: a sequence's last chunk; its padded rows are zero
+      if (r0 + m >= nvalid) y = u32x4{0u, 0u, 0u, 0u};
     }
     emit(m, y);
+    pe2 = pe1;
+    po2 = po1;
+    pe1 = pe0;
+    po1 = po0;
   }
 }
 
@@ -191,10 +209,10 @@ template <int ROWS, class Emit>
 __device__ __forceinline__ void conv_rows(const ChunkParams& p, int n, long long s0, long long t0,
                                           int nvalid, int r0, int chu, int chl, Emit emit) {
   u32x4 raw[ROWS + 3];
-  float wt[8][4];
-  load_conv_w(p, chu, chl, wt);
+  uint32_t wp[8][2];
+  load_conv_w(p, chu, chl, wp);
   conv_load<ROWS>(p, n, s0, t0, nvalid, r0, chu, chl, raw);
-  conv_compute<ROWS>(raw, wt, nvalid, r0, emit);
+  conv_compute<ROWS>(raw, wp, nvalid, r0, emit);
 }
 
 // L2 norm of a row spread over W lanes (8 values each), in fp32 like the
@@ -386,7 +404,9 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
         bf16_t* gout = (bf16_t*)(wave == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK + (long long)hk * DK;
         const unsigned ostride = (unsigned)(p.Hk * DK);
         conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (wave == 0 ? p.Hk * DK : 0) + hk * DK, 8 * g,
-                        [&](int m, float* y) {
+                        [&](int m, const u32x4& yw) {
+          float y[8];
+          unpack8<false>(&yw, y);
           l2norm8<SEGS>(y);
           const u32x4 hw = pack8(y);
           const int r = r0 + m;
@@ -401,9 +421,9 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
         for (int it = tid - 128; it < VG * 4; it += 128) {
           const int g = it % VG, r0 = (it / VG) * 16;
           if (r0 >= nvalid) continue;
-          auto emit = [&](int m, float* y) {
+          auto emit = [&](int m, const u32x4& y) {
             const int r = r0 + m;
-            if (r < nvalid) *(u32x4*)at_bytes(vout, 2u * ((unsigned)r * vstride + 8u * g)) = pack8(y);
+            if (r < nvalid) *(u32x4*)at_bytes(vout, 2u * ((unsigned)r * vstride + 8u * g)) = y;
           };
           conv_rows<16>(p, n, s0, t0, nvalid, r0, vch0, 8 * g, emit);
         }
