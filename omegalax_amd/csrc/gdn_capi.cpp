@@ -57,7 +57,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // sums of o^2 for the gated norm, and the plan of packed sequences (chunk offsets and
 // the ordered copy of cu_seqlens the kernels read).
 struct ChunkWs {
-  size_t rec, kn, qn, vc, opart, off, cu, ord, total;
+  size_t rec, kn, qn, vc, opart, oss, off, cu, ord, total;
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
@@ -79,6 +79,8 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
     w.opart = o;
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
+    w.oss = o;
+    o += align_up((tokens + 63) / 64 * 64 * (size_t)Hv * (size_t)(dv / 16) * 4, 256);
   }
   w.off = o;
   o += align_up((size_t)(N + 1) * 4, 256);
@@ -528,12 +530,14 @@ int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const voi
   p.eps = eps;
   p.qk_l2norm = 1;
   p.o_part = (char*)workspace + ws.opart;
+  p.o_ss = (float*)((char*)workspace + ws.oss);
   REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
   REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
   if (e == hipSuccess)
-    e = omx::launch_norm_epilogue(p.o_part, z, norm_w, out, tokens * Hv, (int)dv, (int)dv_real,
-                                  eps, (hipStream_t)stream);
+    e = omx::launch_norm_epilogue(p.o_part, p.o_ss, omx::layer_ss_slots(p), z, norm_w, out,
+                                  tokens, (int)Hv, (int)dv, (int)dv_real, eps,
+                                  (hipStream_t)stream);
   return launch_status(e, fn);
 }
 

@@ -118,6 +118,40 @@ __device__ __forceinline__ u32x2 pack_lo4(f32x4 x) {
   return u32x2{pack_lo_pair(x[0], x[1], h[0]), pack_lo_pair(x[2], x[3], h[1])};
 }
 
+// Sum of n = 1, 2 or 4 consecutive 16-column partials as the pairwise tree ((a0 + a1) +
+// (a2 + a3)) that a butterfly over the partials of a row forms, so that a row's total is
+// the same however many partials a workgroup adds up first.
+template <int N>
+__device__ __forceinline__ float ss_tree(const float* a) {
+  if constexpr (N == 1) return a[0];
+  else if constexpr (N == 2) return a[0] + a[1];
+  else return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+// Sums of squares of the rows of four 16x16 tiles held transposed (lane (q, r) holds
+// row r, columns 4q .. 4q+3 of tile i in x[i]), reduce-scattered over the four lane rows
+// of the wavefront (q = 0..3) so that lane (q, r) returns the sum of row r of tile q.
+// Two cross-row swaps, no LDS traffic: v_permlane32_swap exchanges the upper 32 lanes of
+// its first operand with the lower 32 lanes of its second, so after swapping (a, b) the
+// two results summed give, in lanes q < 2, a's sum over rows q and q + 2 and, in lanes
+// q >= 2, b's; v_permlane16_swap does the same for odd and even 16-lane rows.
+__device__ __forceinline__ float row_sq_scatter(const f32x4* x) {
+  float ss[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    ss[i] = x[i][0] * x[i][0] + x[i][1] * x[i][1] + x[i][2] * x[i][2] + x[i][3] * x[i][3];
+  const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss[0]), __float_as_uint(ss[2]),
+                                                    false, false);
+  const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss[1]), __float_as_uint(ss[3]),
+                                                    false, false);
+  // lanes q < 2: tiles 0 and 1 summed over rows q, q + 2; lanes q >= 2: tiles 2 and 3
+  const float k0 = __uint_as_float(s02[0]) + __uint_as_float(s02[1]);
+  const float k1 = __uint_as_float(s13[0]) + __uint_as_float(s13[1]);
+  const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(k0), __float_as_uint(k1), false,
+                                                  false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
 // unpack 8 input values (bf16 or fp32) from raw load words
 template <bool F32>
 __device__ __forceinline__ void unpack8(const u32x4* w, float* x) {

@@ -297,6 +297,12 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   __shared__ __align__(16) bf16_t sQ0[Q_::SZK], sQ1[DIRECT ? Q_::SZK : 8];
   __shared__ __align__(16) bf16_t sV0[Q_::SZV], sV1[DIRECT ? Q_::SZV : 8];
   __shared__ __align__(16) unsigned char sRec0[Q_::REC], sRec1[DIRECT ? Q_::REC : 16];
+  // (layer, direct loads) the compute wavefronts' row sums of o^2, by chunk parity: chunk
+  // j's are written after the barrier that opens chunk j + 1 (so no wavefront waits for
+  // the write before a barrier); the loader adds them up after the barrier of chunk j + 2
+  constexpr bool WG_SS = DIRECT && MODE == MODE_LAYER;
+  __shared__ float sSS[WG_SS ? 2 : 1][WG_SS ? NWC : 1][C];
+  float ss_prev = 0.f;  // this lane's row sum of the previous chunk, not yet in sSS
   constexpr int K_LO = C * LDK, V_LO = C * LDT;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -371,6 +377,9 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
       // the loader's loads of chunk j have landed (it waited before arriving), and
       // chunk j-1, the last reader of the other buffer, is finished everywhere
       lds_barrier();
+      if constexpr (WG_SS) {
+        if (j >= 1) sSS[(j - 1) & 1][wave][16 * lq + lr] = ss_prev;
+      }
     } else {
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
@@ -695,7 +704,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           if (16 * i + lr < nvalid) store(i);
       }
     } else {
-      // unnormalised o in bf16; the epilogue kernel applies the norm
+      // unnormalised o in bf16; the epilogue kernel applies the norm, from the fp32 sums
+      // of squares stored below
       const auto ob = buf_rsrc((bf16_t*)p.o_part + (t0 * p.Hv + h) * (long long)DV + col0, 2u * C * o_rs);
       auto store = [&](int i) {
         __builtin_amdgcn_raw_buffer_store_b64(
@@ -710,15 +720,37 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         for (int i = 0; i < 4; ++i)
           if (16 * i + lr < nvalid) store(i);
       }
+      // sum of squares of each token row over the wave's 16 columns, from the fp32 o (the
+      // statistic of the reference's fp32 norm, deltanet.py:282-293): lane (q, r) ends
+      // with row 16q + r's sum (row_sq_scatter).  The partials are stored in 64-token
+      // blocks (ss_index), so a chunk's partials of one slot are one contiguous store.
+      // With direct loads the loader adds the workgroup's values up first (ss_tree);
+      // otherwise each wavefront stores its own.
+      const float mine = row_sq_scatter(o);
+      if constexpr (WG_SS) {
+        ss_prev = mine;
+      } else if (16 * lq + lr < nvalid) {
+        p.o_ss[ss_index(t0 + 16 * lq + lr, h, col0 / 16 + wave, p.Hv, p.ss_slots)] = mine;
+      }
     }
-
-
   };
 
   if constexpr (DIRECT) {
     if (loader) {
       // one barrier per chunk, as the compute wavefronts: after the barrier at the top of
       // chunk j, buffer (j + 1) % 2 is free and receives chunk j + 1
+      // (layer) lane l's row of chunk jj: the workgroup's partial, one per row, stored
+      // after the wait for the next chunk's loads (the following wait covers it)
+      auto store_ss = [&](int jj) {
+        if constexpr (WG_SS) {
+          const long long tj = s0 + (long long)jj * C;
+          const int nvj = (int)((s1 - tj) < C ? (s1 - tj) : C);
+          float v[NWC];
+#pragma unroll
+          for (int w = 0; w < NWC; ++w) v[w] = sSS[jj & 1][w][l];
+          if (l < nvj) p.o_ss[ss_index(tj + l, h, blk, p.Hv, p.ss_slots)] = ss_tree<NWC>(v);
+        }
+      };
       auto load = [&](int j, lds_bf16* nK, lds_bf16* nQ, lds_bf16* nV, lds_u8* nRec) {
         lds_barrier();
         if (j + 1 < nchunks) {
@@ -727,15 +759,31 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           stage_all<DK, MODE, BV>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the next barrier
+        if (j >= 2) store_ss(j - 2);  // written after barrier j - 1, visible after barrier j
       };
       for (int j = 0; j < nchunks; j += 2) {
         load(j, (lds_bf16*)sK1, (lds_bf16*)sQ1, (lds_bf16*)sV1, (lds_u8*)sRec1);
         if (j + 1 < nchunks) load(j + 1, (lds_bf16*)sK0, (lds_bf16*)sQ0, (lds_bf16*)sV0, (lds_u8*)sRec0);
       }
+      if constexpr (WG_SS) {  // the last two chunks' row sums, as in the loop
+        if (nchunks > 0) {
+          lds_barrier();  // chunk n - 2's are visible; the buffer of n - 1's is free
+          if (nchunks >= 2) store_ss(nchunks - 2);
+          lds_barrier();  // chunk n - 1's are visible
+          store_ss(nchunks - 1);
+        }
+      }
     } else {
       for (int j = 0; j < nchunks; j += 2) {
         run_chunk(j, sK0, sQ0, sV0, sRec0);
         if (j + 1 < nchunks) run_chunk(j + 1, sK1, sQ1, sV1, sRec1);
+      }
+      if constexpr (WG_SS) {  // the loader's two barriers after its loop
+        if (nchunks > 0) {
+          lds_barrier();
+          sSS[(nchunks - 1) & 1][wave][16 * lq + lr] = ss_prev;
+          lds_barrier();
+        }
       }
     }
   } else {
@@ -785,6 +833,9 @@ hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
   using Q_ = Cfg<DK, MODE, NWC>;
   ChunkParams q = p;
   q.nb = p.DV / Q_::BV;
+  // (layer) row-sum partials per (token, value head): one per workgroup with direct
+  // loads, else one per wavefront
+  q.ss_slots = Q_::DIRECT ? q.nb : p.DV / 16;
   const unsigned grid = (unsigned)(q.N * q.Hv * q.nb);
   hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD, NWC>), dim3(grid), dim3(Q_::NTH), 0, stream, q);
   return hipGetLastError();
@@ -828,6 +879,10 @@ hipError_t launch_scan_direct(const ChunkParams& p, hipStream_t stream) {
 }  // namespace
 
 int chunk_block_cols() { return kBlockCols; }
+
+int layer_ss_slots(const ChunkParams& p) {
+  return p.dk == 128 ? p.DV / (16 * scan_tiles_per_wg(p)) : p.DV / 16;
+}
 
 int chunk_record_bytes(int mode) { return rec_bytes(mode); }
 

@@ -62,6 +62,13 @@ __device__ __forceinline__ float dot4_bf16(uint32_t w01, uint32_t w23, uint32_t 
                                          __builtin_bit_cast(bf16x2_t, w01), s23, false);
 }
 
+// Index of the partial sum of squares of (token t, value head h, 16-column slice s) in the
+// layer prefill's [ceil(tokens / 64)][Hv][S][64] array (S slices per row): the 64 tokens
+// of a block are contiguous for each (head, slice).
+__device__ __forceinline__ long long ss_index(long long t, int h, int s, int Hv, int S) {
+  return (((t >> 6) * Hv + h) * S + s) * 64 + (t & 63);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // log(1 + e^x), the softplus of jax.nn.softplus; exact branch for large x.

@@ -58,6 +58,9 @@ struct ChunkParams {
   void* conv_state_out;        // [N, conv_dim, K-1] bf16 or null
   void* out;                   // [tokens, Hv*DV] bf16
   void* o_part;                // unnormalised o [tokens, Hv, DV] bf16 (workspace)
+  float* o_ss;                 // [ceil(tokens / 64), Hv, ss_slots, 64] fp32 (workspace):
+                               // partial sums of squares of the fp32 o over a row
+  int ss_slots;                // partials per (token, head) row (set by the scan's launcher)
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
@@ -193,12 +196,16 @@ hipError_t launch_layer_fwd_pieces(const LayerBwdParams& p, hipStream_t stream);
 hipError_t launch_layer_norm_bwd(const LayerBwdParams& p, hipStream_t stream);
 hipError_t launch_layer_tail_bwd(const LayerBwdParams& p, hipStream_t stream);
 
-// Gated RMSNorm of the layer prefill from bf16 o: out = w * o * rsqrt(mean(o^2) + eps)
-// * silu(z) per (token, value head) row of dv (dv / 8 at most 32); the mean divides the
-// row's sum of squares by dv_mean.
-hipError_t launch_norm_epilogue(const void* o_part, const void* z, const float* norm_w, void* out,
-                                long long rows, int dv, int dv_mean, float eps,
-                                hipStream_t stream);
+// Gated RMSNorm of the layer prefill: out = w * o * rsqrt(mean(o^2) + eps) * silu(z) per
+// (token, value head) row of dv (a multiple of 16, dv / 8 at most 32), with o the scan's
+// bf16 o and the row's sum of squares the butterfly sum of its nss fp32 partials in o_ss
+// (ss_index layout, formed by the scan from the fp32 o); the mean divides it by dv_mean.
+hipError_t launch_norm_epilogue(const void* o_part, const float* o_ss, int nss, const void* z,
+                                const float* norm_w, void* out, long long tokens, int Hv, int dv,
+                                int dv_mean, float eps, hipStream_t stream);
+
+// Row-sum partials per (token, value head) the layer scan writes for these parameters.
+int layer_ss_slots(const ChunkParams& p);
 
 // An [R][G][E] view of a buffer for launch_pad_copy: element pointer, group and element
 // counts, row and group strides (elements).
