@@ -183,8 +183,8 @@ MEASURED_TRAFFIC = {
     ("decode", 64, 16, 32, 128): (277_278_720, "profiles/decode_step_c2.md (B=64)"),
     ("decode", 256, 16, 32, 128): (1_107_987_251, "profiles/decode_step_c2.md (B=256)"),
     # layer step: prep 303.2 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
-    ("prefill", 4, 4096, 16, 32, 128): (1_712_742_400, "profiles/prefill_c1.md (layer kernels)"),
-    ("c3", 32768, 8): (3_483_595_776, "profiles/prefill_c3_c4.md (C3 layer call)"),
+    ("prefill", 4, 4096, 16, 32, 128): (1_740_128_870, "profiles/prefill_c1.md (layer kernels)"),
+    ("c3", 32768, 8): (3_533_385_523, "profiles/prefill_c3_c4.md (C3 layer call)"),
 }
 
 
