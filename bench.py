@@ -185,6 +185,7 @@ MEASURED_TRAFFIC = {
     # layer step: prep 303.2 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
     ("prefill", 4, 4096, 16, 32, 128): (1_740_128_870, "profiles/prefill_c1.md (layer kernels)"),
     ("c3", 32768, 8): (3_533_385_523, "profiles/prefill_c3_c4.md (C3 layer call)"),
+    ("bwd", 4, 4096, 16, 32, 128): (7_553_046_835, "profiles/bwd_c1.md (backward call)"),
 }
 
 
@@ -258,10 +259,12 @@ def bench_bwd(B, T, Hk, Hv, d, steps, warmup):
     wall, ms = time_launches(bwd, steps, warmup)
     flops = bwd_flops_per_token_head(d, d) * B * T * Hv
     tf = flops / (ms * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get(("bwd", B, T, Hk, Hv, d))
     return {
         "ms_per_step": wall / steps * 1e3, "kernel_ms": ms,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": tf / PEAK_BF16_TFLOPS,
+                     "traffic": traffic and traffic[0], "traffic_source": traffic and traffic[1],
                      "algorithmic_flops": flops,
                      "kernels": "prep (bwd) + scan (bwd) + rscan + cgrad + qk_final"},
     }
