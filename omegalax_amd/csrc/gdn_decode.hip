@@ -45,7 +45,11 @@ __device__ __forceinline__ void store_st(float* p, float4 x) {
   else *(float4*)p = x;
 }
 
-template <int DK, int DV, bool LAYER, typename InT, bool NT, bool EARLY>
+// Prefetch shape of the layer path's small inputs (PRE): channels per thread and value
+// heads per workgroup it covers.
+constexpr int kPreChannels = 2, kPreHeads = 2;
+
+template <int DK, int DV, bool LAYER, typename InT, bool NT, bool EARLY, bool PRE>
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   constexpr int CG = DV / 4;            // column groups of 4
   constexpr int RG = kThreads / CG;     // row groups
@@ -71,6 +75,47 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       else st[r] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
+  // PRE (layer path, K = 4, 2 dk + gqa dv <= 2 * 256 channels, gqa <= 2): the step's small
+  // inputs -- this thread's conv channels (raw token, the three cached inputs, weights),
+  // z, norm_w and the gate inputs -- are loaded before the state.  The memory counter
+  // retires loads and stores in issue order, so a small load issued after the state
+  // loads, or after a value head's state stores, would wait for all of them.
+  const int conv_dim = 2 * p.Hk * DK + p.Hv * DV;
+  auto conv_channel = [&](int i) {
+    if (i < DK) return hk * DK + i;
+    if (i < 2 * DK) return p.Hk * DK + hk * DK + (i - DK);
+    return 2 * p.Hk * DK + hk * gqa * DV + (i - 2 * DK);
+  };
+  unsigned short pre_x[kPreChannels], pre_h[kPreChannels][3];
+  float pre_w[kPreChannels][4], pre_z[kPreHeads], pre_a[kPreHeads], pre_b[kPreHeads];
+  float pre_nw = 0.f;
+  if constexpr (PRE) {
+    const int nch = 2 * DK + gqa * DV;
+    const unsigned short* xin = (const unsigned short*)p.mixed_qkv + (size_t)b * conv_dim;
+#pragma unroll
+    for (int m = 0; m < kPreChannels; ++m) {
+      const int i = tid + m * kThreads;
+      if (i < nch) {
+        const int c = conv_channel(i);
+        const unsigned short* cs = (const unsigned short*)p.conv_state + ((size_t)b * conv_dim + c) * 3;
+        pre_x[m] = xin[c];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) pre_h[m][j] = cs[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) pre_w[m][j] = p.conv_w[(size_t)c * 4 + j];
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < kPreHeads; ++hh) {
+      const int h = hk * gqa + hh;
+      if (hh < gqa) {
+        if (tid < DV) pre_z[hh] = bf2f(((const bf16_t*)p.z)[((size_t)b * p.Hv + h) * DV + tid]);
+        pre_a[hh] = bf2f(((const bf16_t*)p.a)[(size_t)b * p.Hv + h]);
+        pre_b[hh] = bf2f(((const bf16_t*)p.b)[(size_t)b * p.Hv + h]);
+      }
+    }
+    if (tid < DV) pre_nw = p.norm_w[tid];
+  }
   float4 st[R], stn[R];
   if (EARLY) {
     load_state(0, st);
@@ -87,15 +132,35 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
   __shared__ float s_scal[8];
 
   // ---------------------------------------------------------------- q, k (and conv)
-  if (LAYER) {
-    const int conv_dim = 2 * p.Hk * DK + p.Hv * DV;
+  if (PRE) {
+    // the same arithmetic as below, on the prefetched registers (K = 4)
+    const int nch = 2 * DK + gqa * DV;
+#pragma unroll
+    for (int m = 0; m < kPreChannels; ++m) {
+      const int i = tid + m * kThreads;
+      if (i >= nch) continue;
+      const int c = conv_channel(i);
+      bf16_t* cs = (bf16_t*)p.conv_state + ((size_t)b * conv_dim + c) * 3;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) acc += round_bf(pre_w[m][j]) * bf2f(pre_h[m][j]);
+      acc += round_bf(pre_w[m][3]) * bf2f(pre_x[m]);
+      const float y = round_bf(siluf_(round_bf(acc)));
+      cs[0] = pre_h[m][1];
+      cs[1] = pre_h[m][2];
+      cs[2] = pre_x[m];
+      if (i < DK) s_q[i] = y;
+      else if (i < 2 * DK) s_k[i - DK] = y;
+      else {
+        const int vi = i - 2 * DK;
+        s_red_kv[vi / DV][vi % DV] = y;
+      }
+    }
+  } else if (LAYER) {
     const int nch = 2 * DK + gqa * DV;
     const int K = p.conv_k;
     for (int i = tid; i < nch; i += kThreads) {
-      int c;
-      if (i < DK) c = hk * DK + i;
-      else if (i < 2 * DK) c = p.Hk * DK + hk * DK + (i - DK);
-      else c = 2 * p.Hk * DK + hk * gqa * DV + (i - 2 * DK);
+      const int c = conv_channel(i);
       const bf16_t* xin = (const bf16_t*)p.mixed_qkv + (size_t)b * conv_dim;
       bf16_t* cs = (bf16_t*)p.conv_state + ((size_t)b * conv_dim + c) * (K - 1);
       float hist[kMaxConvK];
@@ -186,8 +251,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
     if (hh > 0 && hh + 1 < gqa) load_state(hh + 1, stn);
     float alpha, beta;
     if (LAYER) {
-      const float av = bf2f(((const bf16_t*)p.a)[(size_t)b * p.Hv + h]);
-      const float bv = bf2f(((const bf16_t*)p.b)[(size_t)b * p.Hv + h]);
+      const float av = PRE ? pre_a[hh < kPreHeads ? hh : 0] : bf2f(((const bf16_t*)p.a)[(size_t)b * p.Hv + h]);
+      const float bv = PRE ? pre_b[hh < kPreHeads ? hh : 0] : bf2f(((const bf16_t*)p.b)[(size_t)b * p.Hv + h]);
       const float g = -expf(p.A_log[h]) * softplusf_(av + p.dt_bias[h]);
       alpha = expf(g);
       beta = round_bf(sigmoidf_(bv));
@@ -257,9 +322,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
       const float rn = s_scal[3];
       bf16_t* out = (bf16_t*)p.out + ((size_t)b * p.Hv + h) * DV;
       const bf16_t* z = (const bf16_t*)p.z + ((size_t)b * p.Hv + h) * DV;
-      for (int i = tid; i < DV; i += kThreads) {
-        const float n = p.norm_w[i] * (s_o[i] * rn);
-        out[i] = f2bf(n * siluf_(bf2f(z[i])));
+      if (PRE) {
+        if (tid < DV) out[tid] = f2bf(pre_nw * (s_o[tid] * rn) * siluf_(pre_z[hh < kPreHeads ? hh : 0]));
+      } else {
+        for (int i = tid; i < DV; i += kThreads) {
+          const float n = p.norm_w[i] * (s_o[i] * rn);
+          out[i] = f2bf(n * siluf_(bf2f(z[i])));
+        }
       }
     } else {
       float* o = p.o + ((size_t)b * p.Hv + h) * DV;
@@ -276,15 +345,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 template <int DK, int DV, bool NT, bool EARLY>
 void launch_cfg(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream) {
   dim3 grid(p.Hk, p.B);
-  if (layer) {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t, NT, EARLY>), grid, dim3(kThreads), 0,
-                       stream, p);
+  const int gqa = p.Hv / p.Hk;
+  const bool pre = p.conv_k == 4 && gqa <= kPreHeads && 2 * DK + gqa * DV <= kPreChannels * kThreads;
+  if (layer && pre) {
+    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t, NT, EARLY, true>), grid, dim3(kThreads),
+                       0, stream, p);
+  } else if (layer) {
+    hipLaunchKernelGGL((decode_kernel<DK, DV, true, bf16_t, NT, EARLY, false>), grid, dim3(kThreads),
+                       0, stream, p);
   } else if (in_bf16) {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, false, bf16_t, NT, EARLY>), grid, dim3(kThreads), 0,
-                       stream, p);
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, bf16_t, NT, EARLY, false>), grid,
+                       dim3(kThreads), 0, stream, p);
   } else {
-    hipLaunchKernelGGL((decode_kernel<DK, DV, false, float, NT, EARLY>), grid, dim3(kThreads), 0,
-                       stream, p);
+    hipLaunchKernelGGL((decode_kernel<DK, DV, false, float, NT, EARLY, false>), grid,
+                       dim3(kThreads), 0, stream, p);
   }
 }
 
