@@ -97,6 +97,27 @@ def test_layer_varlen_with_carried_states(dk, dv):
     assert np.array_equal(np_(conv), conv_ref)
 
 
+def test_layer_many_short_packed_sequences():
+    """1,100 packed sequences of 0-4 tokens: past the 1,024 sequences whose start order the
+    plan sorts (longest first), the scans take them in index order; every sequence restarts
+    its conv window and state (from its own initial state), as the oracle runs each one."""
+    say("layer 1100 short packed sequences")
+    dims = dict(Hk=1, dk=64, Hv=2, dv=64)
+    rng = np.random.default_rng(11)
+    lens = rng.integers(0, 5, size=1100)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    d = W.layer_inputs(1, T, **dims, seed=12)
+    N = len(lens)
+    S0 = (0.02 * rng.standard_normal((N, 2, 64, 64))).astype(np.float32)
+    t = W.to_device(d)
+    out, S, conv = gpu_prefill(t, dims, cu, S0)
+    ref, S_ref, conv_ref = ref_prefill(d, dims, cu, S0)
+    assert rel(np_(out), ref) < BF16_TOL
+    assert rel(np_(S), S_ref) < STATE_TOL
+    assert np.array_equal(np_(conv), conv_ref)
+
+
 def test_layer_offsets_host_checked_or_read_as_ordered_repair():
     """cu_seqlens on the host is checked there (ValueError when invalid); on the device it
     is never read by the host, and the kernels read invalid offsets as c[0] = 0, c[N] = T,
