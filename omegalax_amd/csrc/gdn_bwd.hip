@@ -326,7 +326,7 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
   seq_range(p.cu_seqlens, n, p.T, s0, s1);
   const int nchunks = (int)((s1 - s0 + C - 1) / C);
   const int cbase = p.chunk_off ? p.chunk_off[n] : n * p.nch;
-  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32));
+  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32), true);
   const long long rs = (long long)p.Hv * DV;  // row stride of dO / dV_new
 
   // dS[t][v] = dS[16t + 4lq + v][col0 + c + lr]: gradient of the state leaving the chunk
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
   if (nvalid <= 0) return;
   const int gqa = Hv / p.Hk, hk = h / gqa;
-  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32));
+  const size_t rec_stride = (size_t)rec_bytes(rec_mode(F32), true);
   const float* xb = p.xlpg + ((size_t)ci * Hv + h) * kXlpgFloats;
   const float* Sg = p.states + ((size_t)ci * Hv + h) * DK * DV;
   const float* dSg = p.dstates + ((size_t)ci * Hv + h) * DK * DV;

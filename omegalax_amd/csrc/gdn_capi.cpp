@@ -61,7 +61,7 @@ struct ChunkWs {
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
-                 int mode) {
+                 int mode, bool bwd = false) {
   ChunkWs w{};
   if (B < 0 || T < 0 || Hk < 0 || Hv < 0 || dk < 0 || dv < 0 || N < 0) return w;
   const size_t tokens = (size_t)(B * T);
@@ -69,7 +69,7 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
   const size_t elem = mode == omx::kModeF32 ? 4 : 2;
   size_t o = 0;
   w.rec = o;
-  o += align_up(slots * (size_t)Hv * (size_t)omx::chunk_record_bytes(mode), 256);
+  o += align_up(slots * (size_t)Hv * (size_t)omx::chunk_record_bytes(mode, bwd), 256);
   w.kn = o;
   o += align_up(tokens * (size_t)(Hk * dk) * elem, 256);
   w.qn = o;
@@ -104,7 +104,7 @@ struct BwdWs {
 BwdWs bwd_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
              int mode) {
   BwdWs w{};
-  w.f = chunk_ws(B, T, Hk, Hv, dk, dv, N, mode);
+  w.f = chunk_ws(B, T, Hk, Hv, dk, dv, N, mode, true);  // records with P's lo parts
   if (B < 0 || T < 0 || Hk < 0 || Hv < 0 || dk < 0 || dv < 0 || N < 0) return w;
   const size_t tokens = (size_t)(B * T);
   const size_t slots = (tokens + 63) / 64 + (size_t)N;

@@ -36,7 +36,7 @@ constexpr int kNPairs = 6;                     // (i, p): (0,0) (1,0) (2,0) (2,1
 constexpr int kRecT = 0;                       // 6 pairs x {hi, lo}
 constexpr int kRecP = kRecT + 2 * kNPairs * kPairBytes;  // 6 pairs (hi)
 constexpr int kRecG = kRecP + kNPairs * kPairBytes;      // 4 x 64 fp32 gate vectors
-constexpr int kRecPL = kRecG + 4 * kC * 4;               // fp32 inputs: P lo parts
+constexpr int kRecPL = kRecG + 4 * kC * 4;               // fp32 inputs, backward: P lo parts
 constexpr int kRecBytesBF16 = kRecPL;                    // 19456
 constexpr int kRecBytesF32 = kRecPL + kNPairs * kPairBytes;  // 25600
 // rows of the gate block: e^G, scale e^G, e^{G_last - G} (its last entry, always 1, is
@@ -51,8 +51,11 @@ constexpr int kXlpgX = 0, kXlpgLg = kXlpgMat, kXlpgP = 2 * kXlpgMat, kXlpgG = 3 
 constexpr int kXlpgFloats = 3 * kXlpgMat + kC;
 static_assert(kXlpgFloats == kXlpgFloatsHost, "backward extras layout");
 
-__host__ __device__ constexpr int rec_bytes(int mode) {
-  return mode == MODE_F32 ? kRecBytesF32 : kRecBytesBF16;
+// Backward records (the recompute's prep and scan) carry P's lo parts with either input
+// dtype: the layer backward's o, whose norm adjoint divides by its row RMS, is formed from
+// split operands there.
+__host__ __device__ constexpr int rec_bytes(int mode, bool bwd = false) {
+  return mode == MODE_F32 || bwd ? kRecBytesF32 : kRecBytesBF16;
 }
 // base + off bytes; a uniform 64-bit base plus a 32-bit lane offset is one
 // scalar-base memory instruction with no per-lane 64-bit address arithmetic

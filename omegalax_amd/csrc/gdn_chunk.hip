@@ -50,7 +50,7 @@ constexpr int kBlockCols = 64;  // dv columns per block of the other kernels (nb
 // NWC_: 16-column state tiles (compute wavefronts) per workgroup.  Four on every path;
 // the direct-load path also runs with two or one, so that sequences x heads x dv / 16 tiles
 // fill the chip when 64-column workgroups would leave CUs idle.
-template <int DK, int MODE, int NWC_ = 4>
+template <int DK, int MODE, int NWC_ = 4, bool BWD_ = false>
 struct Cfg {
   static constexpr int NWC = NWC_;
   static constexpr int BV = 16 * NWC;  // state columns per workgroup
@@ -63,8 +63,10 @@ struct Cfg {
   static constexpr int SEGS = DK / 8;           // 8-element segments per q/k row
   static constexpr int NI_KQ = 2 * C * SEGS / NT;
   static constexpr int NI_V = C * (BV / 8) / NT;
-  static constexpr int REC = rec_bytes(MODE);
+  static constexpr int REC = rec_bytes(MODE, BWD_);
   static constexpr int NREC16 = REC / 16;
+  // 16-byte pieces read per chunk: a backward scan that forms no o skips P's lo parts
+  static constexpr int NREC16_NO_O = rec_bytes(MODE) / 16;
   static constexpr int NI_R = (NREC16 + NT - 1) / NT;
   // bf16 rows with dk = 128 are loaded straight from global memory into one of two
   // LDS buffers (no register staging): unpadded rows with XOR-swizzled 16-byte
@@ -88,9 +90,9 @@ struct Cfg {
 };
 
 // Per-thread register prefetch of one chunk's inputs.
-template <int DK, int MODE>
+template <int DK, int MODE, bool BWD>
 struct Prefetch {
-  using Q_ = Cfg<DK, MODE>;
+  using Q_ = Cfg<DK, MODE, 4, BWD>;
   u32x4 kq[Q_::NI_KQ][Q_::RAWW];
   u32x4 v[Q_::NI_V][Q_::RAWW];
   u32x4 rec[Q_::NI_R];
@@ -100,19 +102,20 @@ struct Prefetch {
 // chunk-uniform base (scalar registers) plus a per-thread 32-bit offset that does not
 // change from chunk to chunk; only a sequence's last, partial chunk clamps its rows
 // (rows past the end load the last valid row, in bounds, and staging zeroes them).
-template <int DK, int MODE>
-__device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE>& pf,
+template <int DK, int MODE, bool BWD>
+__device__ __forceinline__ void prefetch(const ChunkParams& p, Prefetch<DK, MODE, BWD>& pf,
                                          long long t0, int nvalid, const unsigned char* rec,
                                          int hk, int h, int col0) {
-  using Q_ = Cfg<DK, MODE>;
+  using Q_ = Cfg<DK, MODE, 4, BWD>;
   constexpr int NT = Q_::NT, BV = Q_::BV;
   constexpr bool F32 = MODE == MODE_F32;
   using In = typename std::conditional<F32, float, bf16_t>::type;
   const int tid = threadIdx.x;
+  const int nrec16 = BWD && !p.o ? Q_::NREC16_NO_O : Q_::NREC16;
 #pragma unroll
   for (int k = 0; k < Q_::NI_R; ++k) {
     const int it = tid + k * NT;
-    if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) pf.rec[k] = ((const u32x4*)rec)[it];
+    if (it < nrec16) pf.rec[k] = ((const u32x4*)rec)[it];
   }
   const unsigned ksl = (unsigned)p.ks_ld, qsl = (unsigned)p.qs_ld, vsl = (unsigned)p.vs_ld;
   const In* kb = (const In*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
@@ -211,12 +214,12 @@ typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
 // The buffers are passed as LDS-space pointers (cast where the __shared__ arrays are
 // named), so no generic-to-LDS conversion happens here.
-template <int DK, int MODE, int BV>
+template <int DK, int MODE, int BV, bool BWD>
 __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, int nvalid,
                                           const unsigned char* rec, int hk, int h, int col0,
                                           lds_bf16* sK, lds_bf16* sQ, lds_bf16* sV, lds_u8* sRec) {
   typedef __attribute__((address_space(1))) void glob_void;
-  constexpr int NRP = rec_bytes(MODE) / 1024;
+  constexpr int NRP = rec_bytes(MODE) / 1024, NRPX = rec_bytes(MODE, BWD) / 1024;
   // V rows: SV 16-byte segments per row, 64 / SV rows per instruction, SV instructions
   constexpr int SV = BV / 8, RPI = 64 / SV;
   const int l = lane_id();
@@ -272,6 +275,15 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
   for (int mi = 0; mi < NRP; ++mi)
     __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
                                      (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+  // (backward) P's lo parts, read where o is formed
+  if constexpr (NRPX > NRP) {
+    if (p.o) {
+#pragma unroll
+      for (int mi = NRP; mi < NRPX; ++mi)
+        __builtin_amdgcn_global_load_lds((glob_void*)(rec + 1024 * mi + 16 * l),
+                                         (lds_void*)(sRec + 1024 * mi), 16, 0, 0);
+    }
+  }
 }
 
 // BWD (the backward pass's recompute): stores the state entering every chunk and V_new,
@@ -281,7 +293,7 @@ template <int DK, int MODE, bool BWD = false, int NWC_ = 4>
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
 // SIMD) instead of holding back for a second workgroup.
 __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE, NWC_>::WPE, Cfg<DK, MODE, NWC_>::WPE))) void scan_kernel(ChunkParams p) {
-  using Q_ = Cfg<DK, MODE, NWC_>;
+  using Q_ = Cfg<DK, MODE, NWC_, BWD>;
   constexpr int NWC = Q_::NWC, BV = Q_::BV, NT = Q_::NT;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
   constexpr bool IS = Q_::IS, OS = Q_::OS;
@@ -351,17 +363,17 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   const unsigned o_elem = (unsigned)lr * o_rs + 16u * wave + 4u * lq;
   const unsigned o_lane = 4u * o_elem, o_lane_h = 2u * o_elem;  // bytes: fp32 o, bf16 o
 
-  Prefetch<DK, MODE> pf;
+  Prefetch<DK, MODE, BWD> pf;
   if (nchunks > 0) {
     const int nv0 = (int)((s1 - s0) < C ? (s1 - s0) : C);
     if constexpr (DIRECT) {
       if (loader) {
-        stage_all<DK, MODE, BV>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
+        stage_all<DK, MODE, BV, BWD>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
                             (lds_bf16*)sV0, (lds_u8*)sRec0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the first barrier
       }
     } else {
-      prefetch<DK, MODE>(p, pf, s0, nv0, rec_of(0), hk, h, col0);
+      prefetch<DK, MODE, BWD>(p, pf, s0, nv0, rec_of(0), hk, h, col0);
     }
   }
 
@@ -427,17 +439,18 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         *(u32x4*)dst = pf.v[k][0] & keep;
       }
     }
+    const int nrec16 = BWD && !p.o ? Q_::NREC16_NO_O : Q_::NREC16;
 #pragma unroll
     for (int k = 0; k < Q_::NI_R; ++k) {
       const int it = tid + k * NT;
-      if (Q_::NI_R * NT == Q_::NREC16 || it < Q_::NREC16) ((u32x4*)sRec)[it] = pf.rec[k];
+      if (it < nrec16) ((u32x4*)sRec)[it] = pf.rec[k];
     }
     __syncthreads();
 
     // issue the next chunk's loads; they land during the rest of this chunk
     if (j + 1 < nchunks) {
       const long long tn = t0 + C;
-      prefetch<DK, MODE>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), rec_of(j + 1), hk, h,
+      prefetch<DK, MODE, BWD>(p, pf, tn, (int)((s1 - tn) < C ? (s1 - tn) : C), rec_of(j + 1), hk, h,
                          col0);
     }
     }
@@ -494,7 +507,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 #pragma unroll
     for (int s2 = 0; s2 < NSK; ++s2) {
       sh[s2] = join(pack_hi4(S[2 * s2]), pack_hi4(S[2 * s2 + 1]));
-      if constexpr (IS) sl[s2] = join(pack_lo4(S[2 * s2]), pack_lo4(S[2 * s2 + 1]));
+      // (backward) the lo half also enters Q S, for the o that the norm's adjoint reads
+      if constexpr (IS || BWD) sl[s2] = join(pack_lo4(S[2 * s2]), pack_lo4(S[2 * s2 + 1]));
       else sl[s2] = sh[s2];
     }
     f32x4 KS[4], QS[4];
@@ -509,6 +523,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
       for (int i = 0; i < 4; ++i) {  // eight independent accumulation chains
         KS[i] = mm<IS, IS>(KS[i], kh[i][s2], kl[i][s2], sh[s2], sl[s2]);
         if constexpr (!DEFER_QS) QS[i] = mm<IS, IS>(QS[i], sh[s2], sl[s2], qh[i][s2], ql[i][s2]);  // (Q S)^T
+        if constexpr (BWD && !IS && !DEFER_QS)
+          if (p.o) QS[i] = mma16(sl[s2], qh[i][s2], QS[i]);
       }
     if constexpr (DIRECT && !IS) {
       // all fragment reads go out back to back, then the state packs, then the
@@ -588,7 +604,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       Uh[pp] = join(pack_hi4(U[2 * pp]), pack_hi4(U[2 * pp + 1]));
-      if constexpr (OS) Ul[pp] = join(pack_lo4(U[2 * pp]), pack_lo4(U[2 * pp + 1]));
+      if constexpr (OS || BWD) Ul[pp] = join(pack_lo4(U[2 * pp]), pack_lo4(U[2 * pp + 1]));
     }
     // P operands and the K^T operands of the state update (read while V_new forms)
     u32x4 ph[kNPairs], pl[kNPairs];
@@ -657,6 +673,12 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
     // or 8-byte (bf16) store per row block, and one gate factor per lane.
     if constexpr (BWD) {
       if (!p.o) return;  // the layer backward also needs o (for its norm's adjoint)
+      // its o comes from split operands throughout (S, V_new and P hi and lo): the adjoint
+      // scales by the row's 1 / RMS, which is large where o's terms nearly cancel
+      if constexpr (!OS) {
+#pragma unroll
+        for (int x = 0; x < kNPairs; ++x) pl[x] = *(const u32x4*)(sRec + kRecPL + x * kPairBytes + 16 * l);
+      }
     }
     if constexpr (DEFER_QS) {
       // (Q S)^T from the chunk's entering state, still held packed in sh
@@ -667,7 +689,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 #pragma unroll
       for (int s2 = 0; s2 < NSK; ++s2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) QS[i] = mma16(sh[s2], qh[i][s2], QS[i]);
+        for (int i = 0; i < 4; ++i) {
+          QS[i] = mma16(sh[s2], qh[i][s2], QS[i]);
+          if constexpr (BWD) QS[i] = mma16(sl[s2], qh[i][s2], QS[i]);
+        }
     }
     f32x4 o[4];
 #pragma unroll
@@ -679,7 +704,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
       for (int pp = 0; pp <= i / 2; ++pp) {  // P is lower triangular
         const int x = pair_index(i, pp);
         o[i] = mma16(Uh[pp], ph[x], o[i]);
-        if constexpr (OS) {
+        if constexpr (OS || BWD) {
           o[i] = mma16(Ul[pp], ph[x], o[i]);
           o[i] = mma16(Uh[pp], pl[x], o[i]);
         }
@@ -756,7 +781,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         if (j + 1 < nchunks) {
           const long long tn = s0 + (long long)(j + 1) * C;
           const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
-          stage_all<DK, MODE, BV>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
+          stage_all<DK, MODE, BV, BWD>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
         }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the next barrier
         if (j >= 2) store_ss(j - 2);  // written after barrier j - 1, visible after barrier j
@@ -830,7 +855,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 // blocks) is replaced by the scan's own count in a copy of the parameters.
 template <int DK, int MODE, bool BWD = false, int NWC = 4>
 hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
-  using Q_ = Cfg<DK, MODE, NWC>;
+  using Q_ = Cfg<DK, MODE, NWC, BWD>;
   ChunkParams q = p;
   q.nb = p.DV / Q_::BV;
   // (layer) row-sum partials per (token, value head): one per workgroup with direct
@@ -884,7 +909,7 @@ int layer_ss_slots(const ChunkParams& p) {
   return p.dk == 128 ? p.DV / (16 * scan_tiles_per_wg(p)) : p.DV / 16;
 }
 
-int chunk_record_bytes(int mode) { return rec_bytes(mode); }
+int chunk_record_bytes(int mode, bool bwd) { return rec_bytes(mode, bwd); }
 
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
   if (dv % kBlockCols != 0 || dv > 256) return false;

@@ -133,7 +133,7 @@ bool chunk_dims_supported(int dk, int dv, bool f32_inputs);
 int chunk_block_cols();
 bool layer_dims_supported(int dk, int dv);
 // bytes of one (chunk, value head) record for a mode
-int chunk_record_bytes(int mode);
+int chunk_record_bytes(int mode, bool bwd = false);
 // cu_in -> the ordered offsets cu_seqlens and chunk_off (one workgroup); then the
 // preparation kernel and the scan
 hipError_t launch_chunk_plan(const ChunkParams& p, hipStream_t stream);

@@ -510,7 +510,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
     }
 
     float* gw = sGw + wave * 2 * C;  // this wave's G log2(e) [0, C) and beta [C, 2C)
-    const size_t rec_stride = (size_t)rec_bytes(MODE);
+    const size_t rec_stride = (size_t)rec_bytes(MODE, BWD);
 
     for (int gg = 0; gg < gqa; ++gg) {
       const int h = hk * gqa + gg;
@@ -670,7 +670,8 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
               put_tile(rec, rec_t_off(bi, bi + 1), z);
               put_tile(rec, rec_t_off(bi, bi + 1) + kPairBytes, z);
               put_tile(rec, rec_p_off(bi, bi + 1), z);
-              if constexpr (IS) put_tile(rec, rec_p_off(bi, bi + 1) + (kRecPL - kRecP), z);
+              if constexpr (IS || BWD)
+                if (IS || p.o) put_tile(rec, rec_p_off(bi, bi + 1) + (kRecPL - kRecP), z);
             }
           } else {
             u32x2* d = sLf + 2 * 64 * tile_index(bi, bj) + l;
@@ -686,7 +687,9 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
           }
           put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
           if constexpr (BWD) put_f32_tile(xb + kXlpgP, bi, bj, val);
-          if constexpr (IS) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
+          // (backward) P's lo parts only where the scan forms o: the layer backward
+          if constexpr (IS || BWD)
+            if (IS || p.o) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
         }
       }
       lds_barrier();  // L blocks and the diagonal inverses of all waves are in LDS

@@ -1,4 +1,5 @@
-"""GPU parity over seeded random layer shapes: prefill, then one cached decode step.
+"""GPU parity over seeded random layer shapes: prefill, then one cached decode step; and
+the layer backward.
 
 Each case draws its head layout (Hk, gqa, dk, dv, with dims the kernels are and are not
 compiled for), a batch or a packed batch with initial states and conv history, runs
@@ -6,6 +7,7 @@ omx_gdn_prefill through the torch binding, continues every sequence by one decod
 from the returned caches, and compares both with the oracle (deltanet.py:243-293 for the
 prefill; the HF cached step for the decode).  Tolerances: bf16 outputs 2e-2, fp32 state
 1e-3 (max-abs-normalised); conv caches are raw data movement and must match bit for bit.
+The backward cases compare omx_gdn_prefill_bwd with the fp64 layer VJP oracle.
 """
 import sys
 
@@ -98,3 +100,54 @@ def test_random_layer_shape_prefill_then_decode(seed):
     assert rel(np_(out1), ref1) < BF16_TOL
     assert rel(np_(S), S_ref1) < STATE_TOL
     assert np.array_equal(np_(conv), conv_ref1)
+
+
+BWD_NAMES = ("dx", "dz", "da", "db", "dconv_w", "dA_log", "ddt_bias", "dnorm_w", "dh0")
+
+
+@pytest.mark.parametrize("seed", range(2200, 2208))
+def test_random_layer_shape_backward(seed):
+    """The layer VJP (omx_gdn_prefill_bwd) against the fp64 VJP oracle on random shapes with
+    head dims up to 128 (the backward's limit), packed or not, with initial states.
+    Gradient tolerances: 2e-2 (bf16-returned activations and their parameter sums), 1e-3
+    for the fp32 initial-state gradient."""
+    from oracle import gdn_vjp as V
+    from omegalax_amd import gdn_prefill_bwd
+    rng = np.random.default_rng(seed)
+    Hk = int(rng.choice([1, 2]))
+    Hv = Hk * int(rng.choice([1, 2, 4]))
+    dk = int(rng.choice([16, 32, 48, 64, 96, 128]))
+    dv = int(rng.choice([16, 32, 64, 80, 128]))
+    if bool(rng.integers(0, 2)):
+        lens = rng.integers(0, 100, size=int(rng.integers(1, 5)))
+        lens[0] = max(int(lens[0]), 1)
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        B, T, N = 1, int(cu[-1]), len(lens)
+    else:
+        cu = None
+        B, T = int(rng.integers(1, 3)), int(rng.integers(1, 160))
+        N = B
+    print(f"random backward seed={seed} Hk={Hk} Hv={Hv} dk={dk} dv={dv} B={B} T={T} N={N} "
+          f"packed={cu is not None}", flush=True)
+    sys.stdout.flush()
+    dims = dict(Hk=Hk, dk=dk, Hv=Hv, dv=dv)
+    d = W.layer_inputs(B, T, **dims, seed=seed)
+    S0 = (0.02 * rng.standard_normal((N, Hv, dk, dv))).astype(np.float32)
+    dout = O.round_bf16(rng.standard_normal((B, T, Hv * dv)))
+    dS = (0.1 * rng.standard_normal((N, Hv, dk, dv))).astype(np.float32)
+    t = W.to_device(d)
+    dev = lambda x: torch.from_numpy(np.ascontiguousarray(x)).cuda()  # noqa: E731
+    got = gdn_prefill_bwd(
+        t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"], t["dt_bias"],
+        t["norm_w"], dev(dout).bfloat16(), num_k_heads=Hk, head_k_dim=dk, num_v_heads=Hv,
+        head_v_dim=dv, cu_seqlens=None if cu is None else dev(cu).int(),
+        initial_state=dev(S0), d_final_state=dev(dS))
+    torch.cuda.synchronize()
+    ref = V.gdn_prefill_layer_bwd(
+        d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"], d["A_log"], d["dt_bias"],
+        d["norm_w"], dout, **dims, cu_seqlens=cu, initial_state=S0, d_final_state=dS,
+        act_round=O.round_bf16)
+    for name, g, r in zip(BWD_NAMES, got, ref):
+        tol = STATE_TOL if name == "dh0" else BF16_TOL
+        err = rel(np_(g), r)
+        assert err < tol, (name, err)
