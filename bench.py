@@ -182,9 +182,9 @@ MEASURED_TRAFFIC = {
     ("core", 1, 65536, 16, 64, 128): (7_707_787_264, "profiles/prefill_c3_c4.md (C4 core call)"),
     ("decode", 64, 16, 32, 128): (277_278_720, "profiles/decode_step_c2.md (B=64)"),
     ("decode", 256, 16, 32, 128): (1_107_987_251, "profiles/decode_step_c2.md (B=256)"),
-    # layer step: prep 303.2 + 409.8 MiB, scan 408.3 + 128.0, epilogue 256.0 + 128.0
-    ("prefill", 4, 4096, 16, 32, 128): (1_740_128_870, "profiles/prefill_c1.md (layer kernels)"),
-    ("c3", 32768, 8): (3_533_385_523, "profiles/prefill_c3_c4.md (C3 layer call)"),
+    # layer step: prep 154.1 + 281.7 MiB, scan 408.6 + 132.0, epilogue 272.0 + 128.0
+    ("prefill", 4, 4096, 16, 32, 128): (1_443_268_915, "profiles/prefill_c1.md (layer kernels)"),
+    ("c3", 32768, 8): (2_954_456_781, "profiles/prefill_c3_c4.md (C3 layer call)"),
     ("bwd", 4, 4096, 16, 32, 128): (7_553_046_835, "profiles/bwd_c1.md (backward call)"),
 }
 

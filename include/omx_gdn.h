@@ -130,7 +130,8 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
 
 /*
  * Bytes of device workspace omx_gdn_prefill needs (16-byte aligned): the chunk
- * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v, and
+ * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v (dk < 128
+ * after padding; with dk = 128 the scan forms the v rows from mixed_qkv itself), and
  * what the gated-norm epilogue reads: the unnormalised bf16 o and the fp32 sums of
  * squares of o per 16 columns of each row.
  */
@@ -147,7 +148,7 @@ size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t 
  * and no allocating library routine.
  *   Arguments, layouts and results are those of omx_gdn_prefill.  Shapes whose workspace
  * exceeds the fixed size are rejected with OMX_GDN_EINVAL (at the Qwen3.5 head layout,
- * Hk=16 Hv=32 d=128, about 1,850 tokens per call).  Every call on one GPU uses that
+ * Hk=16 Hv=32 d=128, about 2,400 tokens per call).  Every call on one GPU uses that
  * GPU's one array: calls that overlap on one GPU (other streams, other threads) race
  * and give undefined results; serialise them.  Nothing in the scratch needs to start
  * at zero: every region is written before it is read within a call.

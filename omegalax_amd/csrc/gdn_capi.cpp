@@ -53,7 +53,8 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // Workspace of the chunked prefill, offsets aligned to 256 bytes: the records of
 // the preparation kernel (one per chunk slot and value head; a sequence adds at
 // most one partial chunk, so ceil(tokens/64) + N slots cover any packing), the
-// normalised k and q, (layer) the conv output of v, the bf16 o and the partial
+// normalised k and q, (layer) the conv output of v (dk < 128: with dk = 128 the scan
+// forms the v rows itself), the bf16 o and the partial
 // sums of o^2 for the gated norm, and the plan of packed sequences (chunk offsets and
 // the ordered copy of cu_seqlens the kernels read).
 struct ChunkWs {
@@ -76,7 +77,7 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
   o += align_up(tokens * (size_t)(Hk * dk) * elem, 256);
   if (mode == omx::kModeLayer) {
     w.vc = o;
-    o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
+    if (!omx::layer_scan_forms_v((int)dk)) o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
     w.opart = o;
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
     w.oss = o;
@@ -296,7 +297,7 @@ void setup_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int 
     p.qs_ld = p.q_ld;
   }
   if (mode == omx::kModeLayer) {
-    p.vc = base + ws.vc;
+    p.vc = omx::layer_scan_forms_v(p.dk) ? nullptr : base + ws.vc;
     p.vs = p.vc;
     p.vs_ld = (long long)p.Hv * p.DV;
   } else {

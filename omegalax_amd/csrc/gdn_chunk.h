@@ -51,6 +51,10 @@ constexpr int kXlpgX = 0, kXlpgLg = kXlpgMat, kXlpgP = 2 * kXlpgMat, kXlpgG = 3 
 constexpr int kXlpgFloats = 3 * kXlpgMat + kC;
 static_assert(kXlpgFloats == kXlpgFloatsHost, "backward extras layout");
 
+// Layer mode with dk = 128 (the scan's direct-load path): the value channels' conv +
+// SiLU runs in the scan's helper wavefronts, so the prep forms the q and k rows only.
+__host__ __device__ constexpr bool layer_v_in_scan(int dk) { return dk == 128; }
+
 // Backward records (the recompute's prep and scan) carry P's lo parts with either input
 // dtype: the layer backward's o, whose norm adjoint divides by its row RMS, is formed from
 // split operands there.

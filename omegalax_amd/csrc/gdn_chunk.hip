@@ -23,13 +23,17 @@
 // two C-layout tiles of R or V_new side by side.  With bf16 inputs and dk = 128
 // the next chunk's K, Q, V rows and record are loaded straight into the other of
 // two LDS buffers while the current chunk computes (one workgroup barrier per
-// chunk); otherwise they are staged through registers.
+// chunk); otherwise they are staged through registers.  On the layer path with
+// dk = 128 two helper wavefronts form the next chunk's V rows instead (conv + SiLU of
+// mixed_qkv's value channels, deltanet.py:243), so the preparation kernel neither
+// reads the value channels nor writes conv(v) to the workspace.
 //
 // Precision.  MFMA inputs are bf16 with fp32 accumulation.  K, Q, V are bf16 on
 // the bf16 and layer paths (exact), or fp32 split into hi+lo bf16 pairs
 // (MODE_F32).  T and the right-hand side R enter V_new = T R as hi+lo pairs, and
 // so does the state-update operand diag(e^{G_last-G}) V_new; with bf16 inputs S
-// enters K S / Q S, and P, V_new enter P V_new, as single bf16.
+// enters K S / Q S, and P, V_new enter P V_new, as single bf16, except in the layer
+// backward's recompute (BWD with p.o set), which forms o from hi+lo S, V_new and P.
 //
 // Modes: MODE_BF16 / MODE_F32 (core function) store o in fp32.  MODE_LAYER stores
 // o in bf16; the epilogue kernel (gdn_epilogue.hip) applies the gated RMSNorm
@@ -37,6 +41,7 @@
 #include <type_traits>
 
 #include "gdn_chunk.h"
+#include "gdn_conv.h"
 #include "gdn_kernels.h"
 
 namespace omx {
@@ -73,10 +78,14 @@ struct Cfg {
   // segments.  fp32 inputs (split on staging) and dk = 64 stage through registers
   // into padded rows.
   static constexpr bool DIRECT = MODE != MODE_F32 && DK == 128;
-  // with direct loads one more wavefront issues them; next to four compute wavefronts it
-  // shares a SIMD with one of them, so each may hold at most half the register file
-  static constexpr int NTH = DIRECT ? NT + 64 : NT;
-  static constexpr int WPE = DIRECT && NWC == 4 ? 2 : 1;
+  // (layer, direct loads) the value channels' conv + SiLU runs here, in NH helper
+  // wavefronts that form the next chunk's V rows while the compute wavefronts scan
+  static constexpr bool VCONV = MODE == MODE_LAYER && layer_v_in_scan(DK);
+  static constexpr int NH = VCONV ? 2 : 0;
+  // with direct loads one more wavefront issues them (and NH more form V); sharing SIMDs
+  // with the compute wavefronts, each may then hold at most half the register file
+  static constexpr int NTH = DIRECT ? NT + 64 * (1 + NH) : NT;
+  static constexpr int WPE = (NTH / 64 + 3) / 4;
   static constexpr int NBUF = DIRECT ? 2 : 1;
   static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
   static constexpr int SZV = DIRECT ? C * BV : NS * C * LDT;  // elements of a V buffer
@@ -87,6 +96,8 @@ struct Cfg {
   static_assert(DIRECT || NWC == 4, "register staging runs four column wavefronts");
   static_assert(NI_KQ * NT == 2 * C * SEGS && (C * SEGS) % NT == 0, "item split");
   static_assert(NI_V * NT == C * (BV / 8), "item split");
+  static_assert(!VCONV || DIRECT, "the helper wavefronts run beside the direct loads");
+  static_assert(!VCONV || (BV / 8) * (C / (BV / 16)) == 64 * NH, "one V task per helper lane");
 };
 
 // Per-thread register prefetch of one chunk's inputs.
@@ -220,6 +231,7 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                           lds_bf16* sK, lds_bf16* sQ, lds_bf16* sV, lds_u8* sRec) {
   typedef __attribute__((address_space(1))) void glob_void;
   constexpr int NRP = rec_bytes(MODE) / 1024, NRPX = rec_bytes(MODE, BWD) / 1024;
+  constexpr bool VCONV = MODE == MODE_LAYER && layer_v_in_scan(DK);  // V rows: helper wavefronts
   // V rows: SV 16-byte segments per row, 64 / SV rows per instruction, SV instructions
   constexpr int SV = BV / 8, RPI = 64 / SV;
   const int l = lane_id();
@@ -244,12 +256,14 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
                                          (lds_void*)(sQ + 512 * mi), 16, 0, 0);
       }
     }
-    const unsigned vrow = (unsigned)(l / SV);
-    const unsigned vo = 2u * (vrow * vld + 8u * (unsigned)((l % SV) ^ swz_v<SV>((int)vrow)));
+    if constexpr (!VCONV) {
+      const unsigned vrow = (unsigned)(l / SV);
+      const unsigned vo = 2u * (vrow * vld + 8u * (unsigned)((l % SV) ^ swz_v<SV>((int)vrow)));
 #pragma unroll
-    for (int mi = 0; mi < SV; ++mi)
-      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb + (long long)(RPI * mi) * p.vs_ld, vo),
-                                       (lds_void*)(sV + 512 * mi), 16, 0, 0);
+      for (int mi = 0; mi < SV; ++mi)
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb + (long long)(RPI * mi) * p.vs_ld, vo),
+                                         (lds_void*)(sV + 512 * mi), 16, 0, 0);
+    }
   } else {
     // a sequence's last, partial chunk: rows past its end repeat the last valid row
 #pragma unroll
@@ -262,13 +276,15 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
       __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(qb, 2u * (rr * qld + 8u * g)),
                                        (lds_void*)(sQ + 512 * mi), 16, 0, 0);
     }
+    if constexpr (!VCONV) {
 #pragma unroll
-    for (int mi = 0; mi < SV; ++mi) {
-      const int row = RPI * mi + l / SV;
-      const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
-      const unsigned g = (unsigned)((l % SV) ^ swz_v<SV>(row));
-      __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, 2u * (rr * vld + 8u * g)),
-                                       (lds_void*)(sV + 512 * mi), 16, 0, 0);
+      for (int mi = 0; mi < SV; ++mi) {
+        const int row = RPI * mi + l / SV;
+        const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
+        const unsigned g = (unsigned)((l % SV) ^ swz_v<SV>(row));
+        __builtin_amdgcn_global_load_lds((glob_void*)at_bytes(vb, 2u * (rr * vld + 8u * g)),
+                                         (lds_void*)(sV + 512 * mi), 16, 0, 0);
+      }
     }
   }
 #pragma unroll
@@ -320,6 +336,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool loader = DIRECT && wave == NWC;  // issues the direct loads, computes nothing
+  const bool helper = Q_::VCONV && wave > NWC;  // forms the V rows (layer, direct loads)
+  const bool compute = wave < NWC;             // owns 16 state columns
   // XCD-aware work item (scan_item): a key head's workgroups share one XCD's L2, and
   // packed sequences start longest first
   const ScanItem item = scan_item(p.seq_order, p.N, p.Hk, p.Hv, p.nb);
@@ -343,7 +361,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   // S[t][v] = S[state_row(t, lq, v)][16w + lr]
   f32x4 S[DK / 16];
   const size_t state_off = ((size_t)n * p.Hv + h) * DK * DV + col0 + 16 * wave + lr;
-  if (p.initial_state && !loader) {
+  if (p.initial_state && compute) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
@@ -798,6 +816,57 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           store_ss(nchunks - 1);
         }
       }
+    } else if (helper) {
+      if constexpr (Q_::VCONV) {
+        // one barrier per chunk, as the loader: after the barrier at the top of chunk j,
+        // V buffer (j + 1) % 2 is free and receives chunk j + 1's rows; chunk 0's are
+        // formed before the first barrier
+        // Conv + SiLU of the value channels chu .. chu + BV - 1 with the prep's arithmetic
+        // (gdn_conv.h), stored in the swizzled layout the compute wavefronts read.  Helper
+        // lane hl (0 .. 127) forms 8 channels of R = BV / 16 consecutive rows, with its
+        // weights loaded once; rows past the sequence end are zero.  A chunk's input rows
+        // are loaded one chunk step ahead (two register sets; loads past the last chunk
+        // repeat it), so their latency is off the step.
+        constexpr int SV = BV / 8, R = BV / 16;
+        const int hl = tid - 64 * (NWC + 1);
+        const int g = hl % SV, r0 = (hl / SV) * R;
+        const int chu = 2 * p.Hk * DK + h * DV + col0;
+        uint32_t wp[8][2];
+        load_conv_w(p, chu, 8 * g, wp);
+        auto nv_of = [&](int j) {
+          const long long tj = s0 + (long long)j * C;
+          return (int)((s1 - tj) < C ? (s1 - tj) : C);
+        };
+        auto load = [&](int j, u32x4* raw) {
+          const int jj = j < nchunks ? j : nchunks - 1;
+          conv_load<R>(p, n, s0, s0 + (long long)jj * C, nv_of(jj), r0, chu, 8 * g, raw);
+        };
+        auto form = [&](int j, const u32x4* raw, bf16_t* nV) {
+          conv_compute<R>(raw, wp, nv_of(j), r0, [&](int m, const u32x4& y) {
+            *(u32x4*)(nV + swz_off<BV>(r0 + m, 8 * g)) = y;
+          });
+        };
+        u32x4 ra[R + 3], rb[R + 3];
+        if (nchunks > 0) {
+          load(0, ra);
+          load(1, rb);
+          form(0, ra, sV0);
+        }
+        for (int j = 0; j < nchunks; j += 2) {
+          lds_barrier();
+          if (j + 1 < nchunks) {
+            load(j + 2, ra);
+            form(j + 1, rb, sV1);
+            lds_barrier();
+            load(j + 3, rb);
+            if (j + 2 < nchunks) form(j + 2, ra, sV0);
+          }
+        }
+        if (nchunks > 0) {  // the loader's two barriers after its loop
+          lds_barrier();
+          lds_barrier();
+        }
+      }
     } else {
       for (int j = 0; j < nchunks; j += 2) {
         run_chunk(j, sK0, sQ0, sV0, sRec0);
@@ -815,7 +884,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
     for (int j = 0; j < nchunks; ++j) run_chunk(j, sK0, sQ0, sV0, sRec0);
   }
 
-  if (p.final_state && !loader) {
+  if (p.final_state && compute) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
@@ -918,6 +987,8 @@ bool chunk_dims_supported(int dk, int dv, bool f32_inputs) {
 }
 
 bool layer_dims_supported(int dk, int dv) { return chunk_dims_supported(dk, dv, false); }
+
+bool layer_scan_forms_v(int dk) { return layer_v_in_scan(dk); }
 
 hipError_t launch_scan_bwd(const ChunkParams& p, int mode, hipStream_t stream) {
   if (mode == MODE_F32) {

@@ -132,6 +132,9 @@ constexpr int kModeBF16 = 0, kModeF32 = 1, kModeLayer = 2;
 bool chunk_dims_supported(int dk, int dv, bool f32_inputs);
 int chunk_block_cols();
 bool layer_dims_supported(int dk, int dv);
+// (layer) whether the scan forms the v rows itself (conv + SiLU), so the workspace holds
+// no conv(v) rows
+bool layer_scan_forms_v(int dk);
 // bytes of one (chunk, value head) record for a mode
 int chunk_record_bytes(int mode, bool bwd = false);
 // cu_in -> the ordered offsets cu_seqlens and chunk_off (one workgroup); then the

@@ -5,7 +5,8 @@
 // here, for all chunks at once, one workgroup per (chunk, key head):
 //   * q, k rows: (layer path) causal depthwise conv + SiLU (deltanet.py:35-50,
 //     243), then the L2 norm at input precision (:30-32, 65-66); written to the
-//     workspace for the scan.  (layer path) v rows: conv + SiLU, written likewise.
+//     workspace for the scan.  (layer path, dk = 64) v rows: conv + SiLU, written
+//     likewise; with dk = 128 the scan forms them from mixed_qkv itself.
 //   * the Gram products K K^T and Q K^T of the key head, once for all gqa value
 //     heads that share it (the repeat-interleave of :272-280);
 //   * per value head: the gates (:248-250 on the layer path), G = cumsum(g)
@@ -25,6 +26,7 @@
 // symmetric; (Q K^T)^T = K Q^T), and the off-diagonal T blocks a second time as
 // T_ij^T = -X^T T_ii^T from the same two operands.
 #include "gdn_chunk.h"
+#include "gdn_conv.h"
 #include "gdn_kernels.h"
 
 namespace omx {
@@ -98,121 +100,6 @@ __device__ __forceinline__ f32x4 col_beta(const float* gw, int bj) {
 // one 16x16 tile's A fragment into its half of a record pair (16 bytes per lane)
 __device__ __forceinline__ void put_tile(__amdgpu_buffer_rsrc_t rec, int off, u32x2 f) {
   __builtin_amdgcn_raw_buffer_store_b64(f, rec, 16 * lane_id(), off, 0);
-}
-
-// conv weights of channels ch0..ch0+7, cast to bf16 as at deltanet.py:243, as packed
-// pairs: wp[e][0] = (w_0, w_1), wp[e][1] = (w_2, w_3) with w_d the weight of the input d
-// tokens back (tap K-1-d); taps beyond K are 0
-__device__ __forceinline__ void load_conv_w(const ChunkParams& p, int chu, int chl, uint32_t (*wp)[2]) {
-  const int K = p.conv_k;
-  const int ch0 = chu + chl;
-  if (K == 4) {  // uniform: each channel's taps are one 16-byte row
-    const float* wb = p.conv_w + (size_t)chu * 4;  // uniform base, lane channel offset
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float4 w = *(const float4*)at_bytes(wb, 16u * (unsigned)(chl + e));
-      wp[e][0] = pack_bf16(w.w, w.z);
-      wp[e][1] = pack_bf16(w.y, w.x);
-    }
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float* w = p.conv_w + (size_t)(ch0 + e) * K;
-    float wt[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) wt[d] = d < K ? w[K - 1 - d] : 0.f;
-    wp[e][0] = pack_bf16(wt[0], wt[1]);
-    wp[e][1] = pack_bf16(wt[2], wt[3]);
-  }
-}
-
-// Raw input row of 8 channels at token t: mixed_qkv inside the sequence, the conv
-// cache (oldest slot first) or zeros before it (deltanet.py:46).
-__device__ __forceinline__ u32x4 conv_input(const ChunkParams& p, int n, long long s0, long long t,
-                                            int ch0) {
-  if (t >= s0) return *(const u32x4*)((const bf16_t*)p.mixed_qkv + t * p.conv_dim + ch0);
-  u32x4 w{0u, 0u, 0u, 0u};
-  const int K = p.conv_k;
-  const int slot = (K - 1) - (int)(s0 - t);
-  if (p.conv_state_in && slot >= 0) {
-    const unsigned short* cs =
-        (const unsigned short*)p.conv_state_in + ((size_t)n * p.conv_dim + ch0) * (K - 1) + slot;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      w[e] = (unsigned)cs[(2 * e) * (K - 1)] | ((unsigned)cs[(2 * e + 1) * (K - 1)] << 16);
-  }
-  return w;
-}
-
-// Causal depthwise conv + SiLU (deltanet.py:35-50, 243) of one 8-channel group over
-// chunk rows r0 .. r0+ROWS-1, streaming down the rows.  conv_load issues every input
-// row once (rows r0-3 .. r0+ROWS-1); conv_compute consumes them.  Inputs and weights
-// are bf16 (the weights cast as the reference casts them), the tap sum is two bf16 dot
-// products per channel with fp32 sums, and the sum and the SiLU output are rounded to
-// bf16 like the reference's bf16 ops; rows at or past nvalid give zeros.
-// emit(m, y) receives row r0 + m as 8 packed bf16 values.
-template <int ROWS>
-__device__ __forceinline__ void conv_load(const ChunkParams& p, int n, long long s0, long long t0,
-                                          int nvalid, int r0, int chu, int chl, u32x4* raw) {
-#pragma unroll
-  for (int k = 0; k < ROWS + 3; ++k) {
-    int row = r0 - 3 + k;
-    row = row < nvalid ? row : nvalid - 1;  // padded rows: in bounds, zeroed below
-    raw[k] = conv_input(p, n, s0, t0 + row, chu + chl);
-  }
-}
-
-// The pairs (x_t, x_{t-1}) of the 8 channels from input rows t (cur) and t-1 (prev):
-// word c of pe holds channel 2c's pair, word c of po channel 2c+1's (v_perm_b32).
-__device__ __forceinline__ void time_pairs(const u32x4& cur, const u32x4& prev, u32x4& pe, u32x4& po) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    pe[c] = __builtin_amdgcn_perm(prev[c], cur[c], 0x05040100u);
-    po[c] = __builtin_amdgcn_perm(prev[c], cur[c], 0x07060302u);
-  }
-}
-
-template <int ROWS, class Emit>
-__device__ __forceinline__ void conv_compute(const u32x4* raw, const uint32_t (*wp)[2], int nvalid,
-                                             int r0, Emit emit) {
-  // time pairs of rows m-2 and m-1 (a row's pair holds it and the row before)
-  u32x4 pe2, po2, pe1, po1;
-  time_pairs(raw[1], raw[0], pe2, po2);
-  time_pairs(raw[2], raw[1], pe1, po1);
-#pragma unroll
-  for (int m = 0; m < ROWS; ++m) {
-    u32x4 pe0, po0;
-    time_pairs(raw[m + 3], raw[m + 2], pe0, po0);
-    u32x4 y;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float a0 = dot4_bf16(wp[2 * c][0], wp[2 * c][1], pe0[c], pe2[c]);
-      const float a1 = dot4_bf16(wp[2 * c + 1][0], wp[2 * c + 1][1], po0[c], po2[c]);
-      const uint32_t u = pack_bf16(a0, a1);  // the pre-activations, rounded to bf16
-      y[c] = pack_bf16(silu_fast(__uint_as_float(u << 16)), silu_fast(__uint_as_float(u & 0xffff0000u)));
-    }
-    if (nvalid < kC) {  // uniform: a sequence's last chunk; its padded rows are zero
-      if (r0 + m >= nvalid) y = u32x4{0u, 0u, 0u, 0u};
-    }
-    emit(m, y);
-    pe2 = pe1;
-    po2 = po1;
-    pe1 = pe0;
-    po1 = po0;
-  }
-}
-
-// conv_load then conv_compute, with the window and weights local to the call
-// (channels chu + chl .. +7: chu uniform, chl the lane's part)
-template <int ROWS, class Emit>
-__device__ __forceinline__ void conv_rows(const ChunkParams& p, int n, long long s0, long long t0,
-                                          int nvalid, int r0, int chu, int chl, Emit emit) {
-  u32x4 raw[ROWS + 3];
-  uint32_t wp[8][2];
-  load_conv_w(p, chu, chl, wp);
-  conv_load<ROWS>(p, n, s0, t0, nvalid, r0, chu, chl, raw);
-  conv_compute<ROWS>(raw, wp, nvalid, r0, emit);
 }
 
 // L2 norm of a row spread over W lanes (8 values each), in fp32 like the
@@ -392,18 +279,21 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
 
     // -------------------------------------------------------------- q, k, v rows
     if constexpr (MODE == MODE_LAYER) {
-      // wave 0: k, wave 1: q -- lane = 8-channel group g + SEGS * row part; each lane
-      // streams C / (64 / SEGS) rows, and the SEGS lanes of a row are adjacent, so
-      // the row's L2 norm is a DPP sum.  Waves 2-3: the v channels of the gqa value
-      // heads, 16 rows per item.
-      if (wave < 2) {
-        constexpr int RP = 64 / SEGS, ROWS = C / RP;
-        const int g = l % SEGS, r0 = (l / SEGS) * ROWS;
-        bf16_t* dst = (wave == 0 ? sK : sQ) + 8 * g;
+      // dk = 64: wave 0 forms the k rows, wave 1 the q rows, waves 2-3 the v channels of
+      // the gqa value heads (16 rows per item).  dk = 128, where the scan forms v: waves
+      // 0 and 2 the k rows (top and bottom half of the chunk), waves 1 and 3 the q rows.
+      // Lane = 8-channel group g + SEGS * row part; each lane streams its rows, and the
+      // SEGS lanes of a row are adjacent, so the row's L2 norm is a DPP sum.
+      constexpr bool SPLIT = layer_v_in_scan(DK);
+      if (SPLIT || wave < 2) {
+        constexpr int RP = 64 / SEGS, ROWS = C / RP / (SPLIT ? 2 : 1);
+        const int which = SPLIT ? (wave & 1) : wave;  // 0: k, 1: q
+        const int g = l % SEGS, r0 = (SPLIT ? (wave >> 1) * (C / 2) : 0) + (l / SEGS) * ROWS;
+        bf16_t* dst = (which == 0 ? sK : sQ) + 8 * g;
         // row t0 of this key head (uniform) plus the lane's byte offset
-        bf16_t* gout = (bf16_t*)(wave == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK + (long long)hk * DK;
+        bf16_t* gout = (bf16_t*)(which == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK + (long long)hk * DK;
         const unsigned ostride = (unsigned)(p.Hk * DK);
-        conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (wave == 0 ? p.Hk * DK : 0) + hk * DK, 8 * g,
+        conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (which == 0 ? p.Hk * DK : 0) + hk * DK, 8 * g,
                         [&](int m, const u32x4& yw) {
           float y[8];
           unpack8<false>(&yw, y);
@@ -413,7 +303,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
           *(u32x4*)(dst + r * LDK) = hw;
           if (r < nvalid) *(u32x4*)at_bytes(gout, 2u * ((unsigned)r * ostride + 8u * g)) = hw;
         });
-      } else {
+      } else if constexpr (!layer_v_in_scan(DK)) {
         const int VG = gqa * p.DV / 8;  // 8-channel groups of v
         const int vch0 = 2 * p.Hk * DK + hk * gqa * p.DV;
         bf16_t* vout = (bf16_t*)p.vc + t0 * (long long)p.Hv * p.DV + (long long)hk * gqa * p.DV;
