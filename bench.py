@@ -455,7 +455,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=["prefill", "c1", "decode", "c3", "core", "bwd",
-                                           "layer_bwd", "layer_module", "copy"],
+                                           "layer_bwd", "layer_module", "copy", "ab_proj"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -487,6 +487,26 @@ def main():
         print(_line("device copy GB/s (counter calibration)", gbs, "GB/s", K, W_,
                     wall / K * 1e3, "f32", {"workload": "256 MiB read + 256 MiB written"}),
               flush=True)
+        return 0
+    if args.workload == "ab_proj":
+        # the gate projections a = in_proj_a(h), b = in_proj_b(h) at C1 (D=2048, Hv=32):
+        # the one-pass kernel against the two library GEMMs it replaces
+        from omegalax_amd import gdn_ab_projections
+        F = torch.nn.functional
+        g = torch.Generator(device="cuda").manual_seed(1001)
+        M, D, Hv = 4 * 4096, 2048, 32
+        h = torch.randn(M, D, generator=g, device="cuda").bfloat16()
+        wa, wb = ((0.02 * torch.randn(Hv, D, generator=g, device="cuda")).bfloat16()
+                  for _ in range(2))
+        wall, ms = time_launches(lambda: gdn_ab_projections(h, wa, wb), K, W_)
+        _, ms_lib = time_launches(lambda: (F.linear(h, wa), F.linear(h, wb)), K, W_)
+        gbs = (M * D + 2 * Hv * D + 2 * M * Hv) * 2 / (ms * 1e-3) / 1e9
+        print(_line("gate projections HBM GB/s (one pass over the hidden rows, config C1)", gbs,
+                    "GB/s", K, W_, wall / K * 1e3, "bf16",
+                    {"workload": f"in_proj_a + in_proj_b, M={M} D={D} Hv={Hv}"},
+                    kernel_ms=ms, two_library_gemms_ms=ms_lib,
+                    roofline={"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
+                              "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}), flush=True)
         return 0
     if args.workload == "layer_module":
         res = bench_layer_module(K, W_)

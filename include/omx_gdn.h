@@ -271,6 +271,21 @@ int omx_gdn_prefill_bwd(const void* mixed_qkv, const void* z, const void* a, con
 size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv,
                                           int64_t dk, int64_t dv, int64_t N);
 
+/*
+ * The layer's gate projections, b = in_proj_b(x) and a = in_proj_a(x)
+ * (deltanet.py:240-241, nnx.Linear with bf16 compute: fp32 accumulation, bf16
+ * output), formed in one pass over the hidden rows instead of two GEMMs that each
+ * read all of x.  No bias (use_bias=False, deltanet.py:182-187).
+ *
+ *   x        [M, D] bf16 (M token rows, rows contiguous), D a multiple of 8
+ *   w_a, w_b [Hv, D] bf16 (the nn.Linear / HF weight layout, [out, in])
+ *   a, b     [M, Hv] bf16
+ *
+ * 1 <= Hv <= 128.  x, w_a and w_b must be 16-byte aligned.
+ */
+int omx_gdn_ab_proj(const void* x, const void* w_a, const void* w_b, void* a, void* b,
+                    int64_t M, int64_t D, int64_t Hv, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

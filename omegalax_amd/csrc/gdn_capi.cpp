@@ -209,7 +209,7 @@ extern "C" {
 
 const char* omx_gdn_last_error(void) { return g_last_error.c_str(); }
 
-int omx_gdn_abi_version(void) { return 103; }
+int omx_gdn_abi_version(void) { return 104; }
 
 int omx_gdn_decode_step(const void* mixed_qkv, const void* z, const void* a, const void* b,
                         const float* conv_w, const float* A_log, const float* dt_bias,
@@ -264,6 +264,23 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
   p.scale = scale; p.eps = 0.f;
   return launch_status(
       omx::launch_decode(p, false, in_dtype == OMX_GDN_BF16, (hipStream_t)stream), fn);
+}
+
+int omx_gdn_ab_proj(const void* x, const void* w_a, const void* w_b, void* a, void* b,
+                    int64_t M, int64_t D, int64_t Hv, void* stream) {
+  const char* fn = "omx_gdn_ab_proj";
+  REQUIRE(M >= 0 && M <= (int64_t)1 << 40, "%s: row count %lld out of range", fn, (long long)M);
+  REQUIRE(D > 0 && D % 8 == 0 && D <= (1 << 20), "%s: D=%lld must be a positive multiple of 8",
+          fn, (long long)D);
+  REQUIRE(Hv >= 1 && Hv <= omx::ab_proj_max_heads(), "%s: Hv=%lld out of range [1, %d]", fn,
+          (long long)Hv, omx::ab_proj_max_heads());
+  if (M == 0) return ok();
+  REQUIRE(x && w_a && w_b && a && b, "%s: a required pointer is NULL", fn);
+  REQUIRE(aligned(x, 16) && aligned(w_a, 16) && aligned(w_b, 16),
+          "%s: x, w_a and w_b must be 16-byte aligned", fn);
+  return launch_status(omx::launch_ab_proj(x, w_a, w_b, a, b, (long long)M, (int)D, (int)Hv,
+                                           (hipStream_t)stream),
+                       fn);
 }
 
 }  // extern "C"

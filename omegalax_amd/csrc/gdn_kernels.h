@@ -226,4 +226,10 @@ bool decode_dims_supported(int dk, int dv);
 int decode_max_gqa();
 hipError_t launch_decode(const DecodeParams& p, bool layer, bool in_bf16, hipStream_t stream);
 
+// The gate projections a = x W_a^T, b = x W_b^T (bf16, fp32 accumulation) in one pass
+// over x [M, D] (gdn_proj.hip); D % 8 == 0, 1 <= Hv <= ab_proj_max_heads().
+int ab_proj_max_heads();
+hipError_t launch_ab_proj(const void* x, const void* wa, const void* wb, void* a, void* b,
+                          long long M, int D, int Hv, hipStream_t stream);
+
 }  // namespace omx

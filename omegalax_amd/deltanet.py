@@ -410,6 +410,60 @@ def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_hea
                             conv_state=conv_state, output_final_state=output_final_state, **cfg)
 
 
+def _ab_proj_fwd(x, w_a, w_b):
+    lead, D = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, D)
+    if x2.dtype != torch.bfloat16 or w_a.dtype != torch.bfloat16 or w_b.dtype != torch.bfloat16:
+        raise ValueError("gdn_ab_projections: x, w_a and w_b must be bf16")
+    Hv = w_a.shape[0]
+    if tuple(w_a.shape) != (Hv, D) or tuple(w_b.shape) != (Hv, D):
+        raise ValueError(f"w_a and w_b must both be [Hv, {D}] (got {tuple(w_a.shape)}, "
+                         f"{tuple(w_b.shape)})")
+    x2, w_a, w_b = x2.contiguous(), w_a.contiguous(), w_b.contiguous()
+    dev = _dev(x2, w_a, w_b)
+    M = x2.shape[0]
+    a = torch.empty((M, Hv), dtype=torch.bfloat16, device=dev)
+    b = torch.empty((M, Hv), dtype=torch.bfloat16, device=dev)
+    _lib.call("omx_gdn_ab_proj", _ptr(x2), _ptr(w_a), _ptr(w_b), _ptr(a), _ptr(b), M, D, Hv,
+              _stream(dev))
+    return a.reshape(*lead, Hv), b.reshape(*lead, Hv)
+
+
+class _ABProj(torch.autograd.Function):
+    """Autograd node of the gate projections: forward omx_gdn_ab_proj; backward the
+    linear maps' adjoints (dx = da W_a + db W_b, dW_a = da^T x, dW_b = db^T x) as bf16
+    library GEMMs, as the two nn.Linear nodes they replace would run them."""
+
+    @staticmethod
+    def forward(ctx, x, w_a, w_b):
+        ctx.save_for_backward(x, w_a, w_b)
+        return _ab_proj_fwd(x, w_a, w_b)
+
+    @staticmethod
+    def backward(ctx, da, db):
+        x, w_a, w_b = ctx.saved_tensors
+        D = x.shape[-1]
+        x2 = x.reshape(-1, D)
+        da = torch.zeros_like(x2[:, :w_a.shape[0]]) if da is None else da.reshape(x2.shape[0], -1)
+        db = torch.zeros_like(x2[:, :w_b.shape[0]]) if db is None else db.reshape(x2.shape[0], -1)
+        dx = (da @ w_a + db @ w_b).reshape(x.shape) if ctx.needs_input_grad[0] else None
+        dwa = da.t() @ x2 if ctx.needs_input_grad[1] else None
+        dwb = db.t() @ x2 if ctx.needs_input_grad[2] else None
+        return dx, dwa, dwb
+
+
+def gdn_ab_projections(x, w_a, w_b):
+    """(a, b) = (in_proj_a(x), in_proj_b(x)) of deltanet.py:240-241 in one pass over x.
+
+    x [..., D] bf16, w_a / w_b [Hv, D] bf16 (nn.Linear weights).  Returns a, b [..., Hv]
+    bf16, as the two bf16 linear maps give them (fp32 accumulation, rounded once).  When
+    gradients are enabled and an input requires them, the call is recorded for autograd.
+    """
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (x, w_a, w_b)):
+        return _ABProj.apply(x, w_a, w_b)
+    return _ab_proj_fwd(x, w_a, w_b)
+
+
 def gdn_decode_step(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, conv_state, state, *,
                     num_k_heads, head_k_dim, num_v_heads, head_v_dim, eps=1e-6):
     """One cached decode step; updates ``conv_state`` and ``state`` in place.

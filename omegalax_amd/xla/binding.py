@@ -20,7 +20,7 @@ from .. import _lib
 
 _XLA_LIB = os.path.join(os.path.dirname(_lib.LIB_PATH), "libomx_gdn_xla.so")
 _TARGETS = ("OmxGdnChunkFwd", "OmxGdnChunkBwd", "OmxGdnPrefill", "OmxGdnPrefillBwd",
-            "OmxGdnDecodeStep")
+            "OmxGdnDecodeStep", "OmxGdnAbProj")
 
 
 @functools.lru_cache(maxsize=None)
@@ -117,3 +117,14 @@ def gdn_decode_step(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, conv_sta
                 dt_bias.astype(jnp.float32), norm_w.astype(jnp.float32), conv_state, state,
                 num_k_heads=num_k_heads, head_k_dim=head_k_dim, num_v_heads=num_v_heads,
                 head_v_dim=head_v_dim, eps=float(eps))
+
+
+def gdn_ab_projections(x, w_a, w_b):
+    """(a, b) = (in_proj_a(x), in_proj_b(x)) of deltanet.py:240-241 in one pass over x:
+    x [..., D] bf16, w_a / w_b [Hv, D] bf16 (the [out, in] weight layout) -> [..., Hv] bf16.
+    Forward only; under jax.grad the reference's own nnx.Linear calls differentiate."""
+    register()
+    out = jax.ShapeDtypeStruct((*x.shape[:-1], w_a.shape[0]), jnp.bfloat16)
+    call = jax.ffi.ffi_call("OmxGdnAbProj", (out, out), vmap_method="sequential")
+    return call(x.astype(jnp.bfloat16), w_a.astype(jnp.bfloat16), w_b.astype(jnp.bfloat16))
+

@@ -148,6 +148,18 @@ ffi::Error DecodeStep(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuff
       num_k_heads, num_v_heads, head_k_dim, head_v_dim, wd[1], stream));
 }
 
+// The gate projections (deltanet.py:240-241): x [M, D] bf16, w_a / w_b [Hv, D] bf16 ->
+// a, b [M, Hv] bf16, one pass over x.
+ffi::Error AbProj(hipStream_t stream, ffi::AnyBuffer x, ffi::AnyBuffer w_a, ffi::AnyBuffer w_b,
+                  ffi::Result<ffi::AnyBuffer> a, ffi::Result<ffi::AnyBuffer> b) {
+  const auto xd = x.dimensions(), wd = w_a.dimensions();
+  if (xd.size() < 1 || wd.size() != 2) return ffi::Error::InvalidArgument("x [..., D], w [Hv, D]");
+  const int64_t D = xd[xd.size() - 1], Hv = wd[0];
+  const int64_t M = D ? (int64_t)x.element_count() / D : 0;
+  return status(omx_gdn_ab_proj(x.untyped_data(), w_a.untyped_data(), w_b.untyped_data(),
+                                a->untyped_data(), b->untyped_data(), M, D, Hv, stream));
+}
+
 }  // namespace
 
 XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnChunkFwd, ChunkFwd,
@@ -248,3 +260,12 @@ XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnDecodeStep, DecodeStep,
                                   .Attr<int64_t>("num_v_heads")
                                   .Attr<int64_t>("head_v_dim")
                                   .Attr<float>("eps"));
+
+XLA_FFI_DEFINE_HANDLER_SYMBOL(OmxGdnAbProj, AbProj,
+                              ffi::Ffi::Bind()
+                                  .Ctx<ffi::PlatformStream<hipStream_t>>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Arg<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>()
+                                  .Ret<ffi::AnyBuffer>());

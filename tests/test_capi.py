@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.lib().omx_gdn_abi_version() == 103
+    assert _lib.lib().omx_gdn_abi_version() == 104
 
 
 def _decode(**over):
@@ -272,3 +272,17 @@ def test_xla_ffi_handlers_build_only_with_jax():
     except ImportError:
         assert B.xla_include_dir() is None
         assert B.build_xla_ffi(verbose=False) is None
+
+
+def test_ab_proj_rejects_bad_shapes_on_the_host():
+    L = _lib.lib()
+    # D must be a positive multiple of 8; 1 <= Hv <= 128; M = 0 is an empty call
+    assert L.omx_gdn_ab_proj(16, 16, 16, 16, 16, 4, 20, 4, None) == _lib.EINVAL
+    assert "multiple of 8" in L.omx_gdn_last_error().decode()
+    assert L.omx_gdn_ab_proj(16, 16, 16, 16, 16, 4, 64, 0, None) == _lib.EINVAL
+    assert L.omx_gdn_ab_proj(16, 16, 16, 16, 16, 4, 64, 129, None) == _lib.EINVAL
+    assert L.omx_gdn_ab_proj(None, None, None, None, None, 0, 64, 32, None) == _lib.OK
+    assert L.omx_gdn_ab_proj(None, 16, 16, 16, 16, 4, 64, 32, None) == _lib.EINVAL
+    assert "NULL" in L.omx_gdn_last_error().decode()
+    assert L.omx_gdn_ab_proj(24, 16, 16, 16, 16, 4, 64, 32, None) == _lib.EINVAL
+    assert "aligned" in L.omx_gdn_last_error().decode()
