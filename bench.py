@@ -7,8 +7,9 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   prefill  (default, the headline) config C1: GDN layer prefill from the projection
            outputs (mixed_qkv, z, a, b) to the gated-norm output, B=4 T=4096 Hk=16 Hv=32
            d=128.  A "step" is one omx_gdn_prefill call over the whole batch.  The line
-           also carries C3, C4, the C2 decode step at B=64 and B=256, the backward passes
-           and the whole layer with its projections, each under its own key.
+           also carries C3, C4, the C2 decode step at B=64 and B=256, the backward passes,
+           the whole layer with its projections and the gate projections, each under its
+           own key.
   c1       the C1 leg of the headline alone (the layer step and the core call).
   decode   config C2: one cached decode step (conv cache + fp32 state in place) at
            --decode-batch, rotating through enough state sets that no step finds its state
@@ -22,6 +23,9 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   layer_module the whole GatedDeltaNet layer at C1 with D=2048 (projection GEMMs included):
            a forward, and a training step (forward + gradients of every parameter and the
            input); the line's value is the training step's tokens/s.
+  ab_proj  the gate projections in_proj_a, in_proj_b at C1 (D=2048, Hv=32) in one pass
+           over the hidden rows (omx_gdn_ab_proj), with the two library GEMMs it replaces
+           timed beside it.
   copy     a plain 256 MiB device copy, the calibration of the HBM traffic counters.
 
 Every "roofline" object divides the algorithmic work of one timed call by that call's
@@ -439,6 +443,26 @@ def cpu_prefill_baseline(T=4096, budget_s=20.0):
                       f"extrapolates to {4 * el / n:.1f} s at the same tokens/s"}
 
 
+def bench_ab_proj(steps, warmup):
+    """The gate projections a = in_proj_a(h), b = in_proj_b(h) at C1 (D=2048, Hv=32,
+    deltanet.py:240-241): the one-pass kernel against the two library GEMMs it replaces."""
+    import torch
+    from omegalax_amd import gdn_ab_projections
+    F = torch.nn.functional
+    g = torch.Generator(device="cuda").manual_seed(1001)
+    M, D, Hv = 4 * 4096, 2048, 32
+    h = torch.randn(M, D, generator=g, device="cuda").bfloat16()
+    wa, wb = ((0.02 * torch.randn(Hv, D, generator=g, device="cuda")).bfloat16()
+              for _ in range(2))
+    wall, ms = time_launches(lambda: gdn_ab_projections(h, wa, wb), steps, warmup)
+    _, ms_lib = time_launches(lambda: (F.linear(h, wa), F.linear(h, wb)), steps, warmup)
+    gbs = (M * D + 2 * Hv * D + 2 * M * Hv) * 2 / (ms * 1e-3) / 1e9
+    return {"config": f"in_proj_a + in_proj_b, M={M} D={D} Hv={Hv}",
+            "ms_per_step": wall / steps * 1e3, "kernel_ms": ms, "two_library_gemms_ms": ms_lib,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gbs / PEAK_HBM_GBS}}
+
+
 def _line(metric, value, unit, steps, warmup, ms, dtype, config, **extra):
     line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
             "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -489,24 +513,12 @@ def main():
               flush=True)
         return 0
     if args.workload == "ab_proj":
-        # the gate projections a = in_proj_a(h), b = in_proj_b(h) at C1 (D=2048, Hv=32):
-        # the one-pass kernel against the two library GEMMs it replaces
-        from omegalax_amd import gdn_ab_projections
-        F = torch.nn.functional
-        g = torch.Generator(device="cuda").manual_seed(1001)
-        M, D, Hv = 4 * 4096, 2048, 32
-        h = torch.randn(M, D, generator=g, device="cuda").bfloat16()
-        wa, wb = ((0.02 * torch.randn(Hv, D, generator=g, device="cuda")).bfloat16()
-                  for _ in range(2))
-        wall, ms = time_launches(lambda: gdn_ab_projections(h, wa, wb), K, W_)
-        _, ms_lib = time_launches(lambda: (F.linear(h, wa), F.linear(h, wb)), K, W_)
-        gbs = (M * D + 2 * Hv * D + 2 * M * Hv) * 2 / (ms * 1e-3) / 1e9
-        print(_line("gate projections HBM GB/s (one pass over the hidden rows, config C1)", gbs,
-                    "GB/s", K, W_, wall / K * 1e3, "bf16",
-                    {"workload": f"in_proj_a + in_proj_b, M={M} D={D} Hv={Hv}"},
-                    kernel_ms=ms, two_library_gemms_ms=ms_lib,
-                    roofline={"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                              "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS}), flush=True)
+        res = bench_ab_proj(K, W_)
+        print(_line("gate projections HBM GB/s (one pass over the hidden rows, config C1)",
+                    res["roofline"]["achieved"], "GB/s", K, W_, res["ms_per_step"], "bf16",
+                    {"workload": res["config"]}, kernel_ms=res["kernel_ms"],
+                    two_library_gemms_ms=res["two_library_gemms_ms"], roofline=res["roofline"]),
+              flush=True)
         return 0
     if args.workload == "layer_module":
         res = bench_layer_module(K, W_)
@@ -575,6 +587,7 @@ def main():
     bwd = bench_bwd(4, 4096, 16, 32, 128, max(K // 2, 5), W_)
     lbwd = bench_layer_bwd(max(K // 2, 5), W_)
     mod = bench_layer_module(K, W_)
+    abp = bench_ab_proj(max(K, 20), W_)
     dec = lambda r: {"config": f"C2 B={r['batch']} (state rotated over {r['state_sets']} sets)",
                      "roofline": r["roofline"], "kernel_ms": r["kernel_ms"],
                      "tokens_per_s": r["tokens_per_s"]}
@@ -593,6 +606,7 @@ def main():
         "layer_backward": {"config": "gdn_prefill_bwd at C1", "kernel_ms": lbwd["kernel_ms"],
                            "tokens_per_s": lbwd["tokens_per_s"]},
         "layer_module": mod,
+        "gate_projections": abp,
     }
     if cpu:
         extra["cpu_baseline"] = pre["cpu_baseline"]
