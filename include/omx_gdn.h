@@ -281,7 +281,8 @@ size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int6
  *   w_a, w_b [Hv, D] bf16 (the nn.Linear / HF weight layout, [out, in])
  *   a, b     [M, Hv] bf16
  *
- * 1 <= Hv <= 128.  x, w_a and w_b must be 16-byte aligned.
+ * 1 <= Hv <= 128.  x, w_a and w_b must be 16-byte aligned; a and b need only bf16
+ * (2-byte) alignment.
  */
 int omx_gdn_ab_proj(const void* x, const void* w_a, const void* w_b, void* a, void* b,
                     int64_t M, int64_t D, int64_t Hv, void* stream);

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
                                                           const bf16_t* __restrict__ wb,
                                                           bf16_t* __restrict__ a,
                                                           bf16_t* __restrict__ b, long long M,
-                                                          int D, int Hv) {
+                                                          int D, int Hv, bool vec_out) {
   using Q_ = ProjCfg<NT, KS>;
   constexpr int KC = Q_::KC, NW = Q_::NW, LDW = Q_::LDW, WV = Q_::WV, XV = Q_::XV;
   __shared__ __align__(16) unsigned char sW[KS][NW * LDW];
@@ -157,7 +157,8 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
   }
 
   // lane (q, r) holds token row row0 + r, output columns 16 t + 4q .. +3 of matrix m,
-  // rounded to bf16 as the reference's bf16 linear map rounds its output
+  // rounded to bf16 as the reference's bf16 linear map rounds its output; one 8-byte
+  // store when the host found Hv % 4 == 0 and both outputs 8-byte aligned
   const long long row = row0 + lr;
   if (row >= M) return;
 #pragma unroll
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int cc = 16 * t + 4 * lq;
-      if ((Hv & 3) == 0) {
+      if (vec_out) {
         if (cc < Hv)
           *(uint2*)(out + cc) = make_uint2(pack_bf16(acc[m][t][0], acc[m][t][1]),
                                            pack_bf16(acc[m][t][2], acc[m][t][3]));
@@ -185,9 +186,11 @@ hipError_t launch_nt(const void* x, const void* wa, const void* wb, void* a, voi
   constexpr int KS = proj_split<NT>();
   const long long blocks = (M + kProjRows - 1) / kProjRows;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  const bool vec_out = Hv % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 8 == 0 &&
+                       reinterpret_cast<uintptr_t>(b) % 8 == 0;
   hipLaunchKernelGGL((ab_proj_kernel<NT, KS>), dim3((unsigned)blocks), dim3(256 * KS), 0, stream,
                      (const bf16_t*)x, (const bf16_t*)wa, (const bf16_t*)wb, (bf16_t*)a,
-                     (bf16_t*)b, M, D, Hv);
+                     (bf16_t*)b, M, D, Hv, vec_out);
   return hipGetLastError();
 }
 

@@ -67,3 +67,24 @@ def test_ab_projections_keep_leading_dims_and_backward():
     (F.linear(rs[0], rs[1]) * da.float()).sum().add((F.linear(rs[0], rs[2]) * db.float()).sum()).backward()
     for t, r in zip(ts, rs):
         assert rel(np_(t.grad), np_(r.grad)) < 2e-2
+
+
+def test_ab_projections_outputs_at_two_byte_alignment():
+    """a and b need only bf16 alignment: outputs that start 2 bytes into a buffer (Hv % 4 == 0,
+    where aligned outputs take 8-byte stores) equal the aligned call bit for bit, and the
+    element before each output is left untouched."""
+    from omegalax_amd import _lib, gdn_ab_projections
+    from omegalax_amd.deltanet import _ptr, _stream
+    M, D, Hv = 130, 96, 8
+    print(f"ab projections misaligned outputs M={M} D={D} Hv={Hv}", flush=True)
+    sys.stdout.flush()
+    x, wa, wb = inputs(M, D, Hv, 11)
+    a_ref, b_ref = gdn_ab_projections(x, wa, wb)
+    bufs = [torch.full((M * Hv + 1,), 7.0, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    a, b = (t[1:].view(M, Hv) for t in bufs)
+    assert _ptr(a) % 8 == 2 and _ptr(b) % 8 == 2
+    _lib.call("omx_gdn_ab_proj", _ptr(x), _ptr(wa), _ptr(wb), _ptr(a), _ptr(b), M, D, Hv,
+              _stream(x.device))
+    torch.cuda.synchronize()
+    assert torch.equal(a, a_ref) and torch.equal(b, b_ref)
+    assert all(float(t[0]) == 7.0 for t in bufs)
