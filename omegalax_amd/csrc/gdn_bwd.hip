@@ -160,27 +160,41 @@ __device__ __forceinline__ void gfrag_row(const T* base, long long ld, int row, 
     for (int e = 0; e < 8; ++e) x[e] = 0.f;
   }
 }
-// global: column `col`, rows k0 + 8q + e (zero at rows >= nvalid)
+// global: column `col`, rows k0 + 8q + e of a row-major fp32 array (stride ld)
 __device__ __forceinline__ void gfrag_col(const float* base, long long ld, int col, int k0,
-                                          int nvalid, float* x) {
+                                          float* x) {
   const int q = lane_id() >> 4;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int m = k0 + 8 * q + e;
-    x[e] = m < nvalid ? base[(long long)m * ld + col] : 0.f;
-  }
+  for (int e = 0; e < 8; ++e) x[e] = base[(long long)(k0 + 8 * q + e) * ld + col];
+}
+
+// Loads whose rows may lie past a sequence's end go through a buffer resource whose range
+// ends at the last valid row: the hardware returns zeros beyond it.  So no load sits under
+// a branch, which would leave the count of outstanding memory operations unknown and turn
+// every later wait for one of them into a wait for all (the previous chunk's stores too).
+// Byte offsets are 32-bit.
+__device__ __forceinline__ float4 bload4(__amdgpu_buffer_rsrc_t r, unsigned off, const float*) {
+  const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return float4{__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]),
+                __uint_as_float(w[3])};
+}
+__device__ __forceinline__ u32x2 bload4(__amdgpu_buffer_rsrc_t r, unsigned off, const bf16_t*) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+// gfrag_col over a buffer resource of fp32 rows (zeros past its range)
+__device__ __forceinline__ void gfrag_col_b(__amdgpu_buffer_rsrc_t r, unsigned ld, unsigned col,
+                                            unsigned k0, float* x) {
+  const unsigned q = (unsigned)lane_id() >> 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    x[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, 4u * ((k0 + 8u * q + e) * ld + col), 0, 0));
 }
 
 // 4 elements in registers (4 bf16 in two words, or 4 floats)
 template <class T> struct Vec4;
 template <> struct Vec4<float> { typedef float4 type; };
 template <> struct Vec4<bf16_t> { typedef u32x2 type; };
-__device__ __forceinline__ float4 load4(const float* src, bool valid) {
-  return valid ? *(const float4*)src : float4{0.f, 0.f, 0.f, 0.f};
-}
-__device__ __forceinline__ u32x2 load4(const bf16_t* src, bool valid) {
-  return valid ? *(const u32x2*)src : u32x2{0u, 0u};
-}
+__device__ __forceinline__ float4 load4(const float* src) { return *(const float4*)src; }
 __device__ __forceinline__ void store4(float* dst, float4 x) { *(float4*)dst = x; }
 // a float at the precision T (bf16 rounded to nearest even)
 template <class T> __device__ __forceinline__ T from_f32(float x);
@@ -349,27 +363,33 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     const long long tt = s0 + (long long)jj * C;
     const int nv = (int)((s1 - tt) < C ? (s1 - tt) : C);
     const int sl = cbase + jj < p.n_rec ? cbase + jj : p.n_rec - 1;
+    // the chunk's valid rows only (zeros past them)
+    const auto kr = buf_rsrc((const KT*)p.ks + tt * p.ks_ld + (long long)hk * DK,
+                             (unsigned)(nv * p.ks_ld * (long long)sizeof(KT)));
+    const auto qr = buf_rsrc((const KT*)p.qs + tt * p.qs_ld + (long long)hk * DK,
+                             (unsigned)(nv * p.qs_ld * (long long)sizeof(KT)));
+    const auto dr = buf_rsrc(p.dO + tt * rs + (long long)h * DV + col0, (unsigned)(4 * nv * rs));
+    static_assert((C * DK / 4) % NT == 0, "a K / Q item's matrix follows from m alone");
 #pragma unroll
     for (int m = 0; m < NKQ; ++m) {
-      const int it = tid + m * NT;
-      const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
+      const int which = m * NT / (C * DK / 4);  // uniform: K items, then Q items
+      const int rem = tid + m * NT - which * (C * DK / 4);
       const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
-      const KT* src = (const KT*)(which ? p.qs : p.ks) + (tt + (row < nv ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
-                      (long long)hk * DK + c4;
-      pkq[m] = load4(src, row < nv);
+      const long long ld = which ? p.qs_ld : p.ks_ld;
+      pkq[m] = bload4(which ? qr : kr, (unsigned)((row * ld + c4) * (long long)sizeof(KT)), (const KT*)nullptr);
     }
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int row = it >> 4, c4 = 4 * (it & 15);
-      pdo[m] = load4(p.dO + (tt + (row < nv ? row : 0)) * rs + (long long)h * DV + col0 + c4, row < nv);
+      pdo[m] = bload4(dr, (unsigned)(4 * (row * rs + c4)), (const float*)nullptr);
     }
     const float* xb = p.xlpg + ((size_t)sl * p.Hv + h) * kXlpgFloats;
 #pragma unroll
     for (int m = 0; m < 2 * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
-      pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15), true);
+      pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15));
     }
     pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
   };
@@ -397,6 +417,9 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     sGate[tid] = pgate;
   };
   if (nchunks > 0) load_chunk(nchunks - 1);
+  // the prologue's loads (some under the uniform p.dht test) have landed: the loop's waits
+  // then count only the loop's own memory operations
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   for (int j = nchunks - 1; j >= 0; --j) {
     const long long t0 = s0 + (long long)j * C;
@@ -453,12 +476,16 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       }
     }
     {
-      float* dd = p.dvnew + t0 * rs + (long long)h * DV + col0 + c + lr;
+      // rows at or past nvalid lie outside the buffer range and are dropped: no branch
+      const auto vd = buf_rsrc(p.dvnew + t0 * rs + (long long)h * DV + col0,
+                               4u * (unsigned)nvalid * (unsigned)rs);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          if (16 * i + 4 * lq + v < nvalid) dd[(long long)(16 * i + 4 * lq + v) * rs] = dvn[i][v];
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(dvn[i][v]), vd,
+              4u * ((unsigned)(16 * i + 4 * lq + v) * (unsigned)rs + (unsigned)(c + lr)), 0, 0);
     }
     // ---------------------------------------------------------------- Y = diag(beta) X^T dV_new
     Op dvp[2];
@@ -622,15 +649,18 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   bf16_t* const sVh = sR + 6 * C * LDR;  // v: exact in bf16 unless the inputs are fp32
   bf16_t* const sVl = sR + 7 * C * LDR;
   const int srow = tid >> 3, sc4 = 4 * (tid & 7);  // this thread's staged item
-  const bool srv = srow < nvalid;
   float4 pf_do, pf_dv, pf_vn;
   typename Vec4<In>::type pf_v;
+  // the chunk's valid rows of dO, dV_new, V_new and v (zeros past them)
+  const unsigned rows_b = (unsigned)(nvalid * rs);  // elements
+  const auto rDO = buf_rsrc(dOb, 4u * rows_b), rDV = buf_rsrc(dVnb, 4u * rows_b);
+  const auto rVN = buf_rsrc(Vnb, 4u * rows_b), rV = buf_rsrc(vb, (unsigned)sizeof(In) * rows_b);
   auto load_rows = [&](int u) {
-    const long long off = (long long)(srv ? srow : 0) * rs + 32 * u + sc4;
-    pf_do = load4(dOb + off, srv);
-    pf_dv = load4(dVnb + off, srv);
-    pf_vn = load4(Vnb + off, srv);
-    pf_v = load4(vb + off, srv);
+    const unsigned off = (unsigned)(srow * rs + 32 * u + sc4);
+    pf_do = bload4(rDO, 4u * off, (const float*)nullptr);
+    pf_dv = bload4(rDV, 4u * off, (const float*)nullptr);
+    pf_vn = bload4(rVN, 4u * off, (const float*)nullptr);
+    pf_v = bload4(rV, (unsigned)sizeof(In) * off, (const In*)nullptr);
   };
   auto f4 = [](float4 x) { return f32x4{x.x, x.y, x.z, x.w}; };
   auto store_rows = [&]() {
@@ -648,8 +678,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     for (int kb = 0; kb < NKB; ++kb) {
       const int cb = wave + CW * kb;
       if (cb >= NCB) continue;
-      gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, DV, sfr[kb]);
-      gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, DV, dfr[kb]);
+      gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, sfr[kb]);
+      gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, dfr[kb]);
     }
   };
   float4 pf_x[C * 16 / CNT];  // X, staged after the last step
@@ -679,15 +709,21 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     constexpr int PER = C * DK / EPI;          // items per matrix
     constexpr int NIT = 2 * PER / CNT;
     static_assert(NIT * CNT == 2 * PER, "staging split");
+    // the chunk's valid rows only (zeros past them, no branch: see bload4)
+    static_assert(PER % CNT == 0, "an item's matrix follows from m alone");
+    const auto kr = buf_rsrc((const KT*)p.ks + t0 * p.ks_ld + (long long)hk * DK,
+                             (unsigned)(nvalid * p.ks_ld * (long long)sizeof(KT)));
+    const auto qr = buf_rsrc((const KT*)p.qs + t0 * p.qs_ld + (long long)hk * DK,
+                             (unsigned)(nvalid * p.qs_ld * (long long)sizeof(KT)));
     u32x4 st[NIT];
 #pragma unroll
     for (int m = 0; m < NIT; ++m) {
-      const int it = tid + m * CNT;
-      const int which = it / PER, rem = it % PER;
+      const int which = m * CNT / PER;  // uniform: K items, then Q items
+      const int rem = tid + m * CNT - which * PER;
       const int row = rem / (DK / EPI), c = EPI * (rem % (DK / EPI));
-      const KT* src = (const KT*)(which ? p.qs : p.ks) + (t0 + (row < nvalid ? row : 0)) * (which ? p.qs_ld : p.ks_ld) +
-                      (long long)hk * DK + c;
-      st[m] = row < nvalid ? *(const u32x4*)src : u32x4{0u, 0u, 0u, 0u};
+      const long long ld = which ? p.qs_ld : p.ks_ld;
+      st[m] = __builtin_amdgcn_raw_buffer_load_b128(which ? qr : kr,
+                                                    (unsigned)((row * ld + c) * (long long)sizeof(KT)), 0, 0);
     }
     load_rows(0);
     load_state(0);
@@ -733,7 +769,7 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
       for (int m = 0; m < C * 16 / CNT; ++m) {
         const int it = tid + m * CNT;
-        pf_x[m] = load4(xb + kXlpgX + (it >> 4) * C + 4 * (it & 15), true);
+        pf_x[m] = load4(xb + kXlpgX + (it >> 4) * C + 4 * (it & 15));
       }
     }
     lds_barrier();
@@ -837,16 +873,16 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
     Op bo[2];
     {
       float b[8];
-      gfrag_col(dVnb, rs, 16 * cv + lr, 0, nvalid, b);
+      gfrag_col_b(rDV, (unsigned)rs, 16 * cv + lr, 0, b);
       bo[0] = split8(b);
-      gfrag_col(dVnb, rs, 16 * cv + lr, 32, nvalid, b);
+      gfrag_col_b(rDV, (unsigned)rs, 16 * cv + lr, 32, b);
       bo[1] = split8(b);
     }
     typename Vec4<In>::type vv4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 16 * i + lr;
-      vv4[i] = load4(vb + (long long)(row < nvalid ? row : 0) * rs + 16 * cv + 4 * lq, row < nvalid);
+      vv4[i] = bload4(rV, (unsigned)sizeof(In) * (unsigned)(row * rs + 16 * cv + 4 * lq), (const In*)nullptr);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
