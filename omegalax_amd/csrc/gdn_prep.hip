@@ -176,12 +176,13 @@ constexpr int kGatePf = 4;  // value heads per key head whose gate inputs load w
 
 // Per-thread register load of the task's inputs: raw q/k rows (core modes)
 // and the gate inputs of value head w of the task's first kGatePf (wavefront w,
-// lane = token).
+// lane = token), with (layer) that head's A_log and dt_bias.
 template <int DK, int MODE>
 struct PrepIn {
   static constexpr int NRAW = MODE == MODE_LAYER ? 1 : PrepCfg<DK, MODE>::NI_KQ * PrepCfg<DK, MODE>::RAWW;
   u32x4 raw[NRAW];
   float ga, gb;
+  float alog, dtb;
 };
 static_assert(kGatePf == NT / 64, "one value head's gate inputs per wavefront");
 
@@ -218,6 +219,14 @@ __device__ __forceinline__ void load_task_inputs(const ChunkParams& p, const Pre
   const long long g0 = t.t0 * p.Hv + (long long)t.hk * gqa;  // token t0, first value head
   pf.ga = 0.f;
   pf.gb = 0.f;
+  pf.alog = 0.f;
+  pf.dtb = 0.f;
+  if constexpr (MODE == MODE_LAYER) {
+    if (gg < gqa) {
+      pf.alog = p.A_log[t.hk * gqa + gg];
+      pf.dtb = p.dt_bias[t.hk * gqa + gg];
+    }
+  }
   if (gg < gqa && l < t.nvalid) {
     const unsigned lo = (unsigned)l * (unsigned)p.Hv;  // lane = token
     if constexpr (MODE == MODE_LAYER) {
@@ -259,6 +268,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
   __shared__ __align__(16) u32x2 sTd[4 * 2 * 64];         // diagonal inverses as A fragments (hi, lo)
   __shared__ __align__(16) float sGw[4 * 2 * C];          // per wave: G log2(e), beta
   __shared__ __align__(16) float sGin[kGatePf * 2 * C];   // gate inputs of kGatePf value heads
+  __shared__ float sPar[kGatePf][2];                        // (layer) their A_log, dt_bias
   constexpr int K_LO = C * LDK;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -290,9 +300,14 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
         const int which = SPLIT ? (wave & 1) : wave;  // 0: k, 1: q
         const int g = l % SEGS, r0 = (SPLIT ? (wave >> 1) * (C / 2) : 0) + (l / SEGS) * ROWS;
         bf16_t* dst = (which == 0 ? sK : sQ) + 8 * g;
-        // row t0 of this key head (uniform) plus the lane's byte offset
-        bf16_t* gout = (bf16_t*)(which == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK + (long long)hk * DK;
+        // row t0 of this key head (uniform) plus the lane's byte offset; rows at or past
+        // nvalid lie outside the resource's range and are dropped, so no store sits under
+        // a branch (which would leave the count of outstanding memory operations unknown
+        // and make the next wait for a load wait for every store too)
         const unsigned ostride = (unsigned)(p.Hk * DK);
+        const auto gout = buf_rsrc((bf16_t*)(which == 0 ? p.kn : p.qn) + t0 * (long long)p.Hk * DK +
+                                       (long long)hk * DK,
+                                   2u * (unsigned)nvalid * ostride);
         conv_rows<ROWS>(p, n, s0, t0, nvalid, r0, (which == 0 ? p.Hk * DK : 0) + hk * DK, 8 * g,
                         [&](int m, const u32x4& yw) {
           float y[8];
@@ -301,19 +316,21 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
           const u32x4 hw = pack8(y);
           const int r = r0 + m;
           *(u32x4*)(dst + r * LDK) = hw;
-          if (r < nvalid) *(u32x4*)at_bytes(gout, 2u * ((unsigned)r * ostride + 8u * g)) = hw;
+          __builtin_amdgcn_raw_buffer_store_b128(hw, gout, 2u * ((unsigned)r * ostride + 8u * g), 0, 0);
         });
       } else if constexpr (!layer_v_in_scan(DK)) {
         const int VG = gqa * p.DV / 8;  // 8-channel groups of v
         const int vch0 = 2 * p.Hk * DK + hk * gqa * p.DV;
-        bf16_t* vout = (bf16_t*)p.vc + t0 * (long long)p.Hv * p.DV + (long long)hk * gqa * p.DV;
         const unsigned vstride = (unsigned)(p.Hv * p.DV);
+        // rows past nvalid are dropped by the range (no store under a branch)
+        const auto vout = buf_rsrc((bf16_t*)p.vc + t0 * (long long)p.Hv * p.DV + (long long)hk * gqa * p.DV,
+                                   2u * (unsigned)nvalid * vstride);
         for (int it = tid - 128; it < VG * 4; it += 128) {
           const int g = it % VG, r0 = (it / VG) * 16;
           if (r0 >= nvalid) continue;
           auto emit = [&](int m, const u32x4& y) {
             const int r = r0 + m;
-            if (r < nvalid) *(u32x4*)at_bytes(vout, 2u * ((unsigned)r * vstride + 8u * g)) = y;
+            __builtin_amdgcn_raw_buffer_store_b128(y, vout, 2u * ((unsigned)r * vstride + 8u * g), 0, 0);
           };
           conv_rows<16>(p, n, s0, t0, nvalid, r0, vch0, 8 * g, emit);
         }
@@ -377,6 +394,10 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
     if constexpr (MODE == MODE_LAYER) {
       sGin[wave * 2 * C + l] = pf.ga;
       sGin[wave * 2 * C + C + l] = pf.gb;
+      if (l == 0) {
+        sPar[wave][0] = pf.alog;
+        sPar[wave][1] = pf.dtb;
+      }
     }
     lds_barrier();
 
@@ -439,6 +460,12 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
           }
           sGin[wave * 2 * C + l] = ga;
           sGin[wave * 2 * C + C + l] = gb;
+          if constexpr (MODE == MODE_LAYER) {
+            if (l == 0 && gg + wave < gqa) {
+              sPar[wave][0] = p.A_log[h + wave];
+              sPar[wave][1] = p.dt_bias[h + wave];
+            }
+          }
         }
         lds_barrier();
       }
@@ -449,7 +476,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
         if constexpr (MODE == MODE_LAYER) {
           // deltanet.py:248-250: beta in bf16, g in fp32 (padded tokens: both 0)
           const float keep = (float)(l < nvalid);
-          g = -expf(p.A_log[h]) * softplusf_(g + p.dt_bias[h]) * keep;
+          g = -expf(sPar[slot][0]) * softplusf_(g + sPar[slot][1]) * keep;
           bt = round_bf(sigmoidf_(bt)) * keep;
         }
         const float G = wave_scan_dpp(g);
