@@ -297,24 +297,33 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
 #pragma unroll
   for (int d = 1; d < 4; ++d)
     if (tb - d >= cs0) load8(p.x + (tb - d) * p.conv_dim + c0, xs[d]);
+  // ends[d]: the end of token t - d's sequence (the rows a dx term may reach)
+  long long ends[4] = {cs1, cs1, cs1, cs1};
   const long long tend = te + 3 < p.tokens ? te + 3 : p.tokens;
-  // the next token's x and dy rows are loaded one iteration ahead
-  u32x4 nx = {0u, 0u, 0u, 0u}, ndy = {0u, 0u, 0u, 0u};
-  if (tb < tend) {
-    nx = *(const u32x4*)(p.x + tb * p.conv_dim + c0);
-    ndy = *(const u32x4*)(dys + tb * dy_ld + dy_c);
-  }
+  // The next token's x and dy rows are loaded one iteration ahead, unconditionally (the
+  // last iteration reloads its own row), and every iteration stores one dx row (see
+  // below): no memory operation sits under a per-thread branch, which would leave the
+  // count of outstanding operations unknown and make each wait for a load cover the
+  // stores as well.  The loads before the loop have landed.
+  u32x4 nx = *(const u32x4*)(p.x + tb * p.conv_dim + c0);
+  u32x4 ndy = *(const u32x4*)(dys + tb * dy_ld + dy_c);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   for (long long t = tb; t < tend; ++t) {
     const u32x4 cx = nx, cdy = ndy;
-    if (t + 1 < tend) {
-      nx = *(const u32x4*)(p.x + (t + 1) * p.conv_dim + c0);
-      ndy = *(const u32x4*)(dys + (t + 1) * dy_ld + dy_c);
+    {
+      const long long tn = t + 1 < tend ? t + 1 : t;
+      nx = *(const u32x4*)(p.x + tn * p.conv_dim + c0);
+      ndy = *(const u32x4*)(dys + tn * dy_ld + dy_c);
     }
     if (t >= cs1) {  // a new sequence starts at t: no history
       token_seq(p.cu_seqlens, p.N, p.T, t, cs0, cs1);
 #pragma unroll
       for (int d = 1; d < 4; ++d) zero8(xs[d]);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the lookup's loads end here
     }
+#pragma unroll
+    for (int d = 3; d > 0; --d) ends[d] = ends[d - 1];
+    ends[0] = cs1;
     unpack8<false>(&cx, xs[0]);
     float dy[8];
     unpack8<false>(&cdy, dy);
@@ -337,10 +346,12 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
     for (int e = 0; e < 8; ++e) dus[0][e] = du[e];
     // dx[s] for s = t - 3 needs du[s .. s + 3] = dus[3 .. 0]; terms past s's sequence end
     // are dropped (tokens s + d >= end(s) belong to the next sequence)
+    // (s < te always: t < te + 3.)  Rows s < tb (the first three iterations) store to
+    // row tb instead, which this thread writes again later (here or in the tail below),
+    // so the store need not sit under a branch.
     const long long s = t - 3;
-    if (s >= tb && s < te) {
-      long long ss0, ss1;
-      token_seq(p.cu_seqlens, p.N, p.T, s, ss0, ss1);
+    {
+      const long long ss1 = ends[3];  // end of s's sequence
       float dx[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -350,7 +361,8 @@ __global__ __launch_bounds__(NT) void conv_bwd_kernel(LayerBwdParams p) {
           if (s + d < ss1) acc += wt[e][d] * dus[3 - d][e];
         dx[e] = acc;
       }
-      *(u32x4*)(p.dx + s * p.conv_dim + c0) = pack8(dx);
+      const long long sw = s >= tb ? s : tb;
+      *(u32x4*)(p.dx + sw * p.conv_dim + c0) = pack8(dx);
     }
 #pragma unroll
     for (int d = 3; d > 0; --d)
