@@ -113,11 +113,13 @@ __global__ __launch_bounds__(NT) void conv_silu_split_kernel(LayerBwdParams p) {
     else zero8(xs[d]);
   }
   // every row of the block is loaded before the first store: one memory round trip per
-  // thread, and no load consumed after a store (the memory counter retires in order)
+  // thread.  The loads are unconditional (rows past te reload row te - 1 and are never
+  // used), so the compiler can count them and a wait for row m does not also wait for the
+  // stores issued before it (the memory counter retires in order).
   u32x4 raw[kConvFwdTB];
 #pragma unroll
   for (int m = 0; m < kConvFwdTB; ++m)
-    raw[m] = tb + m < te ? *(const u32x4*)(p.x + (tb + m) * p.conv_dim + c0) : u32x4{0u, 0u, 0u, 0u};
+    raw[m] = *(const u32x4*)(p.x + (tb + m < te ? tb + m : te - 1) * p.conv_dim + c0);
 #pragma unroll
   for (int m = 0; m < kConvFwdTB; ++m) {
     const long long t = tb + m;
@@ -126,6 +128,7 @@ __global__ __launch_bounds__(NT) void conv_silu_split_kernel(LayerBwdParams p) {
       token_seq(p.cu_seqlens, p.N, p.T, t, s0, s1);
 #pragma unroll
       for (int d = 1; d < 4; ++d) zero8(xs[d]);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the lookup's loads end here
     }
     unpack8<false>(&raw[m], xs[0]);
     float y[8];
