@@ -70,9 +70,15 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
   unsigned char* const sWp = sW[part];
 
   // chunk c's loads: the weight rows this thread stages (row n, 16-byte segment s) and
-  // the lane's token-row segments; elements past D (D % 8 == 0) and weight rows past Hv
-  // are zero
+  // the lane's token-row segments (D % 8 == 0).  Addresses are clamped and the values left
+  // untouched until the next step uses them: a select here would make the compiler wait
+  // for the loads right after issuing them, before the current chunk's products.  Weight
+  // rows past Hv reload row Hv - 1 (they only feed output columns that are not stored);
+  // elements past D reload element 0, finite, and meet zeros in x (xk below).
   u32x4 wreg[WV], xnext[XV];
+  auto xk = [&](int c, int j) {  // step j / 2 (64 elements), half j % 2: 64 (j/2) + 16 q + 8 (j%2)
+    return c * KC + 64 * (j >> 1) + 16 * lq + 8 * (j & 1);
+  };
   auto load = [&](int c) {
     const int k0 = c * KC;
 #pragma unroll
@@ -81,18 +87,13 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
       const int n = it / (KC / 8), s = it % (KC / 8);
       const int m = n / (16 * NT), h = n % (16 * NT);  // matrix, row within it
       const int k = k0 + 8 * s;
-      const bool ok = h < Hv && k < D;
-      const bf16_t* src = (m == 0 ? wa : wb) + (long long)(ok ? h : 0) * D + (ok ? k : 0);
-      const u32x4 v = *(const u32x4*)src;
-      wreg[i] = ok ? v : z4;
+      const bf16_t* src = (m == 0 ? wa : wb) + (long long)(h < Hv ? h : Hv - 1) * D + (k < D ? k : 0);
+      wreg[i] = *(const u32x4*)src;
     }
 #pragma unroll
     for (int j = 0; j < XV; ++j) {
-      // step j / 2 (64 elements), half j % 2: elements 64 (j / 2) + 16 q + 8 (j % 2) .. +7
-      const int k = k0 + 64 * (j >> 1) + 16 * lq + 8 * (j & 1);
-      const bool ok = k < D;
-      const u32x4 v = *(const u32x4*)(xrow + (ok ? k : 0));
-      xnext[j] = ok ? v : z4;
+      const int k = xk(c, j);
+      xnext[j] = *(const u32x4*)(xrow + (k < D ? k : 0));
     }
   };
 
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256 * KS) void ab_proj_kernel(const bf16_t* __restr
     const bool have = c < nch;
     u32x4 xcur[XV];
 #pragma unroll
-    for (int j = 0; j < XV; ++j) xcur[j] = xnext[j];
+    for (int j = 0; j < XV; ++j) xcur[j] = xk(c, j) < D ? xnext[j] : z4;  // zeros past D
     lds_barrier();  // the previous step's fragment reads are done
     if (have) {
 #pragma unroll
