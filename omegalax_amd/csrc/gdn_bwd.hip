@@ -676,8 +676,8 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   auto load_state = [&](int u) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      const int cb = wave + CW * kb;
-      if (cb >= NCB) continue;
+      // unconditional (a block past NCB reloads the last one, unused): see the dv loop
+      const int cb = wave + CW * kb < NCB ? wave + CW * kb : NCB - 1;
       gfrag_col(Sg, DK, 16 * cb + lr, 32 * u, sfr[kb]);
       gfrag_col(dSg, DK, 16 * cb + lr, 32 * u, dfr[kb]);
     }
@@ -762,10 +762,16 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
         for (int e = 0; e < 8; ++e) sds += sfr[kb][e] * dfr[kb][e];
       }
     }
-    if (u + 1 < DV / 32) {
-      load_rows(u + 1);
-      load_state(u + 1);
-    } else {
+    // The next step's loads, issued after this step's values are consumed (split and summed
+    // above) and unconditionally (the last step reloads its own slices, unused; X's rows,
+    // needed after the loop, load every step): loaded under a branch or hoisted above that
+    // use, they would need other registers than the ones the loop carries, and the copies at
+    // the end of the step would wait for them, turning the prefetch into a stall.
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      const int un = u + 1 < DV / 32 ? u + 1 : u;
+      load_rows(un);
+      load_state(un);
 #pragma unroll
       for (int m = 0; m < C * 16 / CNT; ++m) {
         const int it = tid + m * CNT;
