@@ -501,7 +501,7 @@ int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const voi
                  void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
                  int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
                  void* workspace, size_t workspace_bytes, void* stream, int64_t dk_real,
-                 int64_t dv_real) {
+                 int64_t dv_real, bool dry = false) {
   int rc = check_heads(fn, Hk, Hv, dk, dv);
   if (rc) return rc;
   REQUIRE(chunk_size == 64, "%s: chunk_size must be 64 (got %lld)", fn, (long long)chunk_size);
@@ -535,6 +535,9 @@ int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const voi
           "%s: mixed_qkv, z and out must be 16-byte aligned", fn);
   REQUIRE(aligned(norm_w, 16) && aligned(conv_w, 16), "%s: norm_w and conv_w must be 16-byte aligned",
           fn);
+  REQUIRE(N * Hv * (dv / omx::chunk_block_cols()) <= INT32_MAX, "%s: grid too large", fn);
+  REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
+  if (dry) return ok();  // every host check passed; nothing is enqueued
   omx::ChunkParams p{};
   p.mixed_qkv = mixed_qkv; p.z = z; p.a = a; p.b = b;
   p.conv_w = conv_w; p.A_log = A_log; p.dt_bias = dt_bias; p.norm_w = norm_w;
@@ -549,8 +552,6 @@ int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const voi
   p.qk_l2norm = 1;
   p.o_part = (char*)workspace + ws.opart;
   p.o_ss = (float*)((char*)workspace + ws.oss);
-  REQUIRE((int64_t)p.N * p.Hv * p.nb <= INT32_MAX, "%s: grid too large", fn);
-  REQUIRE(((B * T + 63) / 64 + N) * Hk <= INT32_MAX, "%s: grid too large", fn);
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
   if (e == hipSuccess)
     e = omx::launch_norm_epilogue(p.o_part, p.o_ss, omx::layer_ss_slots(p), z, norm_w, out,
@@ -593,21 +594,28 @@ size_t prefill_ws_bytes(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk
   return chunk_ws(B, T, Hk, Hv, dk, dv, N, omx::kModeLayer).total;
 }
 
+// Stand-in workspace address for a validate-only pass (`dry`): it is aligned and never
+// dereferenced or handed to HIP, because a dry pass returns before enqueueing anything.
+alignas(256) unsigned char g_dry_workspace[256];
+
 // The layer prefill behind omx_gdn_prefill and omx_gdn_prefill_noalloc (`fn` names the
 // entry point in error messages): at compiled head dims directly, else on zero-padded
-// copies.
+// copies.  With `dry` it runs every host check and returns before the first HIP call
+// (the workspace pointer is then not looked at).
 int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const void* a,
                   const void* b, const float* conv_w, const float* A_log, const float* dt_bias,
                   const float* norm_w, float eps, const int32_t* cu_seqlens, int64_t N,
                   const float* initial_state, float* final_state, const void* conv_state_in,
                   void* conv_state_out, void* out, int64_t B, int64_t T, int64_t Hk,
                   int64_t Hv, int64_t dk, int64_t dv, int64_t K, int64_t chunk_size,
-                  void* workspace, size_t workspace_bytes, void* stream) {
+                  void* workspace, size_t workspace_bytes, void* stream, bool dry = false) {
+  if (dry) workspace = g_dry_workspace;
   const HeadDims hd = head_dims(kLayerFwd, dk, dv, false);
   if (!hd.pad)
     return prefill_core(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps, cu_seqlens,
                         N, initial_state, final_state, conv_state_in, conv_state_out, out, B, T,
-                        Hk, Hv, dk, dv, K, chunk_size, workspace, workspace_bytes, stream, dk, dv);
+                        Hk, Hv, dk, dv, K, chunk_size, workspace, workspace_bytes, stream, dk, dv,
+                        dry);
   int rc = chunk_shape_check(fn, Hk, Hv, dk, dv, chunk_size, B, T, cu_seqlens, N);
   if (rc) return rc;
   REQUIRE(K >= 2 && K <= 4, "%s: conv kernel size %lld not in [2, 4]", fn, (long long)K);
@@ -621,6 +629,12 @@ int prefill_entry(const char* fn, const void* mixed_qkv, const void* z, const vo
   REQUIRE(workspace && aligned(workspace, 16), "%s: workspace must be non-NULL and 16-byte aligned",
           fn);
   char* base = (char*)workspace;
+  // the inner call's checks (eps, conv size, grid limits) run before the first copy
+  rc = prefill_core(fn, base + w.x, base + w.z, a, b, (const float*)(base + w.cw), A_log, dt_bias,
+                    (const float*)(base + w.nw), eps, cu_seqlens, N, nullptr, nullptr, nullptr,
+                    nullptr, base + w.out, B, T, Hk, Hv, dk2, dv2, K, chunk_size, base + w.inner,
+                    workspace_bytes - w.inner, stream, dk, dv, true);
+  if (rc || dry) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e = hipSuccess;
   if (tok > 0) {
@@ -718,8 +732,13 @@ int omx_gdn_prefill_noalloc(const void* mixed_qkv, const void* z, const void* a,
           "%s: these shapes need %zu bytes of scratch, above the fixed %zu (call omx_gdn_prefill "
           "with a workspace instead)",
           fn, need, kNoAllocScratchBytes);
+  // every argument check before the first HIP call (the device query below included)
+  int rc = prefill_entry(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps, cu_seqlens,
+                         N, initial_state, final_state, conv_state_in, conv_state_out, out, B, T,
+                         Hk, Hv, dk, dv, K, chunk_size, nullptr, kNoAllocScratchBytes, stream, true);
+  if (rc) return rc;
   void* ws = nullptr;
-  const int rc = scratch_for_current_device(fn, &ws);
+  rc = scratch_for_current_device(fn, &ws);
   if (rc) return rc;
   return prefill_entry(fn, mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, eps, cu_seqlens,
                        N, initial_state, final_state, conv_state_in, conv_state_out, out, B, T,

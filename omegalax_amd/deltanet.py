@@ -410,6 +410,15 @@ def gdn_prefill(mixed_qkv, z, a, b, conv_w, A_log, dt_bias, norm_w, *, num_k_hea
                             conv_state=conv_state, output_final_state=output_final_state, **cfg)
 
 
+# omx_gdn_ab_proj's limits (include/omx_gdn.h): D a multiple of 8, 1 <= Hv <= 128
+AB_PROJ_MAX_HEADS = 128
+
+
+def ab_proj_supported(D: int, Hv: int) -> bool:
+    """Whether omx_gdn_ab_proj takes a hidden size D and Hv gate heads."""
+    return D % 8 == 0 and 1 <= Hv <= AB_PROJ_MAX_HEADS
+
+
 def _ab_proj_fwd(x, w_a, w_b):
     lead, D = x.shape[:-1], x.shape[-1]
     x2 = x.reshape(-1, D)
@@ -419,7 +428,13 @@ def _ab_proj_fwd(x, w_a, w_b):
     if tuple(w_a.shape) != (Hv, D) or tuple(w_b.shape) != (Hv, D):
         raise ValueError(f"w_a and w_b must both be [Hv, {D}] (got {tuple(w_a.shape)}, "
                          f"{tuple(w_b.shape)})")
-    x2, w_a, w_b = x2.contiguous(), w_a.contiguous(), w_b.contiguous()
+    if D % 8 != 0 or not 1 <= Hv <= AB_PROJ_MAX_HEADS:
+        raise ValueError(f"gdn_ab_projections: the kernel takes D a multiple of 8 and 1 <= Hv <= "
+                         f"{AB_PROJ_MAX_HEADS} (got D={D}, Hv={Hv})")
+    # the kernel reads 16-byte pieces: a view whose storage offset breaks that alignment is
+    # copied to a fresh (aligned) tensor
+    x2, w_a, w_b = (t.contiguous() for t in (x2, w_a, w_b))
+    x2, w_a, w_b = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (x2, w_a, w_b))
     dev = _dev(x2, w_a, w_b)
     M = x2.shape[0]
     a = torch.empty((M, Hv), dtype=torch.bfloat16, device=dev)

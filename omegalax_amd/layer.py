@@ -21,7 +21,7 @@ from typing import Mapping
 import torch
 import torch.nn.functional as F
 
-from .deltanet import gdn_ab_projections, gdn_decode_step, gdn_prefill
+from .deltanet import ab_proj_supported, gdn_ab_projections, gdn_decode_step, gdn_prefill
 from .segments import lengths_to_cu_seqlens, segment_ids_to_cu_seqlens
 
 _PREFIX = "model.language_model.layers."
@@ -108,8 +108,12 @@ def _projections(params: GDNParams, cfg: GDNConfig, h):
     lead = h.shape[:-1]
     mixed = F.linear(h, params.in_proj_qkv)
     z = F.linear(h, params.in_proj_z).reshape(*lead, cfg.num_v_heads, cfg.head_v_dim)
-    # the two gate projections in one pass over h (deltanet.py:240-241)
-    a, b = gdn_ab_projections(h, params.in_proj_a, params.in_proj_b)
+    # the two gate projections in one pass over h (deltanet.py:240-241); shapes outside the
+    # one-pass kernel's limits take the two library GEMMs, as the other projections do
+    if ab_proj_supported(h.shape[-1], params.in_proj_a.shape[0]):
+        a, b = gdn_ab_projections(h, params.in_proj_a, params.in_proj_b)
+    else:
+        a, b = F.linear(h, params.in_proj_a), F.linear(h, params.in_proj_b)
     return mixed, z, a, b
 
 

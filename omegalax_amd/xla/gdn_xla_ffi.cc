@@ -3,9 +3,12 @@
 //
 // Built by omegalax_amd.build only when jaxlib's FFI headers are importable
 // (jax.ffi.include_dir()); it is not part of libomx_gdn.so and nothing in this
-// repository's torch path loads it.  Each handler validates nothing itself: the C ABI
-// checks shapes, pointers and attributes on the host and its error codes map to FFI
-// errors (EINVAL -> InvalidArgument, EUNSUPPORTED -> Unimplemented, else Internal).
+// repository's torch path loads it.  JAX is absent from the image this was written in, so
+// this file has never been compiled or run there: the handlers are untested source.
+// Each handler checks only ranks and element types (the C ABI takes raw pointers and
+// cannot see them); the C ABI checks shapes, pointers and attributes on the host and its
+// error codes map to FFI errors (EINVAL -> InvalidArgument, EUNSUPPORTED ->
+// Unimplemented, else Internal).
 // Work is enqueued on XLA's stream; no handler synchronises or keeps state, so XLA may
 // run them concurrently and re-run them under remat (model.py:202).
 //
@@ -14,6 +17,7 @@
 // shapes; the layer-level handlers cover deltanet.py:243-293 and a decode step.
 #include <cmath>
 #include <cstdint>
+#include <initializer_list>
 
 #include <hip/hip_runtime.h>
 
@@ -32,8 +36,26 @@ ffi::Error status(int rc) {
   return ffi::Error::Internal(omx_gdn_last_error());
 }
 
-int dtype_code(const ffi::AnyBuffer& x) {
-  return x.element_type() == ffi::DataType::BF16 ? OMX_GDN_BF16 : OMX_GDN_F32;
+// The C ABI reads q/k/v-style inputs as bf16 or fp32 only: any other element type (f16,
+// f64, ...) is rejected here, as are operands whose type differs from the first one's,
+// because the kernels would read them with the first operand's element size.
+ffi::Error qkv_dtype(int* code, std::initializer_list<const ffi::AnyBuffer*> xs) {
+  const ffi::DataType t = (*xs.begin())->element_type();
+  if (t != ffi::DataType::BF16 && t != ffi::DataType::F32)
+    return ffi::Error::InvalidArgument("q, k, v must be bf16 or f32");
+  for (const ffi::AnyBuffer* x : xs)
+    if (x->element_type() != t)
+      return ffi::Error::InvalidArgument("q, k, v (and their gradients) must share one dtype");
+  *code = t == ffi::DataType::BF16 ? OMX_GDN_BF16 : OMX_GDN_F32;
+  return ffi::Error::Success();
+}
+
+// The layer entry points take bf16 activations (and conv caches) only.
+ffi::Error all_bf16(std::initializer_list<const ffi::AnyBuffer*> xs) {
+  for (const ffi::AnyBuffer* x : xs)
+    if (x->element_type() != ffi::DataType::BF16)
+      return ffi::Error::InvalidArgument("the layer's activations and conv caches must be bf16");
+  return ffi::Error::Success();
 }
 
 // chunk_gated_delta_rule(q, k, v, g, beta, chunk_size) -> o (deltanet.py:53-153), with an
@@ -47,10 +69,12 @@ ffi::Error ChunkFwd(hipStream_t stream, ffi::AnyBuffer q, ffi::AnyBuffer k, ffi:
   if (qd.size() != 4 || vd.size() != 4)
     return ffi::Error::InvalidArgument("q and v must be rank 4");
   const int64_t B = qd[0], T = qd[1], Hk = qd[2], dk = qd[3], Hv = vd[2], dv = vd[3];
+  int code = 0;
+  if (ffi::Error e = qkv_dtype(&code, {&q, &k, &v}); e.failure()) return e;
   const float* s0 = initial_state.element_count() ? initial_state.typed_data() : nullptr;
   float* s1 = final_state->element_count() ? final_state->typed_data() : nullptr;
   return status(omx_gdn_chunk_fwd(q.untyped_data(), k.untyped_data(), v.untyped_data(),
-                                  dtype_code(q), g.typed_data(), beta.typed_data(), s0, nullptr,
+                                  code, g.typed_data(), beta.typed_data(), s0, nullptr,
                                   B, o->typed_data(), s1, B, T, Hk, Hv, dk, dv, chunk_size,
                                   1.0f / std::sqrt((float)dk), 1, workspace->untyped_data(),
                                   workspace->size_bytes(), stream));
@@ -67,8 +91,10 @@ ffi::Error ChunkBwd(hipStream_t stream, ffi::AnyBuffer q, ffi::AnyBuffer k, ffi:
   if (qd.size() != 4 || vd.size() != 4)
     return ffi::Error::InvalidArgument("q and v must be rank 4");
   const int64_t B = qd[0], T = qd[1], Hk = qd[2], dkd = qd[3], Hv = vd[2], dvd = vd[3];
+  int code = 0;
+  if (ffi::Error e = qkv_dtype(&code, {&q, &k, &v, &(*dq), &(*dk), &(*dv)}); e.failure()) return e;
   return status(omx_gdn_chunk_bwd(
-      q.untyped_data(), k.untyped_data(), v.untyped_data(), dtype_code(q), g.typed_data(),
+      q.untyped_data(), k.untyped_data(), v.untyped_data(), code, g.typed_data(),
       beta.typed_data(), nullptr, nullptr, B, d_o.typed_data(), nullptr, dq->untyped_data(),
       dk->untyped_data(), dv->untyped_data(), dg->typed_data(), dbeta->typed_data(), nullptr, B,
       T, Hk, Hv, dkd, dvd, chunk_size, 1.0f / std::sqrt((float)dkd), 1,
@@ -85,6 +111,7 @@ ffi::Error Prefill(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuffer 
   const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();  // [B, T, C], [C, K]
   if (xd.size() != 3 || wd.size() != 2)
     return ffi::Error::InvalidArgument("mixed_qkv must be [B, T, C] and conv_w [C, K]");
+  if (ffi::Error e = all_bf16({&mixed_qkv, &z, &a, &b, &(*out)}); e.failure()) return e;
   return status(omx_gdn_prefill(
       mixed_qkv.untyped_data(), z.untyped_data(), a.untyped_data(), b.untyped_data(),
       conv_w.typed_data(), A_log.typed_data(), dt_bias.typed_data(), norm_w.typed_data(), eps,
@@ -109,6 +136,9 @@ ffi::Error PrefillBwd(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuff
   const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();
   if (xd.size() != 3 || wd.size() != 2)
     return ffi::Error::InvalidArgument("mixed_qkv must be [B, T, C] and conv_w [C, K]");
+  if (ffi::Error e = all_bf16({&mixed_qkv, &z, &a, &b, &d_out, &(*dx), &(*dz), &(*da), &(*db)});
+      e.failure())
+    return e;
   return status(omx_gdn_prefill_bwd(
       mixed_qkv.untyped_data(), z.untyped_data(), a.untyped_data(), b.untyped_data(),
       conv_w.typed_data(), A_log.typed_data(), dt_bias.typed_data(), norm_w.typed_data(), eps,
@@ -133,6 +163,9 @@ ffi::Error DecodeStep(hipStream_t stream, ffi::AnyBuffer mixed_qkv, ffi::AnyBuff
   const auto xd = mixed_qkv.dimensions(), wd = conv_w.dimensions();  // [B, C], [C, K]
   if (xd.size() != 2 || wd.size() != 2)
     return ffi::Error::InvalidArgument("mixed_qkv must be [B, C] and conv_w [C, K]");
+  if (ffi::Error e = all_bf16({&mixed_qkv, &z, &a, &b, &conv_state, &(*out), &(*conv_state_out)});
+      e.failure())
+    return e;
   if (conv_state_out->untyped_data() != conv_state.untyped_data() &&
       hipMemcpyAsync(conv_state_out->untyped_data(), conv_state.untyped_data(),
                      conv_state.size_bytes(), hipMemcpyDeviceToDevice, stream) != hipSuccess)
@@ -154,6 +187,7 @@ ffi::Error AbProj(hipStream_t stream, ffi::AnyBuffer x, ffi::AnyBuffer w_a, ffi:
                   ffi::Result<ffi::AnyBuffer> a, ffi::Result<ffi::AnyBuffer> b) {
   const auto xd = x.dimensions(), wd = w_a.dimensions();
   if (xd.size() < 1 || wd.size() != 2) return ffi::Error::InvalidArgument("x [..., D], w [Hv, D]");
+  if (ffi::Error e = all_bf16({&x, &w_a, &w_b, &(*a), &(*b)}); e.failure()) return e;
   const int64_t D = xd[xd.size() - 1], Hv = wd[0];
   const int64_t M = D ? (int64_t)x.element_count() / D : 0;
   return status(omx_gdn_ab_proj(x.untyped_data(), w_a.untyped_data(), w_b.untyped_data(),

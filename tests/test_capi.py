@@ -258,6 +258,31 @@ def test_prefill_noalloc_rejects_shapes_beyond_its_fixed_scratch():
     assert "scratch" in L.omx_gdn_last_error().decode()
 
 
+@pytest.mark.parametrize("dk,dv", [(128, 128), (16, 32)])  # compiled dims, padded copies
+@pytest.mark.parametrize("over,msg", [
+    (dict(chunk_size=32), "chunk_size must be 64"),
+    (dict(out=None), "NULL"),
+    (dict(conv_w=None), "NULL"),
+    (dict(K=5), "conv kernel size"),
+    (dict(eps=2.0), "eps"),
+    (dict(N=2), "N must equal B"),
+])
+def test_prefill_noalloc_checks_arguments_before_any_hip_call(dk, dv, over, msg):
+    """Bad arguments give EINVAL from the host checks alone: on this GPU-less host any HIP
+    call (the device query that finds the scratch array included) would fail with
+    ELAUNCH instead, so the code proves that nothing ran before the checks."""
+    L = _lib.lib()
+    args = dict(mixed_qkv=16, z=16, a=16, b=16, conv_w=16, A_log=16, dt_bias=16, norm_w=16,
+                eps=1e-6, cu_seqlens=None, N=1, initial_state=None, final_state=None,
+                conv_state_in=None, conv_state_out=None, out=16, B=1, T=64, Hk=2, Hv=4, dk=dk,
+                dv=dv, K=4, chunk_size=64, stream=None)
+    args.update(over)
+    rc = L.omx_gdn_prefill_noalloc(*args.values())
+    err = L.omx_gdn_last_error().decode()
+    assert rc == _lib.EINVAL, (rc, err)
+    assert msg in err, err
+
+
 def test_xla_ffi_handlers_build_only_with_jax():
     """The XLA FFI handler source is built only where jaxlib's FFI headers exist; here (no
     JAX) the build skips it cleanly and the torch path does not need it."""

@@ -88,3 +88,46 @@ def test_ab_projections_outputs_at_two_byte_alignment():
     torch.cuda.synchronize()
     assert torch.equal(a, a_ref) and torch.equal(b, b_ref)
     assert all(float(t[0]) == 7.0 for t in bufs)
+
+
+def test_ab_projections_take_a_misaligned_hidden_view():
+    """A bf16 hidden view whose storage offset is not a multiple of 8 elements (not 16-byte
+    aligned) is copied to an aligned tensor first: the result equals the aligned call bit
+    for bit, as does the layer's projection step that calls it."""
+    from omegalax_amd import gdn_ab_projections
+    from omegalax_amd.deltanet import _ptr
+    M, D, Hv = 64, 2048, 32
+    print(f"ab projections misaligned input view M={M} D={D} Hv={Hv}", flush=True)
+    sys.stdout.flush()
+    x, wa, wb = inputs(M, D, Hv, 13)
+    buf = torch.empty(M * D + 1, dtype=torch.bfloat16, device="cuda")
+    xv = buf[1:1 + M * D].view(M, D)
+    xv.copy_(x)
+    assert _ptr(xv) % 16 != 0
+    a, b = gdn_ab_projections(xv, wa, wb)
+    a_ref, b_ref = gdn_ab_projections(x, wa, wb)
+    torch.cuda.synchronize()
+    assert torch.equal(a, a_ref) and torch.equal(b, b_ref)
+
+
+def test_layer_projections_outside_the_kernel_limits_use_library_gemms():
+    """Hv above the one-pass kernel's 128 heads (or D not a multiple of 8) goes to F.linear
+    in the layer module, bit for bit what the two library GEMMs give."""
+    from omegalax_amd.layer import GDNConfig, GDNParams, _projections
+    from omegalax_amd.deltanet import ab_proj_supported
+    F = torch.nn.functional
+    for D, Hv in ((2048, 160), (100, 4)):
+        print(f"layer projections fallback D={D} Hv={Hv}", flush=True)
+        assert not ab_proj_supported(D, Hv)
+        x, wa, wb = inputs(48, D, Hv, D + Hv)
+        cfg = GDNConfig(hidden_size=D, num_k_heads=1, head_k_dim=16, num_v_heads=Hv,
+                        head_v_dim=16)
+        bf = lambda *shape: (0.02 * torch.randn(*shape)).bfloat16().cuda()
+        f32 = lambda *shape: torch.zeros(*shape, device="cuda")
+        params = GDNParams(in_proj_qkv=bf(cfg.conv_dim, D), in_proj_z=bf(Hv * 16, D),
+                           in_proj_b=wb, in_proj_a=wa, conv_w=f32(cfg.conv_dim, 4),
+                           dt_bias=f32(Hv), A_log=f32(Hv), norm_w=f32(16),
+                           out_proj=bf(D, Hv * 16))
+        _, _, a, b = _projections(params, cfg, x)
+        torch.cuda.synchronize()
+        assert torch.equal(a, F.linear(x, wa)) and torch.equal(b, F.linear(x, wb))

@@ -93,3 +93,16 @@ def test_hf_mapping_reports_missing_keys():
     from omegalax_amd.layer import gdn_params_from_hf
     with pytest.raises(KeyError, match="conv1d"):
         gdn_params_from_hf({}, 0)
+
+
+def test_ab_projection_limits_are_checked_up_front():
+    """The one-pass gate projection kernel takes D a multiple of 8 and 1 <= Hv <= 128; the
+    Python wrapper names the limit before any device work (CPU tensors suffice here)."""
+    import torch
+    from omegalax_amd.deltanet import _ab_proj_fwd, ab_proj_supported
+    assert ab_proj_supported(2048, 32) and ab_proj_supported(8, 128)
+    assert not ab_proj_supported(2044, 32) and not ab_proj_supported(2048, 129)
+    x = torch.zeros(4, 20, dtype=torch.bfloat16)
+    w = torch.zeros(4, 20, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        _ab_proj_fwd(x, w, w)

@@ -97,3 +97,41 @@ def test_noalloc_prefill_rejects_shapes_beyond_the_fixed_scratch():
     rc = L.omx_gdn_prefill_noalloc(*args)
     assert rc == _lib.EINVAL
     assert "scratch" in L.omx_gdn_last_error().decode()
+
+
+def test_noalloc_prefill_replays_under_hip_graph_capture():
+    """The entry point records into a HIP graph (torch.cuda.CUDAGraph): one eager call looks
+    the scratch address up, then a call is captured and the graph replayed three times on
+    fresh inputs copied into the captured buffers, with eager work and synchronisations in
+    between; every replay equals omx_gdn_prefill on the same inputs bit for bit.  The path
+    issues no memset, copy or allocation, only kernel launches."""
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    B, T, N = 1, 300, 2
+    Hk, dk, Hv, dv = dims["Hk"], dims["dk"], dims["Hv"], dims["dv"]
+    say(f"noalloc prefill graph capture: B={B} T={T} packed [120, 180], Hk=2 Hv=4 d=128")
+    t, cu, S0, conv0 = case(B, T, dims, 31, packed=[120, 180])
+    run("omx_gdn_prefill_noalloc", t, dims, cu, S0, conv0)  # eager: address lookup
+    Cd = t["mixed_qkv"].shape[-1]
+    out = torch.empty((B, T, Hv * dv), dtype=torch.bfloat16, device="cuda")
+    fs = torch.empty((N, Hv, dk, dv), dtype=torch.float32, device="cuda")
+    cs = torch.empty((N, Cd, 3), dtype=torch.bfloat16, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        stream = torch.cuda.current_stream().cuda_stream
+        _lib.call("omx_gdn_prefill_noalloc", _ptr(t["mixed_qkv"]), _ptr(t["z"]), _ptr(t["a"]),
+                  _ptr(t["b"]), _ptr(t["conv_w"]), _ptr(t["A_log"]), _ptr(t["dt_bias"]),
+                  _ptr(t["norm_w"]), 1e-6, _ptr(cu), N, _ptr(S0), _ptr(fs), _ptr(conv0), _ptr(cs),
+                  _ptr(out), B, T, Hk, Hv, dk, dv, 4, 64, stream)
+    for rep in range(3):
+        say(f"  replay {rep}")
+        t2, _, S2, c2 = case(B, T, dims, 40 + rep, packed=[120, 180])
+        for k in ("mixed_qkv", "z", "a", "b"):
+            t[k].copy_(t2[k])
+        S0.copy_(S2)
+        conv0.copy_(c2)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = run("omx_gdn_prefill", t, dims, cu, S0, conv0)
+        for a, b in zip((out, fs, cs), want):
+            assert torch.equal(a, b)
