@@ -65,11 +65,13 @@ def test_decode_steps_match_oracle(B, Hk, Hv, dk, dv):
         assert np.array_equal(np_(t["conv_state"]), conv_ref), f"step {step} conv cache"
 
 
-def test_decode_c2_full_size_b64():
-    """Config C2 at B=64: S [64,32,128,128] fp32 against the fp64 oracle."""
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_decode_c2_full_size(B):
+    """Config C2 (Hk=16, Hv=32, d=128) at B = 1, 8 (the sweep's small batches) and 64:
+    S [B,32,128,128] fp32 against the fp64 oracle, every sequence."""
     from omegalax_amd import gdn_decode_step
-    say("decode C2 B=64")
-    d = W.decode_inputs(64)
+    say(f"decode C2 B={B}")
+    d = W.decode_inputs(B)
     t = W.to_device(d)
     out = gdn_decode_step(t["mixed_qkv"], t["z"], t["a"], t["b"], t["conv_w"], t["A_log"],
                           t["dt_bias"], t["norm_w"], t["conv_state"], t["state"],

@@ -191,11 +191,28 @@ def test_layer_c1_shape_batch_slice():
     assert torch.equal(out3, out[3:4]) and torch.equal(S3, S[3:4])
 
 
+def key_head_slice(d, hk, Hk, dk, Hv, dv):
+    """The inputs of key head hk and its gqa value heads alone (a layer with Hk=1): its q,
+    k and value channels of mixed_qkv and conv_w, its heads of z, a, b, A_log, dt_bias.
+    Key heads share nothing, so the slice's outputs are the full layer's on those heads.
+    Returns (inputs, channel indices, value-head slice)."""
+    gqa = Hv // Hk
+    hs = slice(hk * gqa, (hk + 1) * gqa)
+    ch = np.concatenate([np.arange(hk * dk, (hk + 1) * dk),
+                         Hk * dk + np.arange(hk * dk, (hk + 1) * dk),
+                         2 * Hk * dk + np.arange(hk * gqa * dv, (hk + 1) * gqa * dv)])
+    sl = dict(mixed_qkv=d["mixed_qkv"][..., ch], z=d["z"][..., hs, :], a=d["a"][..., hs],
+              b=d["b"][..., hs], conv_w=d["conv_w"][ch], A_log=d["A_log"][hs],
+              dt_bias=d["dt_bias"][hs], norm_w=d["norm_w"])
+    return sl, ch, hs
+
+
 def test_layer_c3_full_size_packed_equals_separate():
     """Config C3 at full size: T=32768 packed as 8 Dirichlet-length sequences with carried
     initial states (C1 heads, B=1).  Each sequence's output, final state and conv cache from
-    the packed call equal a separate call on that sequence (GPU vs GPU), and the shortest
-    sequence matches the oracle."""
+    the packed call equal a separate call on that sequence (GPU vs GPU); the shortest
+    sequence matches the oracle on every head, and the longest (the 10,779-token one) on the
+    first and last key heads' value heads: its output, final state and conv cache."""
     say("layer C3 full size")
     dims = dict(Hk=16, dk=128, Hv=32, dv=128)
     d = W.varlen_inputs()
@@ -220,3 +237,17 @@ def test_layer_c3_full_size_packed_equals_separate():
     assert rel(np_(out[:, s:e]), ref) < BF16_TOL
     assert rel(np_(S[n:n + 1]), S_ref) < STATE_TOL
     assert np.array_equal(np_(conv[n:n + 1]), conv_ref)
+    n = int(np.argmax(lens))
+    s, e = int(cu[n]), int(cu[n + 1])
+    Hk, dk, Hv, dv = dims["Hk"], dims["dk"], dims["Hv"], dims["dv"]
+    out_h = np_(out[:, s:e]).reshape(1, e - s, Hv, dv)
+    for hk in (0, Hk - 1):
+        say(f"  longest sequence ({e - s} tokens), key head {hk}: fp64 oracle")
+        dn = {k_: (v_[:, s:e] if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+              for k_, v_ in d.items() if k_ not in ("cu_seqlens", "initial_state")}
+        sl, ch, hs = key_head_slice(dn, hk, Hk, dk, Hv, dv)
+        sdims = dict(Hk=1, dk=dk, Hv=Hv // Hk, dv=dv)
+        ref, S_ref, conv_ref = ref_prefill(sl, sdims, None, S0[n:n + 1, hs])
+        assert rel(out_h[:, :, hs].reshape(ref.shape), ref) < BF16_TOL
+        assert rel(np_(S[n:n + 1, hs]), S_ref) < STATE_TOL
+        assert np.array_equal(np_(conv[n:n + 1])[:, ch], conv_ref)

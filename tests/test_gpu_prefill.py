@@ -164,8 +164,10 @@ def test_chunk_split_sequence_equals_whole():
 def test_chunk_c4_full_size():
     """Config C4 at full size (B=1, T=65536, Hk=16, Hv=64, bf16 N(0,1) q/k/v, e^g ~
     U(0.9, 0.9999), beta = sigmoid(N(0,1))), drawn on the GPU from a seeded generator: the
-    call split at T/2 with the state carried equals the whole call, and a causal prefix
-    (T=4096) of key head 0's four value heads matches the oracle."""
+    call split at T/2 with the state carried equals the whole call, and key head 0's four
+    value heads -- their whole T=65536 output and their final state, from the full-size
+    call -- match the fp64 oracle run on that key head alone (value heads share nothing
+    across key heads, so the slice is exact)."""
     from omegalax_amd import chunk_gated_delta_rule
     say("chunk C4 full size")
     T, Hk, Hv, d = 65536, 16, 64, 128
@@ -186,10 +188,14 @@ def test_chunk_c4_full_size():
         return float((a - b).abs().max() / b.abs().max())
     assert trel(o1, o[:, :n]) < 1e-6 and trel(o2, o[:, n:]) < 1e-6
     assert trel(S2, S) < 1e-6
-    P = 4096
-    o_ref, _ = run_ref(np_(q[:, :P, :1]), np_(k[:, :P, :1]), np_(v[:, :P, :4]),
-                       np_(g[:, :P, :4]), np_(beta[:, :P, :4]), None, "bf16")
-    assert rel(np_(o[:, :P, :4]), o_ref) < BF16_TOL
+    del o1, o2, S1, S2
+    say("  fp64 oracle on key head 0 (value heads 0-3), T=65536")
+    o_ref, S_ref = run_ref(np_(q[:, :, :1]), np_(k[:, :, :1]), np_(v[:, :, :4]),
+                           np_(g[:, :, :4]), np_(beta[:, :, :4]), None, "bf16")
+    e_o, e_S = rel(np_(o[:, :, :4]), o_ref), rel(np_(S[:, :4]), S_ref)
+    say(f"  o {e_o:.2e} (tolerance {BF16_TOL}), final state {e_S:.2e} (tolerance {STATE_TOL})")
+    assert e_o < BF16_TOL
+    assert e_S < STATE_TOL
 
 
 def test_chunk_block_width_does_not_change_results():
