@@ -72,11 +72,6 @@ __device__ __forceinline__ const T* at_bytes(const T* base, unsigned off) {
   return (const T*)((const unsigned char*)base + off);
 }
 
-// Buffer resource over `bytes` bytes at p (raw, stride 0): accesses through it take a
-// 32-bit lane offset and a uniform scalar offset, with no per-lane address arithmetic.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 
 // index of the block pair (i, p), p <= i / 2
 __host__ __device__ constexpr int pair_index(int i, int p) { return i + (i == 3) + p; }

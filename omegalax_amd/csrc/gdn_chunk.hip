@@ -733,10 +733,13 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
     if constexpr (MODE != MODE_LAYER) {
       const auto ob = buf_rsrc(p.o + (t0 * p.Hv + h) * (long long)DV + col0, 4u * C * o_rs);
       auto store = [&](int i) {
+        // row offset in the lane offset: a store of more than 64 bits with a register scalar
+        // offset is one the compiler lets overwrite its data registers right after issue,
+        // which gfx950 does not tolerate
         __builtin_amdgcn_raw_buffer_store_b128(
             u32x4{__float_as_uint(o[i][0]), __float_as_uint(o[i][1]), __float_as_uint(o[i][2]),
                   __float_as_uint(o[i][3])},
-            ob, o_lane, 4 * 16 * i * o_rs, 0);
+            ob, o_lane + 4u * 16u * i * o_rs, 0, 0);
       };
       if (nvalid == C) {
 #pragma unroll

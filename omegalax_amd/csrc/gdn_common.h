@@ -26,6 +26,14 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// Buffer resource over `bytes` bytes at p (raw, stride 0): accesses through it take a
+// 32-bit lane offset and a uniform scalar offset, with no per-lane address arithmetic.
+// Loads at offsets past `bytes` return zeros and stores there are dropped, without a
+// memory access: a range of 0 turns every access through the resource into a no-op.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Workgroup barrier that orders LDS accesses only: it does not wait for the wave's
 // outstanding global loads and stores (__syncthreads does), so prefetches and result
 // stores stay in flight across it.
