@@ -7,7 +7,8 @@ Workloads (synthetic, seeded; inputs resident in HBM before the timed region):
   prefill  (default, the headline) config C1: GDN layer prefill from the projection
            outputs (mixed_qkv, z, a, b) to the gated-norm output, B=4 T=4096 Hk=16 Hv=32
            d=128.  A "step" is one omx_gdn_prefill call over the whole batch.  The line
-           also carries C3, C4, the C2 decode step at B=64 and B=256, the backward passes,
+           also carries C3, C4, the C2 decode step at B=1, 8, 64 and 256 (with its CPU
+           baseline), the backward passes,
            the whole layer with its projections and the gate projections, each under its
            own key.
   c1       the C1 leg of the headline alone (the layer step and the core call).
@@ -107,6 +108,19 @@ def cpu_cores():
         return os.cpu_count() or 1
 
 
+def cpu_model():
+    """The host CPU's model string (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 # ----------------------------------------------------------------------------- decode (C2)
 
 def bench_decode(B, steps, warmup, cpu_baseline, min_rotation_bytes=512 << 20):
@@ -157,23 +171,37 @@ def bench_decode(B, steps, warmup, cpu_baseline, min_rotation_bytes=512 << 20):
     return res
 
 
-def cpu_decode_baseline(B=8, budget_s=10.0):
-    """Oracle decode step (numpy fp64, the 'port') on a bounded sample: B=8 sequences."""
+def cpu_decode_baseline(batches=(1, 8, 64), budget_s=4.0):
+    """Oracle decode step (numpy fp64 restatement, the 'port') at C2's head layout, timed
+    per batch size on whole steps while they fit ``budget_s`` (at least one step each).
+    B=256 is not timed: its fp64 state alone is 1 GiB, and the step scales with the state
+    it streams, so it is reported as B=64's rate (tokens/s per sequence are flat in B on
+    this path, as the three timed sizes show)."""
     from oracle import gdn_oracle as O
     from omegalax_amd import workloads as W
-    d = W.decode_inputs(B)
-    S = d["state"].astype(np.float64)
-    conv = d["conv_state"]
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or n == 0:
-        _, conv, S = O.gdn_decode_step(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"],
-                                       d["A_log"], d["dt_bias"], d["norm_w"], conv, S,
-                                       Hk=16, dk=128, Hv=32, dv=128)
-        n += 1
-    el = time.perf_counter() - t0
-    return {"value": B * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
-            "sample": f"{n} decode steps of the numpy fp64 oracle at B={B}, C2 head layout"}
+    per_b = {}
+    for B in batches:
+        d = W.decode_inputs(B)
+        S = d["state"].astype(np.float64)
+        conv = d["conv_state"]
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            _, conv, S = O.gdn_decode_step(d["mixed_qkv"], d["z"], d["a"], d["b"], d["conv_w"],
+                                           d["A_log"], d["dt_bias"], d["norm_w"], conv, S,
+                                           Hk=16, dk=128, Hv=32, dv=128)
+            n += 1
+            el = time.perf_counter() - t0
+            if el * (n + 1) / n > budget_s:
+                break
+        per_b[f"B={B}"] = {"tokens_per_s": B * n / el, "ms_per_step": el / n * 1e3, "steps": n}
+    top = per_b[f"B={batches[-1]}"]
+    return {"value": top["tokens_per_s"], "unit": "tokens/s", "cores": cpu_cores(),
+            "cpu_model": cpu_model(), "kind": "port", "per_batch": per_b,
+            "sample": f"whole decode steps of the numpy fp64 oracle (conv update, recurrent "
+                      f"step, gated norm) at C2's head layout (Hk=16 Hv=32 d=128) for "
+                      f"B in {list(batches)}, about {budget_s:.0f} s each; value is "
+                      f"B={batches[-1]}'s"}
 
 
 # ----------------------------------------------------------------------------- core call
@@ -437,7 +465,8 @@ def cpu_prefill_baseline(T=4096, budget_s=20.0):
         el = time.perf_counter() - t0
         if el * (n + 1) / n > budget_s:
             break
-    return {"value": B * T * n / el, "unit": "tokens/s", "cores": cpu_cores(), "kind": "port",
+    return {"value": B * T * n / el, "unit": "tokens/s", "cores": cpu_cores(),
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"{n} run(s) of the numpy fp32 layer prefill restatement on one C1 "
                       f"sequence (B=1 T={T}, Hk=16 Hv=32 d=128); C1 (4 such sequences) "
                       f"extrapolates to {4 * el / n:.1f} s at the same tokens/s"}
@@ -582,6 +611,8 @@ def main():
     pre = bench_prefill(K, W_, cpu)
     c3 = bench_c3(max(K // 2, 5), W_)
     c4 = bench_core(1, 65536, 16, 64, 128, max(K // 4, 3), min(W_, 2), long_memory=True)
+    dec1 = bench_decode(1, max(K, 20), W_, False)
+    dec8 = bench_decode(8, max(K, 20), W_, False)
     dec64 = bench_decode(64, max(K, 20), W_, False)
     dec256 = bench_decode(256, max(K, 20), W_, False)
     bwd = bench_bwd(4, 4096, 16, 32, 128, max(K // 2, 5), W_)
@@ -601,6 +632,8 @@ def main():
                "roofline": c4["roofline"]},
         "decode": dec(dec64),
         "decode_b256": dec(dec256),
+        "decode_b1": dec(dec1),
+        "decode_b8": dec(dec8),
         "backward": {"config": "chunk_gated_delta_rule_bwd at C1 (B=4 T=4096 Hk=16 Hv=32 d=128)",
                      "kernel_ms": bwd["kernel_ms"], "roofline": bwd["roofline"]},
         "layer_backward": {"config": "gdn_prefill_bwd at C1", "kernel_ms": lbwd["kernel_ms"],
@@ -610,6 +643,7 @@ def main():
     }
     if cpu:
         extra["cpu_baseline"] = pre["cpu_baseline"]
+        extra["decode_cpu_baseline"] = cpu_decode_baseline()
     print(_line("GDN prefill tokens/s + %MFMA peak; decode-step HBM GB/s + %of 8 TB/s",
                 pre["tokens_per_s"], "tokens/s", K, W_, pre["ms_per_step"], "bf16",
                 {"workload": "C1 GDN layer prefill (projection outputs -> gated-norm output)",
