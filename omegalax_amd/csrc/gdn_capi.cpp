@@ -58,7 +58,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // sums of o^2 for the gated norm, and the plan of packed sequences (chunk offsets and
 // the ordered copy of cu_seqlens the kernels read).
 struct ChunkWs {
-  size_t rec, kn, qn, vc, opart, oss, off, cu, ord, total;
+  size_t rec, kn, qn, vc, opart, oss, xch, off, cu, ord, total;
 };
 
 ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64_t dv, int64_t N,
@@ -82,6 +82,10 @@ ChunkWs chunk_ws(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk, int64
     o += align_up(tokens * (size_t)(Hv * dv) * 2, 256);
     w.oss = o;
     o += align_up((tokens + 63) / 64 * 64 * (size_t)Hv * (size_t)(dv / 16) * 4, 256);
+    // the fused norm's exchange of row partials: {value, tag} per (sequence, value head,
+    // column block, ring entry, row), for up to dv / 16 blocks
+    w.xch = o;
+    o += align_up((size_t)N * (size_t)Hv * (size_t)(dv / 16) * omx::kXchRing * 64 * 8, 256);
   }
   w.off = o;
   o += align_up((size_t)(N + 1) * 4, 256);
@@ -317,6 +321,8 @@ void setup_chunked(omx::ChunkParams& p, const ChunkWs& ws, void* workspace, int 
     p.vc = omx::layer_scan_forms_v(p.dk) ? nullptr : base + ws.vc;
     p.vs = p.vc;
     p.vs_ld = (long long)p.Hv * p.DV;
+    p.ss_xch = (unsigned*)(base + ws.xch);
+    p.ss_xch_slots = omx::layer_scan_blocks(p);
   } else {
     p.vs = p.v;
     p.vs_ld = p.v_ld;
@@ -552,8 +558,10 @@ int prefill_core(const char* fn, const void* mixed_qkv, const void* z, const voi
   p.qk_l2norm = 1;
   p.o_part = (char*)workspace + ws.opart;
   p.o_ss = (float*)((char*)workspace + ws.oss);
+  p.inv_dv = 1.0f / (float)dv_real;
   hipError_t e = launch_chunked(p, ws, workspace, omx::kModeLayer, (hipStream_t)stream);
-  if (e == hipSuccess)
+  // the scan applies the gated norm itself for one-round grids; else the epilogue kernel
+  if (e == hipSuccess && !omx::layer_scan_fuses_norm(p))
     e = omx::launch_norm_epilogue(p.o_part, p.o_ss, omx::layer_ss_slots(p), z, norm_w, out,
                                   tokens, (int)Hv, (int)dv, (int)dv_real, eps,
                                   (hipStream_t)stream);

@@ -137,11 +137,16 @@ __device__ __forceinline__ float ss_tree(const float* a) {
 // its first operand with the lower 32 lanes of its second, so after swapping (a, b) the
 // two results summed give, in lanes q < 2, a's sum over rows q and q + 2 and, in lanes
 // q >= 2, b's; v_permlane16_swap does the same for odd and even 16-lane rows.
+// The four squares are summed by an explicit fma chain: written as a + b + c + d, the
+// compiler may contract the first sum either way round (fma(x0, x0, x1^2) or
+// fma(x1, x1, x0^2)), differently in different kernels, and the scans that fuse the
+// norm must give the statistic of the ones that leave it to the epilogue kernel.
 __device__ __forceinline__ float row_sq_scatter(const f32x4* x) {
   float ss[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    ss[i] = x[i][0] * x[i][0] + x[i][1] * x[i][1] + x[i][2] * x[i][2] + x[i][3] * x[i][3];
+    ss[i] = __builtin_fmaf(x[i][3], x[i][3],
+                           __builtin_fmaf(x[i][2], x[i][2], __builtin_fmaf(x[i][1], x[i][1], x[i][0] * x[i][0])));
   const auto s02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss[0]), __float_as_uint(ss[2]),
                                                     false, false);
   const auto s13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(ss[1]), __float_as_uint(ss[3]),

@@ -304,7 +304,21 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
 
 // BWD (the backward pass's recompute): stores the state entering every chunk and V_new,
 // and o only when p.o is set.
-template <int DK, int MODE, bool BWD = false, int NWC_ = 4>
+//
+// FUSE (layer, direct loads, a grid the chip holds in one round): the gated RMSNorm
+// (deltanet.py:282-293) is applied here and the scan writes the layer's output.  A row of
+// o spans the nb workgroups of a value head (its column blocks), so its statistic needs
+// their partial sums: each workgroup's loader publishes its rows' partial (the fp32 o's
+// sum of squares over the block) for chunk c one step after the chunk, written through
+// to memory (system scope) with a flag raised behind it, and one step later reads every
+// block's partial (L2 bypassed), sums them in slot order with the pairwise tree the
+// epilogue kernel uses and leaves 1/RMS per row in LDS.  Meanwhile the compute
+// wavefronts keep their bf16 o rows in a four-chunk LDS ring and, three steps after the
+// chunk, normalise and gate them: w (o rsqrt(mean + eps)) silu(z), the epilogue kernel's
+// arithmetic, so the output is bit-identical to the unfused path's.  Every workgroup of
+// the grid is resident at once, so a wait for another block's flag ends; it is bounded
+// all the same.
+template <int DK, int MODE, bool BWD = false, int NWC_ = 4, bool FUSE = false>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
 // SIMD) instead of holding back for a second workgroup.
@@ -331,6 +345,12 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   constexpr bool WG_SS = DIRECT && MODE == MODE_LAYER;
   __shared__ float sSS[WG_SS ? 2 : 1][WG_SS ? NWC : 1][C];
   float ss_prev = 0.f;  // this lane's row sum of the previous chunk, not yet in sSS
+  static_assert(!FUSE || WG_SS, "the fused norm runs on the layer's direct-load scan");
+  constexpr int kRing = 4;  // (FUSE) chunks of bf16 o kept per compute wavefront
+  constexpr int kFin = 3;   // (FUSE) steps from a chunk to its normalisation
+  // (FUSE) lane l's 4 x 4 bf16 o values of row block i of chunk c, wave w: sO[c % 4][w][i][l]
+  __shared__ __align__(16) u32x2 sO[FUSE ? kRing : 1][FUSE ? NWC : 1][FUSE ? 4 : 1][64];
+  __shared__ float sRN[FUSE ? 2 : 1][C];  // (FUSE) 1/RMS of each row of a chunk
   constexpr int K_LO = C * LDK, V_LO = C * LDT;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
@@ -395,6 +415,54 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
     }
   }
 
+  // (FUSE) the normalisation of chunk c's rows on the compute wavefronts: o from the LDS
+  // ring, 1/RMS of each row from sRN (left there by the loader), z loaded at the start of
+  // the step; out = w (o rn) silu(z), stored through a buffer whose range ends at the
+  // chunk's last valid row.  The row offsets are in the lane offsets, which the range
+  // check covers (a scalar offset is not relied on to be checked).  c < 0 does nothing.
+  u32x2 zf[4];
+  const float4 nw4 = FUSE ? *(const float4*)(p.norm_w + col0 + 16 * wave + 4 * lq)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+  auto chunk_rows = [&](int c, long long& tc) {
+    tc = s0 + (long long)c * C;
+    return (int)((s1 - tc) < C ? (s1 - tc) : C);
+  };
+  auto z_load = [&](int c) {
+    if constexpr (FUSE) {
+      if (c < 0) return;  // uniform
+      long long tc;
+      const int nvc = chunk_rows(c, tc);
+      const auto zr = buf_rsrc((const bf16_t*)p.z + (tc * p.Hv + h) * (long long)DV + col0,
+                               2u * nvc * o_rs);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        zf[i] = __builtin_amdgcn_raw_buffer_load_b64(zr, o_lane_h + 2u * 16u * i * o_rs, 0, 0);
+    }
+  };
+  auto finalize = [&](int c) {
+    if constexpr (FUSE) {
+      if (c < 0) return;  // uniform
+      long long tc;
+      const int nvc = chunk_rows(c, tc);
+      const auto orr = buf_rsrc((bf16_t*)p.out + (tc * p.Hv + h) * (long long)DV + col0,
+                                2u * nvc * o_rs);
+      const float w[4] = {nw4.x, nw4.y, nw4.z, nw4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x2 ow = sO[c % kRing][wave][i][l];
+        const float rn = sRN[c & 1][16 * i + lr];
+        uint32_t r[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float o0 = __uint_as_float(ow[e] << 16), o1 = __uint_as_float(ow[e] & 0xffff0000u);
+          const float z0 = __uint_as_float(zf[i][e] << 16), z1 = __uint_as_float(zf[i][e] & 0xffff0000u);
+          r[e] = pack_bf16(w[2 * e] * (o0 * rn) * silu_fast(z0), w[2 * e + 1] * (o1 * rn) * silu_fast(z1));
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{r[0], r[1]}, orr, o_lane_h + 2u * 16u * i * o_rs, 0, 0);
+      }
+    }
+  };
+
   // one chunk on the compute wavefronts, from buffer (sK, sQ, sV, sRec)
   auto run_chunk = [&](const int j, bf16_t* sK, bf16_t* sQ, bf16_t* sV, unsigned char* sRec) {
     const long long t0 = s0 + (long long)j * C;
@@ -407,9 +475,11 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
       // the loader's loads of chunk j have landed (it waited before arriving), and
       // chunk j-1, the last reader of the other buffer, is finished everywhere
       lds_barrier();
-      if constexpr (WG_SS) {
+      if constexpr (WG_SS && !FUSE) {
         if (j >= 1) sSS[(j - 1) & 1][wave][16 * lq + lr] = ss_prev;
       }
+      // (FUSE) z of the chunk normalised at the end of this step, in flight meanwhile
+      if constexpr (FUSE) z_load(j - kFin);
     } else {
     __syncthreads();  // the previous chunk's readers are done with the shared arrays
 
@@ -749,6 +819,15 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         for (int i = 0; i < 4; ++i)
           if (16 * i + lr < nvalid) store(i);
       }
+    } else if constexpr (FUSE) {
+      // unnormalised o in bf16 into the LDS ring, and the rows' sums of squares of the fp32
+      // o into sSS for the loader (after the next barrier); finalize() normalises the chunk
+      // kFin steps later
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        sO[j % kRing][wave][i][l] = u32x2{pack_bf16(o[i][0], o[i][1]), pack_bf16(o[i][2], o[i][3])};
+      sSS[j & 1][wave][16 * lq + lr] = row_sq_scatter(o);
+      finalize(j - kFin);
     } else {
       // unnormalised o in bf16; the epilogue kernel applies the norm, from the fp32 sums
       // of squares stored below
@@ -797,6 +876,72 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           if (l < nvj) p.o_ss[ss_index(tj + l, h, blk, p.Hv, p.ss_slots)] = ss_tree<NWC>(v);
         }
       };
+      // (FUSE) the row partials of chunk c in the exchange array: [slot][h][block][row]
+      constexpr int NBX = 256 / BV;  // most column blocks a value head has at this width
+      u32x2 xv[FUSE ? NBX : 1];
+      int gave_up = 0;  // a bounded wait that ran out stops all later waits
+      // ring entry of chunk c of block s: every block has read an entry before any block
+      // writes it again, kXchRing chunks later (a block writes chunk c + 4's partial only
+      // after it has seen every block's partial of chunk c + 2, which they publish after
+      // they have read chunk c's)
+      auto xch_rsrc = [&](int c, int s, unsigned bytes) {
+        return buf_rsrc(p.ss_xch + 2 * ((((size_t)n * p.Hv + h) * p.ss_xch_slots + s) * kXchRing +
+                                        c % kXchRing) * C,
+                        bytes);
+      };
+      // this workgroup's partial of chunk c's row l (its waves' partials, in sSS since the
+      // barrier that opened this step), written through to memory with tag c + 1
+      auto publish = [&](int c) {
+        if constexpr (FUSE) {
+          long long tc;
+          const int nvc = chunk_rows(c, tc);
+          float v[NWC];
+#pragma unroll
+          for (int w = 0; w < NWC; ++w) v[w] = sSS[c & 1][w][l];
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(ss_tree<NWC>(v)), (unsigned)c + 1u},
+                                                xch_rsrc(c, blk, 8u * nvc), 8u * l, 0, 17);
+        }
+      };
+      // every block's partial of chunk c's row l, read past the caches (system scope)
+      auto gather = [&](int c) {
+        if constexpr (FUSE) {
+#pragma unroll
+          for (int s = 0; s < NBX; ++s)
+            if (s < p.nb) xv[s] = __builtin_amdgcn_raw_buffer_load_b64(xch_rsrc(c, s, 8u * C), 8u * l, 0, 17);
+        }
+      };
+      // once every valid row's entries carry chunk c's tag: the row's sum over the blocks in the
+      // pairwise order of the epilogue kernel's butterfly, and 1/RMS into sRN
+      auto finish = [&](int c) {
+        if constexpr (FUSE) {
+          long long tc;
+          const int nvc = chunk_rows(c, tc);
+          auto ready = [&]() {
+            bool r = true;
+#pragma unroll
+            for (int s = 0; s < NBX; ++s)
+              if (s < p.nb) r = r && xv[s][1] == (unsigned)c + 1u;
+            return l >= nvc || r;
+          };
+          for (int tries = 0; !gave_up && __ballot(!ready()) != 0ull; ++tries) {
+            if (tries == (1 << 20)) {  // about a second: give up rather than hang
+              gave_up = 1;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+            gather(c);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+          }
+          float t[NBX];
+#pragma unroll
+          for (int s = 0; s < NBX; ++s) t[s] = s < p.nb ? __uint_as_float(xv[s][0]) : 0.f;
+#pragma unroll
+          for (int w = 1; w < NBX; w <<= 1)
+#pragma unroll
+            for (int s = 0; s + w < NBX; s += 2 * w) t[s] += t[s + w];
+          sRN[c & 1][l] = rsqrtf(__builtin_fmaf(t[0], p.inv_dv, p.eps));  // as the epilogue kernel
+        }
+      };
       auto load = [&](int j, lds_bf16* nK, lds_bf16* nQ, lds_bf16* nV, lds_u8* nRec) {
         lds_barrier();
         if (j + 1 < nchunks) {
@@ -804,14 +949,28 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           const int nvn = (int)((s1 - tn) < C ? (s1 - tn) : C);
           stage_all<DK, MODE, BV, BWD>(p, tn, nvn, rec_of(j + 1), hk, h, col0, nK, nQ, nV, nRec);
         }
+        if constexpr (FUSE) {
+          // chunk j - 1's partial (its waves wrote sSS before this step's barrier), then
+          // the partials of chunk j - 2 that every block published a step ago
+          if (j >= 1 && j - 1 < nchunks) publish(j - 1);
+          if (j >= 2 && j - 2 < nchunks) gather(j - 2);
+        }
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the next barrier
-        if (j >= 2) store_ss(j - 2);  // written after barrier j - 1, visible after barrier j
+        if constexpr (FUSE) {
+          if (j >= 2 && j - 2 < nchunks) finish(j - 2);
+        } else {
+          if (j >= 2) store_ss(j - 2);  // written after barrier j - 1, visible after barrier j
+        }
       };
       for (int j = 0; j < nchunks; j += 2) {
         load(j, (lds_bf16*)sK1, (lds_bf16*)sQ1, (lds_bf16*)sV1, (lds_u8*)sRec1);
         if (j + 1 < nchunks) load(j + 1, (lds_bf16*)sK0, (lds_bf16*)sQ0, (lds_bf16*)sV0, (lds_u8*)sRec0);
       }
-      if constexpr (WG_SS) {  // the last two chunks' row sums, as in the loop
+      if constexpr (FUSE) {  // the pipeline's drain: kFin more steps (no loads)
+        if (nchunks > 0)
+          for (int j = nchunks; j < nchunks + kFin; ++j)
+            load(j, (lds_bf16*)sK0, (lds_bf16*)sQ0, (lds_bf16*)sV0, (lds_u8*)sRec0);
+      } else if constexpr (WG_SS) {  // the last two chunks' row sums, as in the loop
         if (nchunks > 0) {
           lds_barrier();  // chunk n - 2's are visible; the buffer of n - 1's is free
           if (nchunks >= 2) store_ss(nchunks - 2);
@@ -865,9 +1024,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
             if (j + 2 < nchunks) form(j + 2, ra, sV0);
           }
         }
-        if (nchunks > 0) {  // the loader's two barriers after its loop
+        if (nchunks > 0) {  // the loader's barriers after its loop
           lds_barrier();
           lds_barrier();
+          if constexpr (FUSE) lds_barrier();
         }
       }
     } else {
@@ -875,7 +1035,14 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         run_chunk(j, sK0, sQ0, sV0, sRec0);
         if (j + 1 < nchunks) run_chunk(j + 1, sK1, sQ1, sV1, sRec1);
       }
-      if constexpr (WG_SS) {  // the loader's two barriers after its loop
+      if constexpr (FUSE) {  // the drain: the last kFin chunks' normalisation
+        if (nchunks > 0)
+          for (int j = nchunks; j < nchunks + kFin; ++j) {
+            lds_barrier();
+            z_load(j - kFin);
+            finalize(j - kFin);
+          }
+      } else if constexpr (WG_SS) {  // the loader's two barriers after its loop
         if (nchunks > 0) {
           lds_barrier();
           sSS[(nchunks - 1) & 1][wave][16 * lq + lr] = ss_prev;
@@ -925,7 +1092,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 
 // The scan's workgroups cover Cfg::BV columns each; p.nb (the other kernels' 64-column
 // blocks) is replaced by the scan's own count in a copy of the parameters.
-template <int DK, int MODE, bool BWD = false, int NWC = 4>
+template <int DK, int MODE, bool BWD = false, int NWC = 4, bool FUSE = false>
 hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
   using Q_ = Cfg<DK, MODE, NWC, BWD>;
   ChunkParams q = p;
@@ -934,7 +1101,7 @@ hipError_t launch_scan_cfg(const ChunkParams& p, hipStream_t stream) {
   // loads, else one per wavefront
   q.ss_slots = Q_::DIRECT ? q.nb : p.DV / 16;
   const unsigned grid = (unsigned)(q.N * q.Hv * q.nb);
-  hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD, NWC>), dim3(grid), dim3(Q_::NTH), 0, stream, q);
+  hipLaunchKernelGGL((scan_kernel<DK, MODE, BWD, NWC, FUSE>), dim3(grid), dim3(Q_::NTH), 0, stream, q);
   return hipGetLastError();
 }
 
@@ -964,18 +1131,32 @@ int scan_tiles_per_wg(const ChunkParams& p) {
   return 1;
 }
 
-template <int DK, int MODE>
+template <int DK, int MODE, bool FUSE = false>
 hipError_t launch_scan_direct(const ChunkParams& p, hipStream_t stream) {
   switch (scan_tiles_per_wg(p)) {
-    case 1: return launch_scan_cfg<DK, MODE, false, 1>(p, stream);
-    case 2: return launch_scan_cfg<DK, MODE, false, 2>(p, stream);
-    default: return launch_scan_cfg<DK, MODE, false, 4>(p, stream);
+    case 1: return launch_scan_cfg<DK, MODE, false, 1, FUSE>(p, stream);
+    case 2: return launch_scan_cfg<DK, MODE, false, 2, FUSE>(p, stream);
+    default: return launch_scan_cfg<DK, MODE, false, 4, FUSE>(p, stream);
   }
 }
 
 }  // namespace
 
 int chunk_block_cols() { return kBlockCols; }
+
+int layer_scan_blocks(const ChunkParams& p) {
+  return p.dk == 128 ? p.DV / (16 * scan_tiles_per_wg(p)) : p.DV / kBlockCols;
+}
+
+// The layer scan applies the gated norm itself (FUSE) when it loads directly (dk = 128),
+// the exchange array is there and its grid is one round of the chip: at one workgroup per
+// CU (the scan's LDS), every workgroup is then resident together, so the waits for the
+// other column blocks' partials end.
+bool layer_scan_fuses_norm(const ChunkParams& p) {
+  if (!p.ss_xch || !layer_v_in_scan(p.dk)) return false;
+  const long long grid = (long long)p.N * p.Hv * layer_scan_blocks(p);
+  return grid <= device_cus();
+}
 
 int layer_ss_slots(const ChunkParams& p) {
   return p.dk == 128 ? p.DV / (16 * scan_tiles_per_wg(p)) : p.DV / 16;
@@ -1014,7 +1195,10 @@ hipError_t launch_scan(const ChunkParams& p, int mode, hipStream_t stream) {
     return hipErrorInvalidValue;
   }
   if (mode == MODE_LAYER) {
-    if (p.dk == 128) return launch_scan_direct<128, MODE_LAYER>(p, stream);
+    if (p.dk == 128) {
+      if (layer_scan_fuses_norm(p)) return launch_scan_direct<128, MODE_LAYER, true>(p, stream);
+      return launch_scan_direct<128, MODE_LAYER>(p, stream);
+    }
     if (p.dk == 64) return launch_scan_cfg<64, MODE_LAYER>(p, stream);
     return hipErrorInvalidValue;
   }

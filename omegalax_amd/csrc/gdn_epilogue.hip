@@ -24,7 +24,7 @@ namespace {
 __device__ __forceinline__ void norm_row8(uint4 ow, uint4 zw, float ss, const float* norm_w, int c,
                                           float inv_dv, float eps, uint4* dst) {
   const uint32_t ov[4] = {ow.x, ow.y, ow.z, ow.w}, zv[4] = {zw.x, zw.y, zw.z, zw.w};
-  const float rn = rsqrtf(ss * inv_dv + eps);
+  const float rn = rsqrtf(__builtin_fmaf(ss, inv_dv, eps));  // as the scans that fuse the norm
   const float4 w0 = *(const float4*)(norm_w + c), w1 = *(const float4*)(norm_w + c + 4);
   const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
   uint32_t r[4];

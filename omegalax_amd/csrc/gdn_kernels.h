@@ -36,6 +36,9 @@ struct DecodeParams {
 };
 
 // Chunked prefill (core function or fused layer).
+// ring entries per (sequence, value head, column block) of ChunkParams::ss_xch
+constexpr int kXchRing = 4;
+
 struct ChunkParams {
   // core mode inputs: q/k [tokens, *, dk], v [tokens, *, DV] with row strides (elements)
   const void* q;
@@ -61,6 +64,14 @@ struct ChunkParams {
   float* o_ss;                 // [ceil(tokens / 64), Hv, ss_slots, 64] fp32 (workspace):
                                // partial sums of squares of the fp32 o over a row
   int ss_slots;                // partials per (token, head) row (set by the scan's launcher)
+  // (layer, scan with the gated norm fused) the workgroups' row partials of recent chunks,
+  // [N][Hv][ss_xch_slots][kXchRing][64] pairs {fp32 bits, tag}: chunk c of a sequence uses
+  // ring entry c % kXchRing with tag c + 1, written in one 8-byte store, so a reader that
+  // sees its tag sees the value; zeroed by the preparation kernel (the task of each
+  // sequence's first chunk)
+  unsigned* ss_xch;
+  int ss_xch_slots;            // partial slots per (chunk slot, value head) in ss_xch
+  float inv_dv;                // 1 / the caller's dv (the norm's mean)
   // both
   const float* initial_state;  // [N, Hv, dk, DV] or null
   float* final_state;          // [N, Hv, dk, DV] or null
@@ -209,6 +220,11 @@ hipError_t launch_norm_epilogue(const void* o_part, const float* o_ss, int nss, 
 
 // Row-sum partials per (token, value head) the layer scan writes for these parameters.
 int layer_ss_slots(const ChunkParams& p);
+// Column blocks (workgroups) per value head of the layer scan for these parameters.
+int layer_scan_blocks(const ChunkParams& p);
+// Whether the layer scan applies the gated norm itself for these parameters (then it
+// writes p.out and the epilogue kernel is not needed); needs p.ss_xch.
+bool layer_scan_fuses_norm(const ChunkParams& p);
 
 // An [R][G][E] view of a buffer for launch_pad_copy: element pointer, group and element
 // counts, row and group strides (elements).

@@ -649,6 +649,23 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
       }
       lds_barrier();  // sLf / sTd are rewritten for the next value head
     }
+    // (layer) the task of a sequence's first chunk clears the exchange ring of the row
+    // partials of the sequence's value heads under this key head (tag 0); the scan that
+    // fuses the gated norm writes chunk c's entries with tag c + 1 (stores through a buffer
+    // whose range ends at the ring: lanes past it are dropped).  The scan writes and reads
+    // the ring at system scope, past the L2s, so the zeros are written through to memory
+    // the same way (sc0 sc1) rather than left to the L2s' write-back: a previous call's
+    // entries there carry the tags this call waits for.
+    if constexpr (MODE == MODE_LAYER) {
+      if (p.ss_xch && t0 == s0) {
+        const int cnt = gqa * p.ss_xch_slots * kXchRing * C;  // {value, tag} pairs
+        const auto xr = buf_rsrc(
+            p.ss_xch + 2 * (((size_t)n * p.Hv + hk * gqa) * p.ss_xch_slots) * kXchRing * C,
+            8u * (unsigned)cnt);
+        for (int k = 0; k < cnt; k += NT)
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, xr, 8u * (unsigned)(k + tid), 0, 17);
+      }
+    }
   }
 }
 

@@ -250,8 +250,8 @@ def test_prefill_noalloc_rejects_shapes_beyond_its_fixed_scratch():
     L = _lib.lib()
     cap = L.omx_gdn_prefill_noalloc_max_scratch()
     assert cap == 64 << 20
-    assert L.omx_gdn_prefill_workspace_size(1, 2432, 16, 32, 128, 128, 1) <= cap
-    assert L.omx_gdn_prefill_workspace_size(1, 2433, 16, 32, 128, 128, 1) > cap
+    assert L.omx_gdn_prefill_workspace_size(1, 2429, 16, 32, 128, 128, 1) <= cap
+    assert L.omx_gdn_prefill_workspace_size(1, 2430, 16, 32, 128, 128, 1) > cap
     rc = L.omx_gdn_prefill_noalloc(16, 16, 16, 16, 16, 16, 16, 16, 1e-6, None, 1, None, None,
                                    None, None, 16, 1, 4096, 16, 32, 128, 128, 4, 64, None)
     assert rc == _lib.EINVAL

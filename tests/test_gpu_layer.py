@@ -251,3 +251,60 @@ def test_layer_c3_full_size_packed_equals_separate():
         assert rel(out_h[:, :, hs].reshape(ref.shape), ref) < BF16_TOL
         assert rel(np_(S[n:n + 1, hs]), S_ref) < STATE_TOL
         assert np.array_equal(np_(conv[n:n + 1])[:, ch], conv_ref)
+
+
+def test_layer_fused_norm_equals_epilogue_kernel():
+    """The layer scan applies the gated norm itself when its grid is one round of the chip
+    (here B=32 at Hk=2, Hv=4, d=128: 256 workgroups of 64 columns) and leaves it to the
+    epilogue kernel otherwise (B=64: 512).  Both form each row's statistic from the same
+    partials in the same pairwise order and apply the same arithmetic, so the first 32
+    sequences' outputs, final states and conv caches agree bit for bit; rows past a
+    sequence's end (T=300 is not a multiple of 64) stay unwritten in both."""
+    say("layer fused norm == epilogue kernel")
+    dims = dict(Hk=2, dk=128, Hv=4, dv=128)
+    d = W.layer_inputs(64, 300, **dims, seed=31)
+    rng = np.random.default_rng(32)
+    S0 = (0.02 * rng.standard_normal((64, 4, 128, 128))).astype(np.float32)
+    t = W.to_device(d)
+    out64, S64, c64 = gpu_prefill(t, dims, None, S0)
+    t32 = {k_: (v_[:32].contiguous() if k_ in ("mixed_qkv", "z", "a", "b") else v_)
+           for k_, v_ in t.items()}
+    out32, S32, c32 = gpu_prefill(t32, dims, None, S0[:32])
+    assert torch.equal(out32, out64[:32])
+    assert torch.equal(S32, S64[:32]) and torch.equal(c32, c64[:32])
+    # and the fused result against the oracle on one sequence
+    d0 = {k_: (v_[5:6] if k_ in ("mixed_qkv", "z", "a", "b") else v_) for k_, v_ in d.items()}
+    ref, S_ref, _ = ref_prefill(d0, dims, None, S0[5:6])
+    assert rel(np_(out32[5:6]), ref) < BF16_TOL
+    assert rel(np_(S32[5:6]), S_ref) < STATE_TOL
+
+
+def test_layer_fused_norm_writes_nothing_past_the_last_token():
+    """The scan that applies the norm itself stores a ragged last chunk through a buffer
+    whose range ends at the sequence's last row.  At B=1, T=981 (C1's heads: 256
+    workgroups, so the norm is fused) the call writes into an output with 64 guard rows
+    after the last token: the guard rows keep their sentinel, and the first T rows equal
+    the Python API's output."""
+    from omegalax_amd import _lib
+    from omegalax_amd.deltanet import _ptr, _stream, _workspace
+    say("layer fused norm: guard rows past the last token")
+    dims = dict(Hk=16, dk=128, Hv=32, dv=128)
+    T, G = 981, 64
+    d = W.layer_inputs(1, T, **dims, seed=41)
+    t = W.to_device(d)
+    ref, _, _ = gpu_prefill(t, dims)
+    Hk, dk, Hv, dv = 16, 128, 32, 128
+    x, z, a, b = (t[k_].contiguous() for k_ in ("mixed_qkv", "z", "a", "b"))
+    conv_w, A_log, dt_bias, norm_w = (t[k_].float().contiguous()
+                                      for k_ in ("conv_w", "A_log", "dt_bias", "norm_w"))
+    out = torch.full((T + G, Hv * dv), -3.0, dtype=torch.bfloat16, device="cuda")
+    sentinel = out[T:].clone()
+    L = _lib.lib()
+    ws_bytes = L.omx_gdn_prefill_workspace_size(1, T, Hk, Hv, dk, dv, 1)
+    ws = _workspace(ws_bytes, out.device)
+    _lib.call("omx_gdn_prefill", _ptr(x), _ptr(z), _ptr(a), _ptr(b), _ptr(conv_w), _ptr(A_log),
+              _ptr(dt_bias), _ptr(norm_w), 1e-6, None, 1, None, None, None, None, _ptr(out), 1, T,
+              Hk, Hv, dk, dv, conv_w.shape[1], 64, _ptr(ws), ws_bytes, _stream(out.device))
+    torch.cuda.synchronize()
+    assert torch.equal(out[T:], sentinel)
+    assert torch.equal(out[:T], ref.reshape(T, Hv * dv))
