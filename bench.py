@@ -210,12 +210,12 @@ def cpu_decode_baseline(batches=(1, 8, 64), budget_s=4.0):
 # scaled by a plain copy kernel's counters), for the shapes they were taken on, with the
 # profiles/ summary that gives the commands and per-kernel figures.
 MEASURED_TRAFFIC = {
-    ("core", 4, 4096, 16, 32, 128): (1_154_299_392, "profiles/prefill_c1.md (core call)"),
+    ("core", 4, 4096, 16, 32, 128): (1_153_999_872, "profiles/prefill_c1.md (core call)"),
     ("core", 1, 65536, 16, 64, 128): (7_707_787_264, "profiles/prefill_c3_c4.md (C4 core call)"),
-    ("decode", 64, 16, 32, 128): (277_278_720, "profiles/decode_step_c2.md (B=64)"),
-    ("decode", 256, 16, 32, 128): (1_107_987_251, "profiles/decode_step_c2.md (B=256)"),
-    # layer step: prep 154.1 + 281.7 MiB, scan 408.6 + 132.0, epilogue 272.0 + 128.0
-    ("prefill", 4, 4096, 16, 32, 128): (1_443_268_915, "profiles/prefill_c1.md (layer kernels)"),
+    ("decode", 64, 16, 32, 128): (277_346_304, "profiles/decode_step_c2.md (B=64)"),
+    ("decode", 256, 16, 32, 128): (1_108_210_688, "profiles/decode_step_c2.md (B=256)"),
+    # layer step: prep 155.3 + 283.3 MiB, scan (with the gated norm) 546.6 + 136.0
+    ("prefill", 4, 4096, 16, 32, 128): (1_175_575_552, "profiles/prefill_c1.md (layer kernels)"),
     ("c3", 32768, 8): (2_954_456_781, "profiles/prefill_c3_c4.md (C3 layer call)"),
     ("bwd", 4, 4096, 16, 32, 128): (7_553_046_835, "profiles/bwd_c1.md (backward call)"),
 }

@@ -133,7 +133,9 @@ int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const v
  * records and normalised q/k as for omx_gdn_chunk_fwd, the conv output of v (dk < 128
  * after padding; with dk = 128 the scan forms the v rows from mixed_qkv itself), and
  * what the gated-norm epilogue reads: the unnormalised bf16 o and the fp32 sums of
- * squares of o per 16 columns of each row.
+ * squares of o per 16 columns of each row (unused when the scan applies the norm
+ * itself), and the small exchange ring of row partials through which the scan's column
+ * blocks share a row's statistic when it does.
  */
 size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t dk,
                                       int64_t dv, int64_t N);
@@ -151,7 +153,9 @@ size_t omx_gdn_prefill_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_t 
  * Hk=16 Hv=32 d=128, about 2,400 tokens per call).  Every call on one GPU uses that
  * GPU's one array: calls that overlap on one GPU (other streams, other threads) race
  * and give undefined results; serialise them.  Nothing in the scratch needs to start
- * at zero: every region is written before it is read within a call.
+ * at zero: every region is written before it is read within a call, and the one region
+ * read before this call writes it (the fused norm's exchange ring) is cleared by the
+ * call's own kernels, not by a memset, so a call may be captured in a HIP graph.
  */
 int omx_gdn_prefill_noalloc(const void* mixed_qkv, const void* z, const void* a, const void* b,
                             const float* conv_w, const float* A_log, const float* dt_bias,
