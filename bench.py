@@ -492,6 +492,34 @@ def bench_ab_proj(steps, warmup):
                          "frac": gbs / PEAK_HBM_GBS}}
 
 
+def bench_qkv_conv(steps, warmup):
+    """in_proj_qkv at C1 (M = 4 x 4096 tokens, D=2048, N = conv_dim = 8192,
+    deltanet.py:234) three ways: the library GEMM (F.linear, hipBLASLt) the layer uses,
+    the library's own GEMM kernel (omx_gdn_qkv_conv_proj, conv = 0), and that kernel with
+    the causal conv + SiLU (deltanet.py:243) in its epilogue (conv = 1): the prototype of
+    the projection-side fusion, measured against the GEMM it would replace."""
+    import torch
+    from omegalax_amd import qkv_conv_projection
+    F = torch.nn.functional
+    g = torch.Generator(device="cuda").manual_seed(1002)
+    B, T, D, N = 4, 4096, 2048, 8192
+    x = torch.randn(B, T, D, generator=g, device="cuda").bfloat16()
+    w = (torch.randn(N, D, generator=g, device="cuda") / D ** 0.5).bfloat16()
+    cw = (0.5 * torch.randn(N, 4, generator=g, device="cuda")).float()
+    _, ms_lib = time_launches(lambda: F.linear(x, w), steps, warmup)
+    _, ms_own = time_launches(lambda: qkv_conv_projection(x, w), steps, warmup)
+    wall, ms_fused = time_launches(lambda: qkv_conv_projection(x, w, cw), steps, warmup)
+    flops = 2.0 * B * T * D * N
+    tf = lambda ms: flops / (ms * 1e-3) / 1e12
+    return {"config": f"in_proj_qkv M={B * T} D={D} N={N}, conv K=4 over sequences of {T}",
+            "library_gemm_ms": ms_lib, "own_gemm_ms": ms_own, "fused_gemm_conv_ms": ms_fused,
+            "ms_per_step": wall / steps * 1e3,
+            "tflops": {"library_gemm": tf(ms_lib), "own_gemm": tf(ms_own),
+                       "fused_gemm_conv": tf(ms_fused)},
+            "roofline": {"bound": "mfma", "achieved": tf(ms_fused), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": tf(ms_fused) / PEAK_BF16_TFLOPS}}
+
+
 def _line(metric, value, unit, steps, warmup, ms, dtype, config, **extra):
     line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps,
             "warmup": warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
@@ -508,7 +536,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=["prefill", "c1", "decode", "c3", "core", "bwd",
-                                           "layer_bwd", "layer_module", "copy", "ab_proj"],
+                                           "layer_bwd", "layer_module", "copy", "ab_proj",
+                                           "qkv_conv"],
                     default="prefill")
     ap.add_argument("--decode-batch", type=int, default=64)
     ap.add_argument("--batch", type=int, default=4, help="core workload: sequences")
@@ -547,6 +576,13 @@ def main():
                     res["roofline"]["achieved"], "GB/s", K, W_, res["ms_per_step"], "bf16",
                     {"workload": res["config"]}, kernel_ms=res["kernel_ms"],
                     two_library_gemms_ms=res["two_library_gemms_ms"], roofline=res["roofline"]),
+              flush=True)
+        return 0
+    if args.workload == "qkv_conv":
+        res = bench_qkv_conv(K, W_)
+        print(_line("in_proj_qkv + conv TFLOP/s (prototype epilogue fusion, config C1)",
+                    res["roofline"]["achieved"], "TFLOP/s", K, W_, res["ms_per_step"], "bf16",
+                    {"workload": res["config"]}, qkv_conv=res, roofline=res["roofline"]),
               flush=True)
         return 0
     if args.workload == "layer_module":
@@ -619,6 +655,7 @@ def main():
     lbwd = bench_layer_bwd(max(K // 2, 5), W_)
     mod = bench_layer_module(K, W_)
     abp = bench_ab_proj(max(K, 20), W_)
+    qkv = bench_qkv_conv(max(K // 2, 5), W_)
     dec = lambda r: {"config": f"C2 B={r['batch']} (state rotated over {r['state_sets']} sets)",
                      "roofline": r["roofline"], "kernel_ms": r["kernel_ms"],
                      "tokens_per_s": r["tokens_per_s"]}
@@ -640,6 +677,7 @@ def main():
                            "tokens_per_s": lbwd["tokens_per_s"]},
         "layer_module": mod,
         "gate_projections": abp,
+        "qkv_conv_fusion": qkv,
     }
     if cpu:
         extra["cpu_baseline"] = pre["cpu_baseline"]

@@ -276,6 +276,26 @@ size_t omx_gdn_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int6
                                           int64_t dk, int64_t dv, int64_t N);
 
 /*
+ * in_proj_qkv (deltanet.py:234, nnx.Linear with bf16 compute: fp32 accumulation, bf16
+ * output) with, for conv = 1, the causal depthwise conv + SiLU of deltanet.py:35-50, 243
+ * applied in the GEMM's epilogue: out = SiLU(conv(bf16(x W^T))) with the layer prefill's
+ * rounding points.  A prototype of the projection-side fusion, kept to measure it against
+ * the library GEMM (bench.py --workload qkv_conv); the layer calls the library GEMM.
+ *
+ *   x      [M, D] bf16 token rows, D a multiple of 64
+ *   w      [N, D] bf16 (the nn.Linear / HF weight layout, [out, in]), N a multiple of 256
+ *   conv_w [N, K] fp32, K = 4 (conv = 1 only)
+ *   out    [M, N] bf16: x W^T (conv = 0) or its conv + SiLU (conv = 1)
+ *
+ * With conv = 1 the rows are M / T sequences of T rows each, and every sequence starts
+ * from zeros (no conv cache: deltanet.py:46).  x, w, out and conv_w 16-byte aligned; x,
+ * W and out each under 2 GiB.
+ */
+int omx_gdn_qkv_conv_proj(const void* x, const void* w, const float* conv_w, void* out,
+                          int64_t M, int64_t D, int64_t N, int64_t T, int64_t K, int conv,
+                          void* stream);
+
+/*
  * The layer's gate projections, b = in_proj_b(x) and a = in_proj_a(x)
  * (deltanet.py:240-241, nnx.Linear with bf16 compute: fp32 accumulation, bf16
  * output), formed in one pass over the hidden rows instead of two GEMMs that each

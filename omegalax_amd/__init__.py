@@ -6,7 +6,7 @@ reference's interface (omegalax/models/qwen3_5/deltanet.py).
 """
 from .deltanet import (  # noqa: F401
     GDNError, chunk_gated_delta_rule, chunk_gated_delta_rule_bwd, gdn_ab_projections,
-    gdn_decode_step, gdn_prefill, gdn_prefill_bwd,
+    gdn_decode_step, gdn_prefill, gdn_prefill_bwd, qkv_conv_projection,
     recurrent_gated_delta_rule_step,
 )
 from .layer import (  # noqa: F401

@@ -51,6 +51,7 @@ SIGNATURES = {
                                  _i64, _i64, _p, _sz, _p]),
     "omx_gdn_prefill_bwd_workspace_size": (_sz, [_i64] * 7),
     "omx_gdn_ab_proj": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "omx_gdn_qkv_conv_proj": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i, _p]),
 }
 
 

@@ -40,7 +40,7 @@ def hipcc() -> str:
 
 # MFMA-heavy sources: keep MFMA accumulators in VGPRs, so the VALU work on them
 # (scaling, packing to bf16) needs no AGPR<->VGPR copies
-MFMA_VGPR_SOURCES = {"gdn_chunk.hip", "gdn_prep.hip"}
+MFMA_VGPR_SOURCES = {"gdn_chunk.hip", "gdn_prep.hip", "gdn_qkv.hip"}
 MFMA_VGPR_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 

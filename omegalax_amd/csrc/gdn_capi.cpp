@@ -270,6 +270,36 @@ int omx_gdn_recurrent_step(const void* q, const void* k, const void* v, int in_d
       omx::launch_decode(p, false, in_dtype == OMX_GDN_BF16, (hipStream_t)stream), fn);
 }
 
+int omx_gdn_qkv_conv_proj(const void* x, const void* w, const float* conv_w, void* out,
+                          int64_t M, int64_t D, int64_t N, int64_t T, int64_t K, int conv,
+                          void* stream) {
+  const char* fn = "omx_gdn_qkv_conv_proj";
+  REQUIRE(M >= 0, "%s: row count %lld is negative", fn, (long long)M);
+  REQUIRE(D > 0 && D % omx::qkv_proj_tile_depth() == 0,
+          "%s: D=%lld must be a positive multiple of %d", fn, (long long)D,
+          omx::qkv_proj_tile_depth());
+  REQUIRE(N > 0 && N % omx::qkv_proj_tile_cols() == 0,
+          "%s: N=%lld must be a positive multiple of %d", fn, (long long)N,
+          omx::qkv_proj_tile_cols());
+  // 32-bit byte offsets inside the kernel: x, W and out each under 2 GiB
+  REQUIRE(M * D < ((int64_t)1 << 30) && N * D < ((int64_t)1 << 30) && M * N < ((int64_t)1 << 30),
+          "%s: x, W or out exceeds 2 GiB (M=%lld D=%lld N=%lld)", fn, (long long)M, (long long)D,
+          (long long)N);
+  REQUIRE(conv == 0 || conv == 1, "%s: conv must be 0 or 1", fn);
+  if (conv) {
+    REQUIRE(K == 4, "%s: the conv epilogue takes K=4 taps (got %lld)", fn, (long long)K);
+    REQUIRE(T >= 1 && M % T == 0, "%s: M=%lld must be a whole number of sequences of T=%lld rows",
+            fn, (long long)M, (long long)T);
+  }
+  if (M == 0) return ok();
+  REQUIRE(x && w && out && (!conv || conv_w), "%s: a required pointer is NULL", fn);
+  REQUIRE(aligned(x, 16) && aligned(w, 16) && aligned(out, 16) && (!conv || aligned(conv_w, 16)),
+          "%s: x, w, out and conv_w must be 16-byte aligned", fn);
+  return launch_status(omx::launch_qkv_proj(x, w, conv_w, out, (long long)M, (int)N, (int)D,
+                                            (long long)T, conv != 0, (hipStream_t)stream),
+                       fn);
+}
+
 int omx_gdn_ab_proj(const void* x, const void* w_a, const void* w_b, void* a, void* b,
                     int64_t M, int64_t D, int64_t Hv, void* stream) {
   const char* fn = "omx_gdn_ab_proj";

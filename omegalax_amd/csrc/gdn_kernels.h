@@ -245,6 +245,14 @@ hipError_t launch_decode(const DecodeParams& p, bool layer, bool in_bf16, hipStr
 // The gate projections a = x W_a^T, b = x W_b^T (bf16, fp32 accumulation) in one pass
 // over x [M, D] (gdn_proj.hip); D % 8 == 0, 1 <= Hv <= ab_proj_max_heads().
 int ab_proj_max_heads();
+// x W^T for x [M, D], W [N, D] bf16 (bf16 out), and with conv the causal conv + SiLU of
+// that product over sequences of T rows in the epilogue (gdn_qkv.hip); N a multiple of
+// qkv_proj_tile_cols(), D of qkv_proj_tile_depth().
+hipError_t launch_qkv_proj(const void* x, const void* w, const float* conv_w, void* out,
+                           long long M, int N, int D, long long T, bool conv, hipStream_t stream);
+int qkv_proj_tile_cols();
+int qkv_proj_tile_depth();
+
 hipError_t launch_ab_proj(const void* x, const void* wa, const void* wb, void* a, void* b,
                           long long M, int D, int Hv, hipStream_t stream);
 

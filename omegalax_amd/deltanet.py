@@ -444,6 +444,38 @@ def _ab_proj_fwd(x, w_a, w_b):
     return a.reshape(*lead, Hv), b.reshape(*lead, Hv)
 
 
+def qkv_conv_projection(x, w_qkv, conv_w=None, *, seq_len=None):
+    """in_proj_qkv (deltanet.py:234) through the library's own GEMM kernel, and with
+    ``conv_w`` [N, 4] the causal conv + SiLU (deltanet.py:35-50, 243) in its epilogue,
+    over sequences of ``seq_len`` consecutive rows that start from zeros (no conv
+    cache).  x [..., D] bf16, w_qkv [N, D] bf16; returns [..., N] bf16.  A forward-only
+    prototype of the projection-side fusion (omx_gdn_qkv_conv_proj), measured against
+    the library GEMM by ``bench.py --workload qkv_conv``; the layer itself uses F.linear.
+    """
+    lead, D = x.shape[:-1], x.shape[-1]
+    x2 = x.reshape(-1, D).contiguous()
+    w_qkv = w_qkv.contiguous()
+    if x2.dtype != torch.bfloat16 or w_qkv.dtype != torch.bfloat16:
+        raise ValueError("qkv_conv_projection: x and w_qkv must be bf16")
+    N = w_qkv.shape[0]
+    if w_qkv.shape[1] != D:
+        raise ValueError(f"w_qkv must be [N, {D}] (got {tuple(w_qkv.shape)})")
+    M = x2.shape[0]
+    conv = conv_w is not None
+    if conv:
+        conv_w = _f32(conv_w)
+        if tuple(conv_w.shape) != (N, 4):
+            raise ValueError(f"conv_w must be [{N}, 4] (got {tuple(conv_w.shape)})")
+        if seq_len is None:
+            seq_len = x.shape[-2] if x.dim() >= 2 else M
+    x2, w_qkv = (t if t.data_ptr() % 16 == 0 else t.clone() for t in (x2, w_qkv))
+    dev = _dev(x2, w_qkv, conv_w)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _lib.call("omx_gdn_qkv_conv_proj", _ptr(x2), _ptr(w_qkv), _ptr(conv_w), _ptr(out), M, D, N,
+              int(seq_len or M), 4, int(conv), _stream(dev))
+    return out.reshape(*lead, N)
+
+
 class _ABProj(torch.autograd.Function):
     """Autograd node of the gate projections: forward omx_gdn_ab_proj; backward the
     linear maps' adjoints (dx = da W_a + db W_b, dW_a = da^T x, dW_b = db^T x) as bf16

@@ -311,3 +311,24 @@ def test_ab_proj_rejects_bad_shapes_on_the_host():
     assert "NULL" in L.omx_gdn_last_error().decode()
     assert L.omx_gdn_ab_proj(24, 16, 16, 16, 16, 4, 64, 32, None) == _lib.EINVAL
     assert "aligned" in L.omx_gdn_last_error().decode()
+
+
+def test_qkv_conv_proj_rejects_bad_shapes_on_the_host():
+    L = _lib.lib()
+    f = L.omx_gdn_qkv_conv_proj
+    # (x, w, conv_w, out, M, D, N, T, K, conv, stream)
+    assert f(16, 16, 16, 16, 8, 100, 256, 8, 4, 0, None) == _lib.EINVAL  # D not a multiple of 128
+    assert "multiple of 128" in L.omx_gdn_last_error().decode()
+    assert f(16, 16, 16, 16, 8, 128, 300, 8, 4, 0, None) == _lib.EINVAL  # N not a multiple of 256
+    assert "multiple of 256" in L.omx_gdn_last_error().decode()
+    assert f(16, 16, 16, 16, 10, 128, 256, 4, 4, 1, None) == _lib.EINVAL  # M not whole sequences
+    assert "sequences" in L.omx_gdn_last_error().decode()
+    assert f(16, 16, 16, 16, 8, 128, 256, 8, 3, 1, None) == _lib.EINVAL  # K != 4
+    assert f(16, 16, 16, 16, 8, 128, 256, 8, 4, 2, None) == _lib.EINVAL
+    assert f(16, 16, 16, 16, 1 << 20, 2048, 256, 1, 4, 0, None) == _lib.EINVAL  # x over 2 GiB
+    assert f(None, None, None, None, 0, 128, 256, 1, 4, 1, None) == _lib.OK  # empty call
+    assert f(16, None, 16, 16, 8, 128, 256, 8, 4, 1, None) == _lib.EINVAL
+    assert "NULL" in L.omx_gdn_last_error().decode()
+    assert f(16, 16, None, 16, 8, 128, 256, 8, 4, 1, None) == _lib.EINVAL  # conv needs conv_w
+    assert f(24, 16, 16, 16, 8, 128, 256, 8, 4, 1, None) == _lib.EINVAL
+    assert "aligned" in L.omx_gdn_last_error().decode()
