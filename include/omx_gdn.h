@@ -119,6 +119,12 @@ size_t omx_gdn_chunk_fwd_workspace_size(int64_t B, int64_t T, int64_t Hk, int64_
  *   conv_state_out [N, conv_dim, K-1] bf16 or NULL: the last K-1 raw inputs of each
  *                  sequence (the decode cache after this prefill)
  *   out           [B, T, Hv*dv] bf16
+ *
+ * When the scan's grid fits the GPU in one round (at most one workgroup per CU, e.g.
+ * B=4 T=4096 at Hv=32 d=128), its workgroups apply the gated norm themselves and
+ * exchange each row's partial sums while they run, so they must run together: work on
+ * other streams that holds CUs for more than about a second during the call leaves the
+ * affected output rows NaN (a bounded wait that ran out) rather than a wrong value.
  */
 int omx_gdn_prefill(const void* mixed_qkv, const void* z, const void* a, const void* b,
                     const float* conv_w, const float* A_log, const float* dt_bias,

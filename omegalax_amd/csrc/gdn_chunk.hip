@@ -939,7 +939,10 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
           for (int w = 1; w < NBX; w <<= 1)
 #pragma unroll
             for (int s = 0; s + w < NBX; s += 2 * w) t[s] += t[s + w];
-          sRN[c & 1][l] = rsqrtf(__builtin_fmaf(t[0], p.inv_dv, p.eps));  // as the epilogue kernel
+          // as the epilogue kernel; a wait that gave up (a partner block never ran, which a
+          // grid the chip holds at once rules out unless other work kept CUs for a second)
+          // leaves NaN rows rather than rows normalised by partial sums
+          sRN[c & 1][l] = gave_up ? __builtin_nanf("") : rsqrtf(__builtin_fmaf(t[0], p.inv_dv, p.eps));
         }
       };
       auto load = [&](int j, lds_bf16* nK, lds_bf16* nQ, lds_bf16* nV, lds_u8* nRec) {
