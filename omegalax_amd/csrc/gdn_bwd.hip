@@ -352,14 +352,23 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     for (int v = 0; v < 4; ++v)
       dS[t][v] = p.dht ? p.dht[st_off + (size_t)(16 * t + 4 * lq + v) * DV] : 0.f;
 
-  // Per-thread register prefetch of one chunk's inputs: K and Q rows, the chunk's dO
-  // columns, X and P, and one gate value; stored into LDS at the top of the chunk.
+  // Per-thread register prefetch of a chunk's inputs: K and Q rows, the chunk's dO
+  // columns, X and P, and one gate value; stored into LDS at the top of the chunk.  Two
+  // register sets, loaded two chunks ahead: a chunk's rows have two chunk steps to land
+  // (with one the staging waited for them), and the kernel, one wavefront per SIMD, has
+  // the registers.
   constexpr int NKQ = 2 * C * (DK / 4) / NT;
   static_assert(NKQ * NT == 2 * C * (DK / 4), "item split");
-  typename Vec4<KT>::type pkq[NKQ];
-  float4 pdo[C * 16 / NT], pxp[2 * C * 16 / NT];
-  float pgate;
-  auto load_chunk = [&](int jj) {
+  struct Pf {
+    typename Vec4<KT>::type pkq[NKQ];
+    float4 pdo[C * 16 / NT], pxp[2 * C * 16 / NT];
+    float pgate;
+  };
+  Pf pfa, pfb;
+  // chunk jj into f; every call issues the same loads (a chunk before the sequence's first
+  // reloads chunk 0, unused), so the loop's waits stay exact counts
+  auto load_chunk = [&](int jj, Pf& f) {
+    jj = jj < 0 ? 0 : jj;
     const long long tt = s0 + (long long)jj * C;
     const int nv = (int)((s1 - tt) < C ? (s1 - tt) : C);
     const int sl = cbase + jj < p.n_rec ? cbase + jj : p.n_rec - 1;
@@ -376,52 +385,56 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       const int rem = tid + m * NT - which * (C * DK / 4);
       const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
       const long long ld = which ? p.qs_ld : p.ks_ld;
-      pkq[m] = bload4(which ? qr : kr, (unsigned)((row * ld + c4) * (long long)sizeof(KT)), (const KT*)nullptr);
+      f.pkq[m] = bload4(which ? qr : kr, (unsigned)((row * ld + c4) * (long long)sizeof(KT)), (const KT*)nullptr);
     }
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int row = it >> 4, c4 = 4 * (it & 15);
-      pdo[m] = bload4(dr, (unsigned)(4 * (row * rs + c4)), (const float*)nullptr);
+      f.pdo[m] = bload4(dr, (unsigned)(4 * (row * rs + c4)), (const float*)nullptr);
     }
     const float* xb = p.xlpg + ((size_t)sl * p.Hv + h) * kXlpgFloats;
 #pragma unroll
     for (int m = 0; m < 2 * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
-      pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15));
+      f.pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15));
     }
-    pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
+    f.pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
   };
-  auto store_chunk = [&]() {
+  auto store_chunk = [&](const Pf& f) {
 #pragma unroll
     for (int m = 0; m < NKQ; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
       const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
-      store4((which ? sQ : sK) + row * LDK + c4, pkq[m]);
+      store4((which ? sQ : sK) + row * LDK + c4, f.pkq[m]);
     }
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
       const int it = tid + m * NT;
-      put_row4(sDOh, sDOl, (it >> 4) * LDB + 4 * (it & 15), f32x4{pdo[m].x, pdo[m].y, pdo[m].z, pdo[m].w});
+      put_row4(sDOh, sDOl, (it >> 4) * LDB + 4 * (it & 15), f32x4{f.pdo[m].x, f.pdo[m].y, f.pdo[m].z, f.pdo[m].w});
     }
 #pragma unroll
     for (int m = 0; m < 2 * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
-      const f32x4 v = f32x4{pxp[m].x, pxp[m].y, pxp[m].z, pxp[m].w};
+      const f32x4 v = f32x4{f.pxp[m].x, f.pxp[m].y, f.pxp[m].z, f.pxp[m].w};
       if (which) put_row4(sPh, sPl, (rem >> 4) * LDB + 4 * (rem & 15), v);
       else put_row4(sXh, sXl, (rem >> 4) * LDB + 4 * (rem & 15), v);
     }
-    sGate[tid] = pgate;
+    sGate[tid] = f.pgate;
   };
-  if (nchunks > 0) load_chunk(nchunks - 1);
+  if (nchunks > 0) {
+    load_chunk(nchunks - 1, pfa);
+    load_chunk(nchunks - 2, pfb);
+  }
   // the prologue's loads (some under the uniform p.dht test) have landed: the loop's waits
   // then count only the loop's own memory operations
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
-  for (int j = nchunks - 1; j >= 0; --j) {
+  // chunk j from the registers of cur, which then receive chunk jn
+  auto step = [&](const int j, Pf& cur, const int jn) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
     const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
@@ -429,8 +442,8 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     // kernels and the prefetched rows are per-thread registers, so neither the prefetch
     // nor the stores are waited for at a barrier.
     lds_barrier();  // the previous chunk's readers are done
-    store_chunk();
-    if (j > 0) load_chunk(j - 1);  // lands while this chunk computes
+    store_chunk(cur);
+    load_chunk(jn, cur);  // lands during this chunk and the next
     lds_barrier();
     const float* sEG = sGate + kGateEG * C;
     const float* sEGS = sGate + kGateEGS * C;
@@ -531,7 +544,15 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       }
       dS[t] = acc;
     }
+  };
+  // chunks n-1, n-3, ... from pfa and n-2, n-4, ... from pfb, each set reloaded with the
+  // chunk two below the one it held
+  int j = nchunks - 1;
+  for (; j >= 1; j -= 2) {
+    step(j, pfa, j - 2);
+    step(j - 1, pfb, j - 3);
   }
+  if (j == 0) step(0, pfa, -2);
   if (p.dh0) {
 #pragma unroll
     for (int t = 0; t < DK / 16; ++t)
