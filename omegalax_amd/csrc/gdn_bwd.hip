@@ -217,36 +217,43 @@ __device__ __forceinline__ void load8v(const float* p, float* x) {
   x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
 }
 
-// Row sums of a C-layout tile (rows 16 bi + 4q + v, summed over its 16 columns) added
-// into arr[row] (lanes r == 0 write; one lane per row); column sums likewise.
+// Row sums of a C-layout tile (lane (q, r) holds rows 16 bi + 4q + v, v = 0..3, of
+// column r) added into arr[row], without LDS traffic: a reduce-scatter over the 16 lanes of
+// each row group with DPP moves.  Lanes r and r ^ 8 split the four rows between them
+// (row_ror:8), lanes r and its mirror in the 8-lane half split the pair (row_half_mirror),
+// then each quad sums (quad_perm); lane r with r % 4 == 0 ends with row 16 bi + 4q + r / 4.
 __device__ __forceinline__ void add_rows(float* arr, int bi, f32x4 x) {
-  const int l = lane_id();
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    float s = x[v];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    s += __shfl_xor(s, 8);
-    x[v] = s;
-  }
-  if ((l & 15) == 0) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) arr[16 * bi + 4 * (l >> 4) + v] += x[v];
-  }
+  const int l = lane_id(), r = l & 15;
+  const bool up8 = (r & 8) != 0, up4 = (r & 4) != 0;
+  const float k0 = up8 ? x[2] : x[0], k1 = up8 ? x[3] : x[1];
+  const float g0 = up8 ? x[0] : x[2], g1 = up8 ? x[1] : x[3];
+  const float a0 = k0 + dpp_f<0x128>(g0), a1 = k1 + dpp_f<0x128>(g1);
+  const float kb = up4 ? a1 : a0, gb = up4 ? a0 : a1;
+  float s = kb + dpp_f<0x141>(gb);
+  s += dpp_f<0x4E>(s);
+  s += dpp_f<0xB1>(s);
+  if ((r & 3) == 0) arr[16 * bi + 4 * (l >> 4) + (r >> 2)] += s;
 }
+// Column sums of a C-layout tile (column 16 bj + r, summed over its 16 rows) added into
+// arr[col]: the lane's four rows, then across the four row groups with the 16- and 32-lane
+// swaps (lanes of row group 0 write).
 __device__ __forceinline__ void add_cols(float* arr, int bj, f32x4 x) {
   const int l = lane_id();
   float s = x[0] + x[1] + x[2] + x[3];
-  s += __shfl_xor(s, 16);
-  s += __shfl_xor(s, 32);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  s = __uint_as_float(b[0]) + __uint_as_float(b[1]);
   if ((l >> 4) == 0) arr[16 * bj + (l & 15)] += s;
 }
 
+// Sum over the 64 lanes, left in every lane (DPP within each row, then the row swaps).
 __device__ __forceinline__ float wave_sum(float s) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) s += __shfl_xor(s, o);
-  return s;
+  s = group_sum_dpp<16>(s);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 __device__ __forceinline__ int rec_mode(bool f32) { return f32 ? MODE_F32 : MODE_BF16; }
