@@ -719,16 +719,20 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) dp[j] = dxa[j] = zero4();
   const int bi = wave & 3, half = wave >> 2;  // row block and column-block pair
-  // P and Lg at this wavefront's tiles (bi, 2 half + jj), read elementwise later
+  // P and Lg at this wavefront's tiles (bi, 2 half + jj), used elementwise after the
+  // products over dv.  fp32 inputs read them from the preparation kernel's matrices; bf16
+  // inputs form them after the products over dv from the staged K and Q rows.
   float pP[2][4], pLg[2][4];
+  if constexpr (F32) {
 #pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
+    for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int o = (16 * bi + 4 * lq + v) * C + 16 * (2 * half + jj) + lr;
-      pP[jj][v] = xb[kXlpgP + o];
-      pLg[jj][v] = xb[kXlpgLg + o];
-    }
+      for (int v = 0; v < 4; ++v) {
+        const int o = (16 * bi + 4 * lq + v) * C + 16 * (2 * half + jj) + lr;
+        pP[jj][v] = xb[kXlpgP + o];
+        pLg[jj][v] = xb[kXlpgLg + o];
+      }
+  }
   // ---------------------------------------------------------------- stage
   // K and Q rows in 16-byte items, every load issued (with the first step's) before any
   // store, so the workgroup waits for one memory round trip rather than one per item
@@ -833,6 +837,32 @@ __global__ __launch_bounds__(CNT) void cgrad_kernel(BwdParams p) {
   for (int m = 0; m < C * 16 / CNT; ++m) {
     const int it = tid + m * CNT;
     put_row4(sXh, sXl, (it >> 4) * LDB + 4 * (it & 15), f4(pf_x[m]));
+  }
+  if constexpr (!F32) {
+    // P = lower(scale Q K^T * Gamma) and Lg = strict_lower(K K^T * Gamma) at this
+    // wavefront's tiles, with the preparation kernel's arithmetic (the exact bf16 products
+    // summed by the same MFMA over the same dk blocks in the same order, then
+    // scale * acc * 2^{min(G_i log2 e - G_m log2 e, 0)} * mask), so they are the values it
+    // left in its matrices, without storing and reloading 32 KiB per (chunk, value head)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int bj = 2 * half + jj;
+      f32x4 kk = zero4(), qk = zero4();
+#pragma unroll
+      for (int s2 = 0; s2 < DK / 32; ++s2) {
+        const u32x4 km = frag_bf16((const bf16_t*)sK, LDK, 16 * bj, 32 * s2);
+        kk = mma16(frag_bf16((const bf16_t*)sK, LDK, 16 * bi, 32 * s2), km, kk);
+        qk = mma16(frag_bf16((const bf16_t*)sQ, LDK, 16 * bi, 32 * s2), km, qk);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * bi + 4 * lq + v, col = 16 * bj + lr;
+        const float e = __builtin_amdgcn_exp2f(
+            fminf(sG[row] * 1.4426950408889634f - sG[col] * 1.4426950408889634f, 0.f));
+        pLg[jj][v] = kk[v] * e * (float)(row > col);
+        pP[jj][v] = scale * qk[v] * e * (float)(row >= col);
+      }
+    }
   }
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {

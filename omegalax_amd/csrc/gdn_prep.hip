@@ -434,7 +434,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
           const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2);
           const int bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
           if (mat == 0) put_f32_tile(xb + kXlpgX, bj, bi, zero4());
-          else put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
+          else if (IS || mat != 1) put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
         }
       }
 
@@ -523,7 +523,8 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
               lg[v] = acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i > m);
               val[v] = bt * lg[v];
             }
-            put_f32_tile(xb + kXlpgLg, bi, bj, lg);
+            // (bf16 inputs: the gradient kernel forms its Lg tiles from K itself)
+            if constexpr (IS) put_f32_tile(xb + kXlpgLg, bi, bj, lg);
           } else {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
