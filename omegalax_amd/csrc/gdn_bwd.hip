@@ -307,6 +307,18 @@ __device__ __forceinline__ Op op_pair(const bf16_t* h, const bf16_t* lo, int ld,
   o.l = u32x4{c[0], c[1], d[0], d[1]};
   return o;
 }
+// op_tr in the block-pair contraction order (kslot<true>): entries k0 + 4q .. +3 and
+// k0 + 16 + 4q .. +3 down storage column c0 + r
+__device__ __forceinline__ Op op_tr_pair(const bf16_t* h, const bf16_t* lo, int ld, int c0, int k0) {
+  const int l = lane_id(), q = l >> 4, s = l & 15;
+  const int off = (k0 + 4 * q + (s >> 2)) * ld + c0 + 4 * (s & 3);
+  const u32x2 a = ds_read_tr(h + off), b = ds_read_tr(h + off + 16 * ld);
+  const u32x2 c = ds_read_tr(lo + off), d = ds_read_tr(lo + off + 16 * ld);
+  Op o;
+  o.h = u32x4{a[0], a[1], b[0], b[1]};
+  o.l = u32x4{c[0], c[1], d[0], d[1]};
+  return o;
+}
 // the fp32 values (hi + lo) of an operand's 8 slots
 __device__ __forceinline__ void op_values(const Op& o, float* x) {
 #pragma unroll
@@ -328,7 +340,10 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
   // dO (this block's 64 columns), X^T and P, row-major, as bf16 hi / lo planes
   __shared__ __align__(16) bf16_t sDO[2 * C * LDB];
   __shared__ __align__(16) bf16_t sX[2 * C * LDB];
-  __shared__ __align__(16) bf16_t sP[2 * C * LDB];
+  // bf16 inputs form the P operands in registers (PREC) from the staged K and Q rows and G
+  constexpr bool PREC = !F32;
+  __shared__ __align__(16) bf16_t sP[PREC ? 8 : 2 * C * LDB];
+  __shared__ float sGl[PREC ? C : 1];
   __shared__ __align__(16) float sGate[4 * C];
   bf16_t* const sDOh = sDO;
   bf16_t* const sDOl = sDO + C * LDB;
@@ -368,8 +383,8 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
   static_assert(NKQ * NT == 2 * C * (DK / 4), "item split");
   struct Pf {
     typename Vec4<KT>::type pkq[NKQ];
-    float4 pdo[C * 16 / NT], pxp[2 * C * 16 / NT];
-    float pgate;
+    float4 pdo[C * 16 / NT], pxp[(PREC ? 1 : 2) * C * 16 / NT];
+    float pgate, pg;
   };
   Pf pfa, pfb;
   // chunk jj into f; every call issues the same loads (a chunk before the sequence's first
@@ -402,11 +417,12 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     }
     const float* xb = p.xlpg + ((size_t)sl * p.Hv + h) * kXlpgFloats;
 #pragma unroll
-    for (int m = 0; m < 2 * C * 16 / NT; ++m) {
+    for (int m = 0; m < (PREC ? 1 : 2) * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
       f.pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15));
     }
+    if constexpr (PREC) f.pg = xb[kXlpgG + (tid & (C - 1))];
     f.pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
   };
   auto store_chunk = [&](const Pf& f) {
@@ -423,13 +439,15 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       put_row4(sDOh, sDOl, (it >> 4) * LDB + 4 * (it & 15), f32x4{f.pdo[m].x, f.pdo[m].y, f.pdo[m].z, f.pdo[m].w});
     }
 #pragma unroll
-    for (int m = 0; m < 2 * C * 16 / NT; ++m) {
+    for (int m = 0; m < (PREC ? 1 : 2) * C * 16 / NT; ++m) {
       const int it = tid + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
       const f32x4 v = f32x4{f.pxp[m].x, f.pxp[m].y, f.pxp[m].z, f.pxp[m].w};
       if (which) put_row4(sPh, sPl, (rem >> 4) * LDB + 4 * (rem & 15), v);
       else put_row4(sXh, sXl, (rem >> 4) * LDB + 4 * (rem & 15), v);
     }
+    if constexpr (PREC)
+      if (tid < C) sGl[tid] = f.pg;
     sGate[tid] = f.pgate;
   };
   if (nchunks > 0) {
@@ -480,14 +498,43 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       kds[i] = acc;
     }
     // ---------------------------------------------------------------- dV_new = P^T dO + e^{G_last-G} K dS
+    // (PREC) tile (mb, nb) of P = lower(scale Q K^T * Gamma) in the C layout, with the
+    // preparation kernel's arithmetic: scale * acc * 2^{min(G_m log2 e - G_n log2 e, 0)} * mask
+    auto ptile = [&](int mb, int nb) {
+      f32x4 acc = zero4();
+      if constexpr (PREC) {
+#pragma unroll
+        for (int s2 = 0; s2 < DK / 32; ++s2)
+          acc = mma16(frag_bf16((const bf16_t*)sQ, LDK, 16 * mb, 32 * s2),
+                      frag_bf16((const bf16_t*)sK, LDK, 16 * nb, 32 * s2), acc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 16 * mb + 4 * lq + v, n = 16 * nb + lr;
+          acc[v] = p.scale * acc[v] *
+                   __builtin_amdgcn_exp2f(fminf(sGl[m] * 1.4426950408889634f - sGl[n] * 1.4426950408889634f, 0.f)) *
+                   (float)(m >= n);
+        }
+      }
+      return acc;
+    };
     f32x4 dvn[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int p2 = i / 2; p2 < 2; ++p2)  // P^T is upper triangular
-        acc = mm3<true, true>(acc, op_tr(sPh, sPl, LDB, 16 * i, 32 * p2),
-                              op_tr(sDOh, sDOl, LDB, c, 32 * p2));
+      for (int p2 = i / 2; p2 < 2; ++p2) {  // P^T is upper triangular
+        if constexpr (PREC) {
+          // P^T rows 16i .. +15 over tokens 32 p2 .. +31 from the P tiles (2 p2, i) and
+          // (2 p2 + 1, i) side by side (block-pair order; (2 p2, i) is above the diagonal,
+          // zero, when 2 p2 < i), against dO read in the same order
+          const f32x4 t0 = 2 * p2 >= i ? ptile(2 * p2, i) : zero4();
+          acc = mm3<true, true>(acc, join_op(t0, ptile(2 * p2 + 1, i)),
+                                op_tr_pair(sDOh, sDOl, LDB, c, 32 * p2));
+        } else {
+          acc = mm3<true, true>(acc, op_tr(sPh, sPl, LDB, 16 * i, 32 * p2),
+                                op_tr(sDOh, sDOl, LDB, c, 32 * p2));
+        }
+      }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * i + 4 * lq + v;

@@ -45,8 +45,8 @@ constexpr int kGateEG = 0, kGateEGS = 1, kGateEL = 2, kGateBeta = 3;
 
 // backward extras per (chunk slot, value head), fp32 row-major 64x64 matrices:
 // X^T (X = (I + L)^-1, upper triangular as stored), Lg = strict_lower(K K^T * Gamma)
-// (L = diag(beta) Lg; written for fp32 inputs only: with bf16 inputs the gradient kernel
-// forms the Lg tiles it needs from K), P, then G
+// (L = diag(beta) Lg), P, then G.  Lg and P are written for fp32 inputs only: with bf16
+// inputs the backward kernels form the Lg and P tiles they need from K, Q and G
 constexpr int kXlpgMat = kC * kC;
 constexpr int kXlpgX = 0, kXlpgLg = kXlpgMat, kXlpgP = 2 * kXlpgMat, kXlpgG = 3 * kXlpgMat;
 constexpr int kXlpgFloats = 3 * kXlpgMat + kC;

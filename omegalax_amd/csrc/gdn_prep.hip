@@ -428,13 +428,13 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
       const auto rec = buf_rsrc(p.rec + ((size_t)ci * p.Hv + h) * rec_stride, (unsigned)rec_stride);
       float* xb = BWD ? p.xlpg + ((size_t)ci * p.Hv + h) * kXlpgFloats : nullptr;
       if constexpr (BWD) {
-        // the lower tiles of X^T and the upper tiles of Lg and P are zero
-        for (int z = wave; z < 18; z += 4) {
+        // the lower tiles of X^T and (fp32 inputs) the upper tiles of Lg and P are zero
+        for (int z = wave; z < (IS ? 18 : 6); z += 4) {
           const int mat = z / 6, u = z % 6;
           const int bi = u < 3 ? 0 : (u < 5 ? 1 : 2);
           const int bj = u < 3 ? u + 1 : (u < 5 ? u - 1 : 3);
           if (mat == 0) put_f32_tile(xb + kXlpgX, bj, bi, zero4());
-          else if (IS || mat != 1) put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
+          else if (IS) put_f32_tile(xb + mat * kXlpgMat, bi, bj, zero4());
         }
       }
 
@@ -604,7 +604,8 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
             val[v] = sc * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i >= m);
           }
           put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
-          if constexpr (BWD) put_f32_tile(xb + kXlpgP, bi, bj, val);
+          // (bf16 inputs: the backward kernels form their P operands from K and Q)
+          if constexpr (BWD && IS) put_f32_tile(xb + kXlpgP, bi, bj, val);
           // (backward) P's lo parts only where the scan forms o: the layer backward
           if constexpr (IS || BWD)
             if (IS || p.o) put_tile(rec, rec_p_off(bi, bj) + (kRecPL - kRecP), pack_lo4(val));
