@@ -378,7 +378,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeParams p) {
 // Shapes: the layer path with K = 4, gqa 1 or 2, 2 dk + gqa dv <= 512 channels, dv 64 or
 // 128 and dk a multiple of the row groups.
 template <int DK, int DV, int GQA, bool NT>
-__global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeParams p) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void decode_stream_kernel(DecodeParams p) {
   constexpr int WC = DV / 4;                           // state columns of one wavefront
   constexpr int CGS = WC / 4;                          // column groups of 4 per wavefront
   constexpr int RGW = 64 / CGS, R = DK / RGW;          // row groups, rows per lane
@@ -404,6 +405,9 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeParams p)
 
   __shared__ __align__(16) float s_q[2][DK], s_k[2][DK], s_v[2][GQA][DV];
   __shared__ float s_ss[2][4];
+  // normalised k and scaled q of the current item, one copy per wavefront, in the order its
+  // lanes read them: row rg + RGW r at rg R + r (a lane's rows are contiguous)
+  __shared__ __align__(16) float s_kn[4][DK], s_qn[4][DK];
 
   // item i of this workgroup (i >= my_items: a stand-in whose accesses are all no-ops)
   struct Item {
@@ -533,7 +537,13 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeParams p)
     rq = rsqrtf(wave_sum(ssq) + 1e-6f);
     rk = rsqrtf(wave_sum(ssk) + 1e-6f);
     float d = 0.f;
-    for (int j = lane; j < DK; j += 64) d += round_bf(s_q[ib][j] * rq) * scale * round_bf(s_k[ib][j] * rk);
+    for (int j = lane; j < DK; j += 64) {
+      const float qn = round_bf(s_q[ib][j] * rq) * scale, kn = round_bf(s_k[ib][j] * rk);
+      const int pj = (j % RGW) * R + j / RGW;
+      s_qn[wave][pj] = qn;
+      s_kn[wave][pj] = kn;
+      d += qn * kn;
+    }
     qk = wave_sum(d);
   };
 
@@ -553,9 +563,9 @@ __global__ __launch_bounds__(kThreads) void decode_stream_kernel(DecodeParams p)
     const Item t = item(i);
     const int ib = i & 1;
     const float alpha = alpha_i[hh], beta = beta_i[hh];
-    // normalised k and scaled q of row rg + RGW r, formed from LDS where used
-    auto k_row = [&](int r) { return round_bf(s_k[ib][rg + RGW * r] * rk); };
-    auto q_row = [&](int r) { return round_bf(s_q[ib][rg + RGW * r] * rq) * scale; };
+    // normalised k and scaled q of row rg + RGW r, read from this wavefront's copy where used
+    auto k_row = [&](int r) { return s_kn[wave][rg * R + r]; };
+    auto q_row = [&](int r) { return s_qn[wave][rg * R + r]; };
     float kv[4] = {0.f, 0.f, 0.f, 0.f}, qs[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < R; ++r) {
