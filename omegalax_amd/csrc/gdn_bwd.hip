@@ -330,30 +330,46 @@ __device__ __forceinline__ void op_values(const Op& o, float* x) {
 
 // ============================================================================ reverse scan
 
+// With bf16 inputs (LDR) four loader wavefronts beside the four compute wavefronts move
+// each chunk's rows into one of two LDS buffers while the compute wavefronts work on the
+// other, with one barrier per chunk; the compute wavefronts then issue no loads at all.
+// fp32 K and Q rows leave no room for a second buffer, so with fp32 inputs the compute
+// wavefronts stage the rows themselves from a register prefetch two chunks deep.
 template <int DK, bool F32>
-__global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
+__global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
   using KT = typename std::conditional<F32, float, bf16_t>::type;
   constexpr int LDK = DK + (F32 ? 4 : 8);
   constexpr int LDB = C + 8;  // stride (bf16) of a split plane
-  __shared__ __align__(16) KT sK[C * LDK];
-  __shared__ __align__(16) KT sQ[C * LDK];
-  // dO (this block's 64 columns), X^T and P, row-major, as bf16 hi / lo planes
-  __shared__ __align__(16) bf16_t sDO[2 * C * LDB];
-  __shared__ __align__(16) bf16_t sX[2 * C * LDB];
+  constexpr bool LDR = !F32;
   // bf16 inputs form the P operands in registers (PREC) from the staged K and Q rows and G
   constexpr bool PREC = !F32;
+  // Buffer 0 and (LDR) buffer 1 are separate objects, so the compiler can tell the
+  // loaders' writes to one from the compute wavefronts' reads of the other.
+  __shared__ __align__(16) KT sK0[C * LDK], sK1[LDR ? C * LDK : 8];
+  __shared__ __align__(16) KT sQ0[C * LDK], sQ1[LDR ? C * LDK : 8];
+  // dO (this block's 64 columns), X^T and (fp32 inputs) P, row-major, as bf16 hi / lo planes
+  __shared__ __align__(16) bf16_t sDO0[2 * C * LDB], sDO1[LDR ? 2 * C * LDB : 8];
+  __shared__ __align__(16) bf16_t sX0[2 * C * LDB], sX1[LDR ? 2 * C * LDB : 8];
   __shared__ __align__(16) bf16_t sP[PREC ? 8 : 2 * C * LDB];
-  __shared__ float sGl[PREC ? C : 1];
-  __shared__ __align__(16) float sGate[4 * C];
-  bf16_t* const sDOh = sDO;
-  bf16_t* const sDOl = sDO + C * LDB;
-  bf16_t* const sXh = sX;
-  bf16_t* const sXl = sX + C * LDB;
+  __shared__ float sGl0[PREC ? C : 1], sGl1[LDR ? C : 1];
+  __shared__ __align__(16) float sGate0[4 * C], sGate1[LDR ? 4 * C : 4];
+  struct Buf {
+    KT* K;
+    KT* Q;
+    bf16_t* DO;
+    bf16_t* X;
+    float* Gl;
+    float* Gate;
+  };
+  const Buf B0{sK0, sQ0, sDO0, sX0, sGl0, sGate0};
+  const Buf B1{sK1, sQ1, sDO1, sX1, sGl1, sGate1};
   bf16_t* const sPh = sP;
   bf16_t* const sPl = sP + C * LDB;
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool loader = LDR && wave >= NT / 64;  // (LDR) waves 4-7 stage rows only
+  const int st = loader ? tid - NT : tid;       // index among the threads that stage rows
   const ScanItem item = scan_item(p.seq_order, p.N, p.Hk, p.Hv, p.nb);
   const int blk = item.blk, h = item.h, n = item.n;
   const int gqa = p.Hv / p.Hk, hk = h / gqa;
@@ -368,17 +384,27 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
   // dS[t][v] = dS[16t + 4lq + v][col0 + c + lr]: gradient of the state leaving the chunk
   f32x4 dS[DK / 16];
   const size_t st_off = ((size_t)n * p.Hv + h) * DK * DV + col0 + c + lr;
+  auto init_dS = [&]() {
 #pragma unroll
-  for (int t = 0; t < DK / 16; ++t)
+    for (int t = 0; t < DK / 16; ++t)
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-      dS[t][v] = p.dht ? p.dht[st_off + (size_t)(16 * t + 4 * lq + v) * DV] : 0.f;
+      for (int v = 0; v < 4; ++v)
+        dS[t][v] = p.dht ? p.dht[st_off + (size_t)(16 * t + 4 * lq + v) * DV] : 0.f;
+  };
+  // gradient of the initial state
+  auto write_dh0 = [&]() {
+    if (p.dh0) {
+#pragma unroll
+      for (int t = 0; t < DK / 16; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) p.dh0[st_off + (size_t)(16 * t + 4 * lq + v) * DV] = dS[t][v];
+    }
+  };
 
-  // Per-thread register prefetch of a chunk's inputs: K and Q rows, the chunk's dO
-  // columns, X and P, and one gate value; stored into LDS at the top of the chunk.  Two
-  // register sets, loaded two chunks ahead: a chunk's rows have two chunk steps to land
-  // (with one the staging waited for them), and the kernel, one wavefront per SIMD, has
-  // the registers.
+  // Per-thread register copy of a chunk's inputs: K and Q rows, the chunk's dO columns,
+  // X and P, and one gate value, loaded by the NT staging threads (the loaders, or with
+  // fp32 inputs the compute wavefronts, two register sets deep) and stored into LDS a
+  // chunk step later.
   constexpr int NKQ = 2 * C * (DK / 4) / NT;
   static_assert(NKQ * NT == 2 * C * (DK / 4), "item split");
   struct Pf {
@@ -386,7 +412,6 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
     float4 pdo[C * 16 / NT], pxp[(PREC ? 1 : 2) * C * 16 / NT];
     float pgate, pg;
   };
-  Pf pfa, pfb;
   // chunk jj into f; every call issues the same loads (a chunk before the sequence's first
   // reloads chunk 0, unused), so the loop's waits stay exact counts
   auto load_chunk = [&](int jj, Pf& f) {
@@ -404,72 +429,69 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
 #pragma unroll
     for (int m = 0; m < NKQ; ++m) {
       const int which = m * NT / (C * DK / 4);  // uniform: K items, then Q items
-      const int rem = tid + m * NT - which * (C * DK / 4);
+      const int rem = st + m * NT - which * (C * DK / 4);
       const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
       const long long ld = which ? p.qs_ld : p.ks_ld;
       f.pkq[m] = bload4(which ? qr : kr, (unsigned)((row * ld + c4) * (long long)sizeof(KT)), (const KT*)nullptr);
     }
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
-      const int it = tid + m * NT;
+      const int it = st + m * NT;
       const int row = it >> 4, c4 = 4 * (it & 15);
       f.pdo[m] = bload4(dr, (unsigned)(4 * (row * rs + c4)), (const float*)nullptr);
     }
     const float* xb = p.xlpg + ((size_t)sl * p.Hv + h) * kXlpgFloats;
 #pragma unroll
     for (int m = 0; m < (PREC ? 1 : 2) * C * 16 / NT; ++m) {
-      const int it = tid + m * NT;
+      const int it = st + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
       f.pxp[m] = load4(xb + (which ? kXlpgP : kXlpgX) + (rem >> 4) * C + 4 * (rem & 15));
     }
-    if constexpr (PREC) f.pg = xb[kXlpgG + (tid & (C - 1))];
-    f.pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[tid];
+    if constexpr (PREC) f.pg = xb[kXlpgG + (st & (C - 1))];
+    f.pgate = ((const float*)(p.rec + ((size_t)sl * p.Hv + h) * rec_stride + kRecG))[st];
   };
-  auto store_chunk = [&](const Pf& f) {
+  auto store_chunk = [&](const Pf& f, const Buf& bf) {
+    bf16_t* const sDOh = bf.DO;
+    bf16_t* const sDOl = bf.DO + C * LDB;
+    bf16_t* const sXh = bf.X;
+    bf16_t* const sXl = bf.X + C * LDB;
 #pragma unroll
     for (int m = 0; m < NKQ; ++m) {
-      const int it = tid + m * NT;
+      const int it = st + m * NT;
       const int which = it / (C * DK / 4), rem = it % (C * DK / 4);
       const int row = rem / (DK / 4), c4 = 4 * (rem % (DK / 4));
-      store4((which ? sQ : sK) + row * LDK + c4, f.pkq[m]);
+      store4((which ? bf.Q : bf.K) + row * LDK + c4, f.pkq[m]);
     }
 #pragma unroll
     for (int m = 0; m < C * 16 / NT; ++m) {
-      const int it = tid + m * NT;
+      const int it = st + m * NT;
       put_row4(sDOh, sDOl, (it >> 4) * LDB + 4 * (it & 15), f32x4{f.pdo[m].x, f.pdo[m].y, f.pdo[m].z, f.pdo[m].w});
     }
 #pragma unroll
     for (int m = 0; m < (PREC ? 1 : 2) * C * 16 / NT; ++m) {
-      const int it = tid + m * NT;
+      const int it = st + m * NT;
       const int which = it / (C * 16), rem = it % (C * 16);
       const f32x4 v = f32x4{f.pxp[m].x, f.pxp[m].y, f.pxp[m].z, f.pxp[m].w};
       if (which) put_row4(sPh, sPl, (rem >> 4) * LDB + 4 * (rem & 15), v);
       else put_row4(sXh, sXl, (rem >> 4) * LDB + 4 * (rem & 15), v);
     }
     if constexpr (PREC)
-      if (tid < C) sGl[tid] = f.pg;
-    sGate[tid] = f.pgate;
+      if (st < C) bf.Gl[st] = f.pg;
+    bf.Gate[st] = f.pgate;
   };
-  if (nchunks > 0) {
-    load_chunk(nchunks - 1, pfa);
-    load_chunk(nchunks - 2, pfb);
-  }
-  // the prologue's loads (some under the uniform p.dht test) have landed: the loop's waits
-  // then count only the loop's own memory operations
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-
-  // chunk j from the registers of cur, which then receive chunk jn
-  auto step = [&](const int j, Pf& cur, const int jn) {
+  // chunk j on the compute wavefronts, from the rows staged in bf
+  auto compute = [&](const int j, const Buf& bf) {
     const long long t0 = s0 + (long long)j * C;
     const int nvalid = (int)((s1 - t0) < C ? (s1 - t0) : C);
     const int slot = cbase + j < p.n_rec ? cbase + j : p.n_rec - 1;
-    // Barriers here order LDS accesses only (lds_barrier): the global stores go to later
-    // kernels and the prefetched rows are per-thread registers, so neither the prefetch
-    // nor the stores are waited for at a barrier.
-    lds_barrier();  // the previous chunk's readers are done
-    store_chunk(cur);
-    load_chunk(jn, cur);  // lands during this chunk and the next
-    lds_barrier();
+    const KT* const sK = bf.K;
+    const KT* const sQ = bf.Q;
+    const bf16_t* const sDOh = bf.DO;
+    const bf16_t* const sDOl = bf.DO + C * LDB;
+    const bf16_t* const sXh = bf.X;
+    const bf16_t* const sXl = bf.X + C * LDB;
+    const float* const sGl = bf.Gl;
+    const float* const sGate = bf.Gate;
     const float* sEG = sGate + kGateEG * C;
     const float* sEGS = sGate + kGateEGS * C;
     const float* sEL = sGate + kGateEL * C;  // e^{G_last - G}; e^{G_last} in the last slot
@@ -599,19 +621,76 @@ __global__ __launch_bounds__(NT) void rscan_kernel(BwdParams p) {
       dS[t] = acc;
     }
   };
-  // chunks n-1, n-3, ... from pfa and n-2, n-4, ... from pfb, each set reloaded with the
-  // chunk two below the one it held
-  int j = nchunks - 1;
-  for (; j >= 1; j -= 2) {
-    step(j, pfa, j - 2);
-    step(j - 1, pfb, j - 3);
-  }
-  if (j == 0) step(0, pfa, -2);
-  if (p.dh0) {
-#pragma unroll
-    for (int t = 0; t < DK / 16; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) p.dh0[st_off + (size_t)(16 * t + 4 * lq + v) * DV] = dS[t][v];
+  // Barriers here order LDS accesses only (lds_barrier): the global stores go to later
+  // kernels and the staged rows come from per-thread registers, so neither the loads nor
+  // the stores are waited for at a barrier.
+  if constexpr (LDR) {
+    // Chunk j is computed from one buffer while the loaders store chunk j - 1, loaded
+    // during the step before, into the other and load chunk j - 2 (a chunk below the
+    // sequence's first reloads chunk 0, unused): the barrier that opens a step finds the
+    // next buffer filled and the previous one read.  The two roles run separate loops
+    // with one barrier per step each, so neither holds the other's registers.
+    int j = nchunks - 1;
+    if (loader) {
+      Pf f;
+      if (nchunks > 0) {
+        load_chunk(nchunks - 1, f);
+        store_chunk(f, B0);
+        load_chunk(nchunks - 2, f);
+      }
+      auto lstep = [&](const int jj, const Buf& nxt) {
+        lds_barrier();
+        store_chunk(f, nxt);
+        load_chunk(jj - 2, f);
+      };
+      for (; j >= 1; j -= 2) {
+        lstep(j, B1);
+        lstep(j - 1, B0);
+      }
+      if (j == 0) lstep(0, B1);
+    } else {
+      init_dS();
+      // the prologue's loads under the uniform p.dht test have landed
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      auto cstep = [&](const int jj, const Buf& cur) {
+        lds_barrier();
+        compute(jj, cur);
+      };
+      for (; j >= 1; j -= 2) {
+        cstep(j, B0);
+        cstep(j - 1, B1);
+      }
+      if (j == 0) cstep(0, B0);
+      write_dh0();
+    }
+  } else {
+    init_dS();
+    Pf pfa, pfb;
+    if (nchunks > 0) {
+      load_chunk(nchunks - 1, pfa);
+      load_chunk(nchunks - 2, pfb);
+    }
+    // the prologue's loads (some under the uniform p.dht test) have landed: the loop's
+    // waits then count only the loop's own memory operations
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // chunk j from the registers of cur, which then receive chunk jn (lands during this
+    // chunk and the next)
+    auto step = [&](const int jj, Pf& cur, const int jn) {
+      lds_barrier();  // the previous chunk's readers are done
+      store_chunk(cur, B0);
+      load_chunk(jn, cur);
+      lds_barrier();
+      compute(jj, B0);
+    };
+    // chunks n-1, n-3, ... from pfa and n-2, n-4, ... from pfb, each set reloaded with the
+    // chunk two below the one it held
+    int j = nchunks - 1;
+    for (; j >= 1; j -= 2) {
+      step(j, pfa, j - 2);
+      step(j - 1, pfb, j - 3);
+    }
+    if (j == 0) step(0, pfa, -2);
+    write_dh0();
   }
 }
 
@@ -1205,7 +1284,7 @@ __global__ __launch_bounds__(NT) void qk_final_kernel(BwdParams p, long long row
 
 template <int DK, bool F32>
 hipError_t launch_bwd_dk(const BwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((rscan_kernel<DK, F32>), dim3((unsigned)(p.N * p.Hv * p.nb)), dim3(NT), 0,
+  hipLaunchKernelGGL((rscan_kernel<DK, F32>), dim3((unsigned)(p.N * p.Hv * p.nb)), dim3(F32 ? NT : 2 * NT), 0,
                      stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
