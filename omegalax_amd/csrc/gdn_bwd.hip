@@ -330,6 +330,9 @@ __device__ __forceinline__ void op_values(const Op& o, float* x) {
 
 // ============================================================================ reverse scan
 
+// index of the lower-triangular 16x16 tile (mb, nb), mb >= nb, of a 64x64 chunk matrix
+__device__ __forceinline__ constexpr int ptile_index(int mb, int nb) { return mb * (mb + 1) / 2 + nb; }
+
 // With bf16 inputs (LDR) four loader wavefronts beside the four compute wavefronts move
 // each chunk's rows into one of two LDS buffers while the compute wavefronts work on the
 // other, with one barrier per chunk; the compute wavefronts then issue no loads at all.
@@ -351,6 +354,9 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
   __shared__ __align__(16) bf16_t sDO0[2 * C * LDB], sDO1[LDR ? 2 * C * LDB : 8];
   __shared__ __align__(16) bf16_t sX0[2 * C * LDB], sX1[LDR ? 2 * C * LDB : 8];
   __shared__ __align__(16) bf16_t sP[PREC ? 8 : 2 * C * LDB];
+  // (LDR) the chunk's ten lower-triangular 16x16 tiles of P, formed once by the loaders:
+  // lane l of tile t holds its C-layout values as bf16 hi (2 words) then lo (2 words)
+  __shared__ __align__(16) u32x4 sPT[LDR ? 10 : 1][64];
   __shared__ float sGl0[PREC ? C : 1], sGl1[LDR ? C : 1];
   __shared__ __align__(16) float sGate0[4 * C], sGate1[LDR ? 4 * C : 4];
   struct Buf {
@@ -479,6 +485,35 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
       if (st < C) bf.Gl[st] = f.pg;
     bf.Gate[st] = f.pgate;
   };
+  // (LDR) tile (mb, nb) of P = lower(scale Q K^T * Gamma) in the C layout, from the rows
+  // staged in bf, with the preparation kernel's arithmetic:
+  // scale * acc * 2^{min(G_m log2 e - G_n log2 e, 0)} * mask
+  auto form_ptile = [&](int mb, int nb, const Buf& bf) {
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int s2 = 0; s2 < DK / 32; ++s2)
+      acc = mma16(frag_bf16((const bf16_t*)bf.Q, LDK, 16 * mb, 32 * s2),
+                  frag_bf16((const bf16_t*)bf.K, LDK, 16 * nb, 32 * s2), acc);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = 16 * mb + 4 * lq + v, n = 16 * nb + lr;
+      acc[v] = p.scale * acc[v] *
+               __builtin_amdgcn_exp2f(fminf(bf.Gl[m] * 1.4426950408889634f - bf.Gl[n] * 1.4426950408889634f, 0.f)) *
+               (float)(m >= n);
+    }
+    return acc;
+  };
+  // (LDR) the ten tiles, dealt over the four loaders (t = lw, lw + 4, lw + 8), into sPT
+  auto form_ptiles = [&](const Buf& bf) {
+    const int lw = wave - NT / 64;
+    for (int t = lw; t < 10; t += 4) {  // uniform per wavefront
+      const int mb = t < 1 ? 0 : t < 3 ? 1 : t < 6 ? 2 : 3;
+      const int nb = t - mb * (mb + 1) / 2;
+      const f32x4 x = form_ptile(mb, nb, bf);
+      const u32x2 hi = pack_hi4(x), lo = pack_lo4(x);
+      sPT[t][l] = u32x4{hi[0], hi[1], lo[0], lo[1]};
+    }
+  };
   // chunk j on the compute wavefronts, from the rows staged in bf
   auto compute = [&](const int j, const Buf& bf) {
     const long long t0 = s0 + (long long)j * C;
@@ -490,7 +525,6 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
     const bf16_t* const sDOl = bf.DO + C * LDB;
     const bf16_t* const sXh = bf.X;
     const bf16_t* const sXl = bf.X + C * LDB;
-    const float* const sGl = bf.Gl;
     const float* const sGate = bf.Gate;
     const float* sEG = sGate + kGateEG * C;
     const float* sEGS = sGate + kGateEGS * C;
@@ -519,26 +553,9 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
       }
       kds[i] = acc;
     }
+    // (LDR) the loaders' P tiles of this chunk are in sPT after this barrier
+    if constexpr (LDR) lds_barrier();
     // ---------------------------------------------------------------- dV_new = P^T dO + e^{G_last-G} K dS
-    // (PREC) tile (mb, nb) of P = lower(scale Q K^T * Gamma) in the C layout, with the
-    // preparation kernel's arithmetic: scale * acc * 2^{min(G_m log2 e - G_n log2 e, 0)} * mask
-    auto ptile = [&](int mb, int nb) {
-      f32x4 acc = zero4();
-      if constexpr (PREC) {
-#pragma unroll
-        for (int s2 = 0; s2 < DK / 32; ++s2)
-          acc = mma16(frag_bf16((const bf16_t*)sQ, LDK, 16 * mb, 32 * s2),
-                      frag_bf16((const bf16_t*)sK, LDK, 16 * nb, 32 * s2), acc);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = 16 * mb + 4 * lq + v, n = 16 * nb + lr;
-          acc[v] = p.scale * acc[v] *
-                   __builtin_amdgcn_exp2f(fminf(sGl[m] * 1.4426950408889634f - sGl[n] * 1.4426950408889634f, 0.f)) *
-                   (float)(m >= n);
-        }
-      }
-      return acc;
-    };
     f32x4 dvn[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -549,9 +566,12 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
           // P^T rows 16i .. +15 over tokens 32 p2 .. +31 from the P tiles (2 p2, i) and
           // (2 p2 + 1, i) side by side (block-pair order; (2 p2, i) is above the diagonal,
           // zero, when 2 p2 < i), against dO read in the same order
-          const f32x4 t0 = 2 * p2 >= i ? ptile(2 * p2, i) : zero4();
-          acc = mm3<true, true>(acc, join_op(t0, ptile(2 * p2 + 1, i)),
-                                op_tr_pair(sDOh, sDOl, LDB, c, 32 * p2));
+          const u32x4 tb = sPT[ptile_index(2 * p2 + 1, i)][l];
+          const u32x4 ta = 2 * p2 >= i ? sPT[ptile_index(2 * p2, i)][l] : u32x4{0u, 0u, 0u, 0u};
+          Op pt;
+          pt.h = u32x4{ta[0], ta[1], tb[0], tb[1]};
+          pt.l = u32x4{ta[2], ta[3], tb[2], tb[3]};
+          acc = mm3<true, true>(acc, pt, op_tr_pair(sDOh, sDOl, LDB, c, 32 * p2));
         } else {
           acc = mm3<true, true>(acc, op_tr(sPh, sPl, LDB, 16 * i, 32 * p2),
                                 op_tr(sDOh, sDOl, LDB, c, 32 * p2));
@@ -638,16 +658,20 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
         store_chunk(f, B0);
         load_chunk(nchunks - 2, f);
       }
-      auto lstep = [&](const int jj, const Buf& nxt) {
+      // the P tiles of the chunk the compute wavefronts work on, published by the
+      // step's second barrier, then the next chunk's rows
+      auto lstep = [&](const Buf& cur, const Buf& nxt, const int jj) {
+        lds_barrier();
+        form_ptiles(cur);
         lds_barrier();
         store_chunk(f, nxt);
         load_chunk(jj - 2, f);
       };
       for (; j >= 1; j -= 2) {
-        lstep(j, B1);
-        lstep(j - 1, B0);
+        lstep(B0, B1, j);
+        lstep(B1, B0, j - 1);
       }
-      if (j == 0) lstep(0, B1);
+      if (j == 0) lstep(B0, B1, 0);
     } else {
       init_dS();
       // the prologue's loads under the uniform p.dht test have landed
