@@ -335,9 +335,11 @@ __device__ __forceinline__ constexpr int ptile_index(int mb, int nb) { return mb
 
 // With bf16 inputs (LDR) four loader wavefronts beside the four compute wavefronts move
 // each chunk's rows into one of two LDS buffers while the compute wavefronts work on the
-// other, with one barrier per chunk; the compute wavefronts then issue no loads at all.
-// fp32 K and Q rows leave no room for a second buffer, so with fp32 inputs the compute
-// wavefronts stage the rows themselves from a register prefetch two chunks deep.
+// other, and form the chunk's P tiles once for all of them; the compute wavefronts issue
+// no loads at all.  Two barriers per chunk: one opens the step (the chunk's rows are
+// staged, the other buffer is free), one publishes the P tiles.  fp32 K and Q rows leave
+// no room for a second buffer, so with fp32 inputs the compute wavefronts stage the rows
+// themselves from a register prefetch two chunks deep.
 template <int DK, bool F32>
 __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
   using KT = typename std::conditional<F32, float, bf16_t>::type;
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool loader = LDR && wave >= NT / 64;  // (LDR) waves 4-7 stage rows only
+  const bool loader = LDR && wave >= NT / 64;  // (LDR) waves 4-7: rows and P tiles only
   const int st = loader ? tid - NT : tid;       // index among the threads that stage rows
   const ScanItem item = scan_item(p.seq_order, p.N, p.Hk, p.Hv, p.nb);
   const int blk = item.blk, h = item.h, n = item.n;
@@ -649,7 +651,7 @@ __global__ __launch_bounds__(F32 ? NT : 2 * NT) void rscan_kernel(BwdParams p) {
     // during the step before, into the other and load chunk j - 2 (a chunk below the
     // sequence's first reloads chunk 0, unused): the barrier that opens a step finds the
     // next buffer filled and the previous one read.  The two roles run separate loops
-    // with one barrier per step each, so neither holds the other's registers.
+    // with the same two barriers per step, so neither holds the other's registers.
     int j = nchunks - 1;
     if (loader) {
       Pf f;
