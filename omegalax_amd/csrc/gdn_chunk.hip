@@ -84,7 +84,12 @@ struct Cfg {
   static constexpr int NH = VCONV ? 2 : 0;
   // with direct loads one more wavefront issues them (and NH more form V); sharing SIMDs
   // with the compute wavefronts, each may then hold at most half the register file
-  static constexpr int NTH = DIRECT ? NT + 64 * (1 + NH) : NT;
+  // loader wavefronts: two in the backward's bf16 recompute (the next chunk's K/Q rows in
+  // one's registers, its V rows and record in the other's, so that the loads are not
+  // queued behind the state stores of the same step), one elsewhere.  In the forward scan
+  // the second loader measured slower (C1 core call 0.311-0.319 against 0.292-0.297 ms).
+  static constexpr int NL = DIRECT ? (MODE == MODE_BF16 && BWD_ ? 2 : 1) : 0;
+  static constexpr int NTH = DIRECT ? NT + 64 * (NL + NH) : NT;
   static constexpr int WPE = (NTH / 64 + 3) / 4;
   static constexpr int NBUF = DIRECT ? 2 : 1;
   static constexpr int SZK = DIRECT ? C * DK : NS * C * LDK;  // elements of a K or Q buffer
@@ -302,6 +307,88 @@ __device__ __forceinline__ void stage_all(const ChunkParams& p, long long t0, in
   }
 }
 
+// Register staging of the bf16 path's two loaders (stage_all's addresses: lane l of
+// piece mi holds the 16 bytes stage_all's instruction mi puts at the buffer offset +
+// 16 l).  A chunk's pieces are loaded two chunk steps before the step that reads them and
+// stored into their LDS buffer one step before it, so its loads have about two steps to
+// land; split over two wavefronts, neither holds more than 132 VGPRs of rows.
+struct KQRegs {
+  u32x4 k[16], q[16];
+};
+template <int DK>
+__device__ __forceinline__ void stage_kq(const ChunkParams& p, long long t0, int nvalid, int hk, KQRegs& r) {
+  const int l = lane_id();
+  const bf16_t* kb = (const bf16_t*)p.ks + t0 * p.ks_ld + (long long)hk * DK;
+  const bf16_t* qb = (const bf16_t*)p.qs + t0 * p.qs_ld + (long long)hk * DK;
+  const unsigned kld = (unsigned)p.ks_ld, qld = (unsigned)p.qs_ld;
+  // rows past the sequence end repeat the last valid row, as in stage_all
+#pragma unroll
+  for (int mi = 0; mi < 16; ++mi) {
+    const int row = 4 * mi + (l >> 4);
+    const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
+    const unsigned g = (unsigned)((l & 15) ^ swz_k(row & 15));
+    r.k[mi] = *(const u32x4*)at_bytes(kb, 2u * (rr * kld + 8u * g));
+    r.q[mi] = *(const u32x4*)at_bytes(qb, 2u * (rr * qld + 8u * g));
+  }
+}
+__device__ __forceinline__ void put_kq(const KQRegs& r, lds_bf16* sK, lds_bf16* sQ) {
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  const int l = lane_id();
+#pragma unroll
+  for (int mi = 0; mi < 16; ++mi) {
+    *(lds_u32x4*)(sK + 512 * mi + 8 * l) = r.k[mi];
+    *(lds_u32x4*)(sQ + 512 * mi + 8 * l) = r.q[mi];
+  }
+}
+template <int MODE, int BV, bool BWD>
+struct VRRegs {
+  static constexpr int NV = BV / 8, NR = rec_bytes(MODE) / 1024, NRX = rec_bytes(MODE, BWD) / 1024;
+  u32x4 v[NV], r[NRX];
+};
+template <int MODE, int BV, bool BWD>
+__device__ __forceinline__ void stage_vr(const ChunkParams& p, long long t0, int nvalid,
+                                         const unsigned char* rec, int h, int col0,
+                                         VRRegs<MODE, BV, BWD>& r) {
+  using R_ = VRRegs<MODE, BV, BWD>;
+  constexpr int SV = BV / 8, RPI = 64 / SV;
+  const int l = lane_id();
+  const bf16_t* vb = (const bf16_t*)p.vs + t0 * p.vs_ld + (long long)h * p.DV + col0;
+  const unsigned vld = (unsigned)p.vs_ld;
+#pragma unroll
+  for (int mi = 0; mi < SV; ++mi) {
+    const int row = RPI * mi + l / SV;
+    const unsigned rr = (unsigned)(row < nvalid ? row : nvalid - 1);
+    const unsigned g = (unsigned)((l % SV) ^ swz_v<SV>(row));
+    r.v[mi] = *(const u32x4*)at_bytes(vb, 2u * (rr * vld + 8u * g));
+  }
+#pragma unroll
+  for (int mi = 0; mi < R_::NR; ++mi) r.r[mi] = *(const u32x4*)(rec + 1024 * mi + 16 * l);
+  // (backward) P's lo parts, read where o is formed
+  if constexpr (R_::NRX > R_::NR) {
+    if (p.o) {
+#pragma unroll
+      for (int mi = R_::NR; mi < R_::NRX; ++mi) r.r[mi] = *(const u32x4*)(rec + 1024 * mi + 16 * l);
+    }
+  }
+}
+template <int MODE, int BV, bool BWD>
+__device__ __forceinline__ void put_vr(const ChunkParams& p, const VRRegs<MODE, BV, BWD>& r, lds_bf16* sV,
+                                       lds_u8* sRec) {
+  using R_ = VRRegs<MODE, BV, BWD>;
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  const int l = lane_id();
+#pragma unroll
+  for (int mi = 0; mi < R_::NV; ++mi) *(lds_u32x4*)(sV + 512 * mi + 8 * l) = r.v[mi];
+#pragma unroll
+  for (int mi = 0; mi < R_::NR; ++mi) *(lds_u32x4*)(sRec + 1024 * mi + 16 * l) = r.r[mi];
+  if constexpr (R_::NRX > R_::NR) {
+    if (p.o) {
+#pragma unroll
+      for (int mi = R_::NR; mi < R_::NRX; ++mi) *(lds_u32x4*)(sRec + 1024 * mi + 16 * l) = r.r[mi];
+    }
+  }
+}
+
 // BWD (the backward pass's recompute): stores the state entering every chunk and V_new,
 // and o only when p.o is set.
 //
@@ -322,7 +409,7 @@ template <int DK, int MODE, bool BWD = false, int NWC_ = 4, bool FUSE = false>
 // One workgroup per CU is the design point (the state fills the register file): the
 // compiler may use the whole file (half of it with a loader wavefront, which shares a
 // SIMD) instead of holding back for a second workgroup.
-__global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE, NWC_>::WPE, Cfg<DK, MODE, NWC_>::WPE))) void scan_kernel(ChunkParams p) {
+__global__ __launch_bounds__((Cfg<DK, MODE, NWC_, BWD>::NTH)) __attribute__((amdgpu_waves_per_eu(Cfg<DK, MODE, NWC_, BWD>::WPE, Cfg<DK, MODE, NWC_, BWD>::WPE))) void scan_kernel(ChunkParams p) {
   using Q_ = Cfg<DK, MODE, NWC_, BWD>;
   constexpr int NWC = Q_::NWC, BV = Q_::BV, NT = Q_::NT;
   constexpr int LDK = Q_::LDK, SEGS = Q_::SEGS;
@@ -355,8 +442,8 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
 
   const int tid = threadIdx.x, l = tid & 63, lq = l >> 4, lr = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const bool loader = DIRECT && wave == NWC;  // issues the direct loads, computes nothing
-  const bool helper = Q_::VCONV && wave > NWC;  // forms the V rows (layer, direct loads)
+  const bool loader = DIRECT && wave >= NWC && wave < NWC + Q_::NL;  // loads, computes nothing
+  const bool helper = Q_::VCONV && wave >= NWC + Q_::NL;  // forms the V rows (layer, direct loads)
   const bool compute = wave < NWC;             // owns 16 state columns
   // XCD-aware work item (scan_item): a key head's workgroups share one XCD's L2, and
   // packed sequences start longest first
@@ -405,7 +492,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   if (nchunks > 0) {
     const int nv0 = (int)((s1 - s0) < C ? (s1 - s0) : C);
     if constexpr (DIRECT) {
-      if (loader) {
+      if (loader && wave == NWC) {
         stage_all<DK, MODE, BV, BWD>(p, s0, nv0, rec_of(0), hk, h, col0, (lds_bf16*)sK0, (lds_bf16*)sQ0,
                             (lds_bf16*)sV0, (lds_u8*)sRec0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): landed before the first barrier
@@ -861,7 +948,57 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
   };
 
   if constexpr (DIRECT) {
-    if (loader) {
+    if (loader && Q_::NL == 2) {
+      if constexpr (Q_::NL == 2) {
+        // one barrier per chunk, as the compute wavefronts: after the barrier at the top of
+        // chunk j, buffer (j + 1) % 2 is free and receives chunk j + 1 from the registers,
+        // which then receive chunk j + 2.  The two loaders run separate loops, so neither
+        // holds the other's rows.
+        auto rows = [&](int c, long long& tc) {
+          tc = s0 + (long long)c * C;
+          return (int)((s1 - tc) < C ? (s1 - tc) : C);
+        };
+        if (wave == NWC) {  // the K and Q rows
+          KQRegs r;
+          long long tc;
+          if (nchunks > 1) {
+            const int nvc = rows(1, tc);
+            stage_kq<DK>(p, tc, nvc, hk, r);
+          }
+          auto step = [&](int j, lds_bf16* nK, lds_bf16* nQ) {
+            lds_barrier();
+            if (j + 1 < nchunks) put_kq(r, nK, nQ);
+            if (j + 2 < nchunks) {
+              const int nvc = rows(j + 2, tc);
+              stage_kq<DK>(p, tc, nvc, hk, r);
+            }
+          };
+          for (int j = 0; j < nchunks; j += 2) {
+            step(j, (lds_bf16*)sK1, (lds_bf16*)sQ1);
+            if (j + 1 < nchunks) step(j + 1, (lds_bf16*)sK0, (lds_bf16*)sQ0);
+          }
+        } else {  // the V rows and the record
+          VRRegs<MODE, BV, BWD> r;
+          long long tc;
+          if (nchunks > 1) {
+            const int nvc = rows(1, tc);
+            stage_vr<MODE, BV, BWD>(p, tc, nvc, rec_of(1), h, col0, r);
+          }
+          auto step = [&](int j, lds_bf16* nV, lds_u8* nRec) {
+            lds_barrier();
+            if (j + 1 < nchunks) put_vr<MODE, BV, BWD>(p, r, nV, nRec);
+            if (j + 2 < nchunks) {
+              const int nvc = rows(j + 2, tc);
+              stage_vr<MODE, BV, BWD>(p, tc, nvc, rec_of(j + 2), h, col0, r);
+            }
+          };
+          for (int j = 0; j < nchunks; j += 2) {
+            step(j, (lds_bf16*)sV1, (lds_u8*)sRec1);
+            if (j + 1 < nchunks) step(j + 1, (lds_bf16*)sV0, (lds_u8*)sRec0);
+          }
+        }
+      }
+    } else if (loader) {
       // one barrier per chunk, as the compute wavefronts: after the barrier at the top of
       // chunk j, buffer (j + 1) % 2 is free and receives chunk j + 1
       // (layer) lane l's row of chunk jj: the workgroup's partial, one per row, stored
@@ -993,7 +1130,7 @@ __global__ __launch_bounds__((Cfg<DK, MODE, NWC_>::NTH)) __attribute__((amdgpu_w
         // are loaded one chunk step ahead (two register sets; loads past the last chunk
         // repeat it), so their latency is off the step.
         constexpr int SV = BV / 8, R = BV / 16;
-        const int hl = tid - 64 * (NWC + 1);
+        const int hl = tid - 64 * (NWC + Q_::NL);
         const int g = hl % SV, r0 = (hl / SV) * R;
         const int chu = 2 * p.Hk * DK + h * DV + col0;
         uint32_t wp[8][2];
