@@ -340,6 +340,7 @@ __device__ __forceinline__ void put_kq(const KQRegs& r, lds_bf16* sK, lds_bf16* 
     *(lds_u32x4*)(sQ + 512 * mi + 8 * l) = r.q[mi];
   }
 }
+static_assert(kRecP % 1024 == 0 && kRecG % 1024 == 0, "P fills whole 1 KiB record pieces");
 template <int MODE, int BV, bool BWD>
 struct VRRegs {
   static constexpr int NV = BV / 8, NR = rec_bytes(MODE) / 1024, NRX = rec_bytes(MODE, BWD) / 1024;
@@ -361,8 +362,11 @@ __device__ __forceinline__ void stage_vr(const ChunkParams& p, long long t0, int
     const unsigned g = (unsigned)((l % SV) ^ swz_v<SV>(row));
     r.v[mi] = *(const u32x4*)at_bytes(vb, 2u * (rr * vld + 8u * g));
   }
+  // P (hi parts) only where o is formed: the prep leaves it out of a recompute without o
+  const bool with_p = !BWD || p.o;
 #pragma unroll
-  for (int mi = 0; mi < R_::NR; ++mi) r.r[mi] = *(const u32x4*)(rec + 1024 * mi + 16 * l);
+  for (int mi = 0; mi < R_::NR; ++mi)
+    if (with_p || mi < kRecP / 1024 || mi >= kRecG / 1024) r.r[mi] = *(const u32x4*)(rec + 1024 * mi + 16 * l);
   // (backward) P's lo parts, read where o is formed
   if constexpr (R_::NRX > R_::NR) {
     if (p.o) {
@@ -379,8 +383,10 @@ __device__ __forceinline__ void put_vr(const ChunkParams& p, const VRRegs<MODE, 
   const int l = lane_id();
 #pragma unroll
   for (int mi = 0; mi < R_::NV; ++mi) *(lds_u32x4*)(sV + 512 * mi + 8 * l) = r.v[mi];
+  const bool with_p = !BWD || p.o;
 #pragma unroll
-  for (int mi = 0; mi < R_::NR; ++mi) *(lds_u32x4*)(sRec + 1024 * mi + 16 * l) = r.r[mi];
+  for (int mi = 0; mi < R_::NR; ++mi)
+    if (with_p || mi < kRecP / 1024 || mi >= kRecG / 1024) *(lds_u32x4*)(sRec + 1024 * mi + 16 * l) = r.r[mi];
   if constexpr (R_::NRX > R_::NR) {
     if (p.o) {
 #pragma unroll

@@ -587,7 +587,7 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
               const u32x2 z = {0u, 0u};
               put_tile(rec, rec_t_off(bi, bi + 1), z);
               put_tile(rec, rec_t_off(bi, bi + 1) + kPairBytes, z);
-              put_tile(rec, rec_p_off(bi, bi + 1), z);
+              if (!BWD || IS || p.o) put_tile(rec, rec_p_off(bi, bi + 1), z);
               if constexpr (IS || BWD)
                 if (IS || p.o) put_tile(rec, rec_p_off(bi, bi + 1) + (kRecPL - kRecP), z);
             }
@@ -603,7 +603,8 @@ __global__ __launch_bounds__(NT, (prep_blocks_per_cu<DK, MODE>())) void prep_ker
             const int m = 16 * bj + 4 * lq + v;
             val[v] = sc * acc[v] * __builtin_amdgcn_exp2f(fminf(Gi - Gm[v], 0.f)) * (float)(i >= m);
           }
-          put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
+          // (a backward recompute that forms no o reads no P: bf16 inputs leave it out)
+          if (!BWD || IS || p.o) put_tile(rec, rec_p_off(bi, bj), pack_hi4(val));
           // (bf16 inputs: the backward kernels form their P operands from K and Q)
           if constexpr (BWD && IS) put_f32_tile(xb + kXlpgP, bi, bj, val);
           // (backward) P's lo parts only where the scan forms o: the layer backward
