@@ -84,11 +84,14 @@ struct Cfg {
   static constexpr int NH = VCONV ? 2 : 0;
   // with direct loads one more wavefront issues them (and NH more form V); sharing SIMDs
   // with the compute wavefronts, each may then hold at most half the register file
-  // loader wavefronts: two in the backward's bf16 recompute (the next chunk's K/Q rows in
-  // one's registers, its V rows and record in the other's, so that the loads are not
-  // queued behind the state stores of the same step), one elsewhere.  In the forward scan
-  // the second loader measured slower (C1 core call 0.311-0.319 against 0.292-0.297 ms).
-  static constexpr int NL = DIRECT ? (MODE == MODE_BF16 && BWD_ ? 2 : 1) : 0;
+  // loader wavefronts: two in the backward's bf16 recompute (the chunk after next's K/Q
+  // rows in one's registers, its V rows and record in the other's, so that the loads are
+  // not queued behind the state stores of the same step) and in the bf16 forward scan's
+  // narrow workgroups (where the second loader takes a SIMD no compute wavefront uses:
+  // C4 2.663-2.666 -> 2.605-2.639 ms), one elsewhere.  In the forward scan's 64-column
+  // workgroups the second loader measured slower (C1 core call 0.311-0.319 against
+  // 0.292-0.297 ms).
+  static constexpr int NL = DIRECT ? (MODE == MODE_BF16 && (BWD_ || NWC_ < 4) ? 2 : 1) : 0;
   static constexpr int NTH = DIRECT ? NT + 64 * (NL + NH) : NT;
   static constexpr int WPE = (NTH / 64 + 3) / 4;
   static constexpr int NBUF = DIRECT ? 2 : 1;
