@@ -65,9 +65,10 @@ def test_decode_steps_match_oracle(B, Hk, Hv, dk, dv):
         assert np.array_equal(np_(t["conv_state"]), conv_ref), f"step {step} conv cache"
 
 
-@pytest.mark.parametrize("B", [1, 8, 64])
+@pytest.mark.parametrize("B", [1, 8, 64, 128])
 def test_decode_c2_full_size(B):
-    """Config C2 (Hk=16, Hv=32, d=128) at B = 1, 8 (the sweep's small batches) and 64:
+    """Config C2 (Hk=16, Hv=32, d=128) at B = 1, 8 (the sweep's small batches), 64 and 128
+    (2,048 items: the smallest batch whose grid is one workgroup per CU with 8 items each):
     S [B,32,128,128] fp32 against the fp64 oracle, every sequence."""
     from omegalax_amd import gdn_decode_step
     say(f"decode C2 B={B}")
